@@ -1,0 +1,238 @@
+"""ctypes front end for oracle/liboracle.so -- the CPU restatement of the
+reference's input generators and CPU references.
+
+TEST INFRASTRUCTURE ONLY.  Importable from tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg; the product package never imports it.  See
+oracle.cpp for the reference file:line each function restates and how each
+is pinned.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+F32, F16, BF16 = 0, 1, 2
+MODE_RANDOM, MODE_ALL_ONES, MODE_RAND_INT, MODE_HPL, MODE_HALVES = 0, 1, 2, 3, 4
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_SZ = ctypes.c_size_t
+
+
+def build() -> None:
+    """Compile liboracle.so (and oracle/_ref when the reference is present)."""
+    subprocess.run(["make", "-s", "-C", _HERE, "all"], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        sig = {
+            "oracle_rand_state": (ctypes.c_uint32, [_I, _I]),
+            "oracle_next_rand": (ctypes.c_uint32, [ctypes.POINTER(ctypes.c_uint32)]),
+            "oracle_bucket_value": (ctypes.c_float, [ctypes.POINTER(ctypes.c_uint32), ctypes.c_float]),
+            "oracle_rand_int": (ctypes.c_float, [_SZ]),
+            "oracle_hpl": (ctypes.c_float, [_SZ]),
+            "oracle_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
+            "oracle_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+            "oracle_f32_to_bf16": (ctypes.c_uint16, [ctypes.c_float]),
+            "oracle_bf16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+            "oracle_f64_to_f16": (ctypes.c_uint16, [ctypes.c_double]),
+            "oracle_gemm_inputs": (None, [_P, _I, _I, _I, _I, _I, _I]),
+            "oracle_gemm_nt": (None, [_P, _P, _P, _I, _I, _I, _I, _I]),
+            "oracle_gemm_nt_rows": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _I]),
+            "oracle_gemm_element": (ctypes.c_float, [_P, _P, _I, _I, _I64, _I64]),
+            "oracle_round_output": (None, [_P, _P, _SZ, _I]),
+            "oracle_fa_f32_inputs": (None, [_P, _P, _P, _I, _I, _I, _I]),
+            "oracle_fa_f32_reference": (None, [_P, _P, _P, _P, _I, _I, _I]),
+            "oracle_fa_gfx950_inputs": (None, [_P, _P, _P, _SZ, _I, _I, _I]),
+            "oracle_attention_rows": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
+                                             ctypes.c_double, _P, _P, _I, _P, _I]),
+            "oracle_fa_reference_rows": (_I, [_I, _P]),
+            "oracle_fa_reference_heads": (_I, [_I, _P]),
+            "oracle_streamk_worker_interval": (_I, [_I64, _I, _I, ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
+            "oracle_streamk_owner": (_I64, [_I64, _I, _I64]),
+            "oracle_streamk_segments": (_I, [_I, _I, _I, _I, _P, _P, _P, _P, _I]),
+            "oracle_hardware_threads": (_I, []),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def hardware_threads() -> int:
+    return lib().oracle_hardware_threads()
+
+
+# ---- generators --------------------------------------------------------
+def gemm_inputs(rows: int, k: int, dtype: int = F16, seed: int = 0, stream: int = 0,
+                mode: int = MODE_RANDOM) -> np.ndarray:
+    out = np.empty(rows * k, dtype=np.uint16)
+    lib().oracle_gemm_inputs(_ptr(out), rows, k, dtype, seed, stream, mode)
+    return out.reshape(rows, k)
+
+
+def f16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return np.asarray(bits, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def bits_to_f32(bits: np.ndarray, dtype: int) -> np.ndarray:
+    return bf16_bits_to_f32(bits) if dtype == BF16 else f16_bits_to_f32(bits)
+
+
+def round_output(c: np.ndarray, out_dtype: int) -> np.ndarray:
+    c = np.ascontiguousarray(c, dtype=np.float32)
+    if out_dtype == F32:
+        return c.copy()
+    out = np.empty(c.shape, dtype=np.uint16)
+    lib().oracle_round_output(_ptr(c), _ptr(out), c.size, out_dtype)
+    return out
+
+
+# ---- GEMM reference ------------------------------------------------------
+def gemm_nt(a: np.ndarray, b: np.ndarray, dtype: int = F16, threads: int | None = None) -> np.ndarray:
+    """C[M,N] = A[M,K] . B[N,K]^T, float accumulation in ascending k."""
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    m, k = a.shape
+    n, k2 = b.shape
+    assert k == k2
+    c = np.empty((m, n), dtype=np.float32)
+    lib().oracle_gemm_nt(_ptr(a), _ptr(b), _ptr(c), m, n, k, dtype,
+                         threads or hardware_threads())
+    return c
+
+
+def gemm_nt_rows(a: np.ndarray, b: np.ndarray, m0: int, m1: int, dtype: int = F16,
+                 threads: int | None = None) -> np.ndarray:
+    """Rows [m0, m1) of A . B^T (same arithmetic as gemm_nt)."""
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    m, k = a.shape
+    n = b.shape[0]
+    c = np.zeros((m, n), dtype=np.float32)
+    lib().oracle_gemm_nt_rows(_ptr(a), _ptr(b), _ptr(c), m0, m1, n, k, dtype,
+                              threads or hardware_threads())
+    return c[m0:m1]
+
+
+def gemm_elements(a: np.ndarray, b: np.ndarray, rows, cols, dtype: int = F16) -> np.ndarray:
+    """Sampled C[rows[i], cols[i]] with the runner's per-element arithmetic."""
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    k = a.shape[1]
+    L = lib()
+    return np.array([L.oracle_gemm_element(_ptr(a), _ptr(b), k, dtype, int(r), int(c))
+                     for r, c in zip(rows, cols)], dtype=np.float32)
+
+
+# ---- flash attention ----------------------------------------------------------
+def fa_f32_inputs(block_m: int, seq_n: int, head_dim: int, seed: int = 0):
+    q = np.empty(block_m * head_dim, dtype=np.uint16)
+    k = np.empty(seq_n * head_dim, dtype=np.uint16)
+    v = np.empty(seq_n * head_dim, dtype=np.uint16)
+    lib().oracle_fa_f32_inputs(_ptr(q), _ptr(k), _ptr(v), block_m, seq_n, head_dim, seed)
+    return q.reshape(block_m, head_dim), k.reshape(seq_n, head_dim), v.reshape(seq_n, head_dim)
+
+
+def fa_f32_reference(q, k, v) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    block_m, head_dim = q.shape
+    seq_n = k.shape[0]
+    out = np.empty((block_m, head_dim), dtype=np.float32)
+    lib().oracle_fa_f32_reference(_ptr(q), _ptr(k), _ptr(v), _ptr(out), block_m, seq_n, head_dim)
+    return out
+
+
+def fa_gfx950_inputs(elements: int, seed: int = 0, input_scale: int = 1, zero_qk: bool = False):
+    q = np.empty(elements, dtype=np.uint16)
+    k = np.empty(elements, dtype=np.uint16)
+    v = np.empty(elements, dtype=np.uint16)
+    lib().oracle_fa_gfx950_inputs(_ptr(q), _ptr(k), _ptr(v), elements, seed, input_scale,
+                                  int(zero_qk))
+    return q, k, v
+
+
+def attention_rows(q, k, v, *, dtype: int, batch: int, q_heads: int, kv_heads: int,
+                   seq_q: int, seq_k: int, head_dim: int, causal: bool, scale: float,
+                   heads, rows, threads: int | None = None) -> np.ndarray:
+    """Double-precision softmax(QK^T*scale)V for the (flat head, row) pairs."""
+    q = np.ascontiguousarray(q, dtype=np.uint16).ravel()
+    k = np.ascontiguousarray(k, dtype=np.uint16).ravel()
+    v = np.ascontiguousarray(v, dtype=np.uint16).ravel()
+    heads = np.ascontiguousarray(heads, dtype=np.int32)
+    rows = np.ascontiguousarray(rows, dtype=np.int32)
+    assert heads.shape == rows.shape
+    out = np.empty((len(rows), head_dim), dtype=np.float32)
+    lib().oracle_attention_rows(_ptr(q), _ptr(k), _ptr(v), dtype, batch, q_heads, kv_heads,
+                                seq_q, seq_k, head_dim, int(causal), float(scale),
+                                _ptr(heads), _ptr(rows), len(rows), _ptr(out),
+                                threads or hardware_threads())
+    return out
+
+
+def fa_reference_rows(sequence: int) -> list[int]:
+    buf = np.zeros(max(sequence, 8), dtype=np.int32)
+    n = lib().oracle_fa_reference_rows(sequence, _ptr(buf))
+    return buf[:n].tolist()
+
+
+def fa_reference_heads(head_count: int) -> list[int]:
+    buf = np.zeros(max(head_count, 4), dtype=np.int32)
+    n = lib().oracle_fa_reference_heads(head_count, _ptr(buf))
+    return buf[:n].tolist()
+
+
+# ---- Stream-K partition -------------------------------------------------------
+def streamk_worker_interval(total: int, workers: int, worker: int) -> tuple[int, int]:
+    b, e = _I64(), _I64()
+    if lib().oracle_streamk_worker_interval(total, workers, worker, ctypes.byref(b), ctypes.byref(e)):
+        raise ValueError("bad Stream-K interval arguments")
+    return b.value, e.value
+
+
+def streamk_owner_for_iteration(total: int, workers: int, iteration: int) -> int:
+    r = lib().oracle_streamk_owner(total, workers, iteration)
+    if r < 0:
+        raise ValueError("bad Stream-K owner arguments")
+    return r
+
+
+def streamk_worker_segments(tile_count: int, k_iterations: int, workers: int, worker: int):
+    cap = 64
+    t = np.zeros(cap, np.int32)
+    kb = np.zeros(cap, np.int32)
+    ke = np.zeros(cap, np.int32)
+    sl = np.zeros(cap, np.int32)
+    n = lib().oracle_streamk_segments(tile_count, k_iterations, workers, worker,
+                                      _ptr(t), _ptr(kb), _ptr(ke), _ptr(sl), cap)
+    if n < 0:
+        raise ValueError("bad Stream-K segment arguments")
+    return [(int(t[i]), int(kb[i]), int(ke[i]), None if sl[i] < 0 else int(sl[i]))
+            for i in range(n)]

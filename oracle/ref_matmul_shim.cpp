@@ -1,0 +1,92 @@
+// ref_matmul_shim.cpp -- builds the reference runner's CPU-side code, from the
+// reference checkout, into oracle/_ref/libref_matmul.so.
+//
+// TEST INFRASTRUCTURE ONLY (never shipped, never loaded by the product).  It
+// uses the reference's own trick (test/Integration/Inputs/
+// wave_matmul_rand_int_test.cpp:9-10): define WAVE_MATMUL_CALIBRATE_RUNNER_NO_MAIN
+// and include the runner source where it lies (path given by -include on the
+// compile line in oracle/Makefile), then export C entry points over the
+// runner's own functions so tests/golden/make_golden.py can record vectors.
+#include <cstdint>
+#include <cstring>
+
+extern "C" {
+
+void ref_make_input_bytes(int rows, int k, int type, int seed, int stream,
+                          int all_ones, int rand_int, int hpl, uint8_t *out) {
+  std::vector<uint8_t> b =
+      makeInputBytes(rows, k, type == 2 ? InputType::BF16 : InputType::F16,
+                     seed, stream, all_ones != 0, rand_int != 0, hpl != 0);
+  std::memcpy(out, b.data(), b.size());
+}
+
+float ref_half_to_float(uint16_t h) { return halfToFloat(h); }
+uint16_t ref_float_to_half_bits(float v) { return floatToHalfBits(v); }
+uint16_t ref_float_to_bf16_bits(float v) { return floatToBF16Bits(v); }
+float ref_random_input_value(uint32_t *state) { return randomInputValue(*state); }
+uint32_t ref_rand_state(int seed, int stream) { return randState(seed, stream); }
+float ref_hipblaslt_rand_int(size_t i) { return hipblasLtRandInt(i); }
+float ref_hipblaslt_hpl(size_t i) { return hipblasLtHpl(i); }
+
+// C[m][n] via computeExpectedElement (float accumulate) for the given mode,
+// then roundExpectedOutput for the requested output type (0 f32, 1 f16, 2 bf16).
+void ref_gemm_expected(int m, int n, int k, int type, int seed, int mode,
+                       int out_type, double *out) {
+  Args a;
+  a.m = m;
+  a.n = n;
+  a.k = k;
+  a.inputType = type == 2 ? InputType::BF16 : InputType::F16;
+  a.seed = seed;
+  a.allOnes = mode == 1;
+  a.randInt = mode == 2;
+  a.hpl = mode == 3;
+  a.cType = out_type == 1 ? CType::F16 : out_type == 2 ? CType::BF16 : CType::F32;
+  HostInputs in = makeHostInputs(a);
+  for (int i = 0; i < m; ++i)
+    for (int j = 0; j < n; ++j)
+      out[static_cast<size_t>(i) * n + j] =
+          roundExpectedOutput(computeExpectedElement(in, a, i, j), a.cType);
+}
+
+// getOutputCoordinate for a 16x16 single-wave tile (rand_int_test.cpp:112-141).
+void ref_output_coordinate(int wave_size, int wmma, int index, int *m, int *n) {
+  Args a;
+  a.m = 16;
+  a.n = 16;
+  a.bm = 1;
+  a.bn = 1;
+  a.waveMTiles = 1;
+  a.waveNTiles = 1;
+  a.waveSize = wave_size;
+  a.accumulatorLayout = wmma ? AccumulatorLayout::Wmma : AccumulatorLayout::Mfma;
+  OutputCoordinate c = getOutputCoordinate(a, index);
+  *m = c.m;
+  *n = c.n;
+}
+
+// getStreamKWorkspaceSizes + makeLaunchShape for the Stream-K ABI.
+void ref_streamk_workspace(int m, int n, int k, int workers, uint64_t *scratch,
+                           uint64_t *counters, int *grid_x, int *block) {
+  Args a;
+  a.m = m;
+  a.n = n;
+  a.k = k;
+  a.bm = 2;
+  a.bn = 2;
+  a.waveMTiles = 8;
+  a.waveNTiles = 8;
+  a.waveKTiles = 2;
+  a.waveSize = 64;
+  a.cType = CType::F16;
+  a.kernelABI = KernelABI::StreamK;
+  a.streamKWorkers = workers;
+  StreamKWorkspaceSizes s = getStreamKWorkspaceSizes(a);
+  *scratch = s.scratchBytes;
+  *counters = s.counterElements;
+  LaunchShape l = makeLaunchShape(a);
+  *grid_x = l.gridX;
+  *block = l.blockThreads;
+}
+
+} // extern "C"
