@@ -1,0 +1,18 @@
+"""wave-mi355x: MI355X-native (gfx950) drop-in for the reference's GEMM,
+Stream-K GEMM and flash-attention forward kernels.
+
+The package directory name starts with a digit, so import it with
+``importlib.import_module("7_amd")``.  The compute lives in
+``libwave_runtime.so`` (hand-written HIP, C ABI in include/wave_runtime.h);
+``ops`` wraps it for torch tensors and ``runtime`` is the ctypes binding.
+"""
+
+from . import runtime
+from .ops import (StreamKWorkspace, flash_attention, flash_attention_f32, gemm,
+                  gemm_streamk, streamk_workspace_bytes)
+from .runtime import WaveError
+
+__all__ = [
+    "runtime", "gemm", "gemm_streamk", "StreamKWorkspace", "streamk_workspace_bytes",
+    "flash_attention", "flash_attention_f32", "WaveError",
+]

@@ -1,0 +1,32 @@
+// attention.hpp -- host-side launch interface of the flash-attention kernels
+// (attention_fwd.hip: production forward, head_dim 128; fa_small.hip: the
+// single-workgroup flash_attention_f32 ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace wave {
+namespace attention {
+
+struct FwdArgs {
+  const void *Q = nullptr;  // [batch][q_heads][seq_q][head_dim]
+  const void *K = nullptr;  // [batch][kv_heads][seq_k][head_dim]
+  const void *V = nullptr;  // [batch][kv_heads][seq_k][head_dim]
+  void *O = nullptr;        // [batch][q_heads][seq_q][head_dim]
+  int batch = 1, q_heads = 1, kv_heads = 1, seq_q = 0, seq_k = 0;
+  int head_dim = 128;
+  int dtype = 1;            // wave::kF16 or wave::kBF16 (Q, K, V and O)
+  int causal = 0;           // mask key > query (top-left aligned)
+  float scale = 0.f;        // softmax scale; 0 selects 1/sqrt(head_dim)
+};
+
+hipError_t launch_fwd(const FwdArgs &args, hipStream_t stream);
+
+// flash_attention_f32 ABI: Q [block_m][head_dim] f16 already multiplied by
+// log2(e)/sqrt(head_dim), K/V [seq_n][head_dim] f16, O [block_m][head_dim]
+// f32 = sum_n 2^(s_n - max) V_n / sum_n 2^(s_n - max), s_n = Q.K_n.
+hipError_t launch_small(const void *Q, const void *K, const void *V, float *O,
+                        int block_m, int seq_n, int head_dim, hipStream_t stream);
+
+} // namespace attention
+} // namespace wave

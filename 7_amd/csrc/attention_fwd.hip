@@ -1,0 +1,37 @@
+// attention_fwd.hip -- instantiation and host launch of the gfx950
+// flash-attention forward kernel (attention_kernels.hpp).
+#include "attention_kernels.hpp"
+
+#include <cmath>
+
+namespace wave {
+namespace attention {
+
+constexpr int kWaves = 4;
+
+hipError_t launch_fwd(const FwdArgs &a, hipStream_t stream) {
+  Params p{};
+  p.Q = static_cast<const uint16_t *>(a.Q);
+  p.K = static_cast<const uint16_t *>(a.K);
+  p.V = static_cast<const uint16_t *>(a.V);
+  p.O = static_cast<uint16_t *>(a.O);
+  p.batch = a.batch;
+  p.q_heads = a.q_heads;
+  p.kv_heads = a.kv_heads;
+  p.seq_q = a.seq_q;
+  p.seq_k = a.seq_k;
+  p.q_blocks = (a.seq_q + 32 * kWaves - 1) / (32 * kWaves);
+  p.causal = a.causal;
+  const float scale = a.scale > 0.f ? a.scale : 1.0f / std::sqrt((float)a.head_dim);
+  p.scale_log2 = scale * kLog2e;
+  const dim3 grid(p.q_blocks * a.batch * a.q_heads);
+  const dim3 block(64 * kWaves);
+  if (a.dtype == kF16)
+    hipLaunchKernelGGL((fwd_kernel<kF16, kWaves>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((fwd_kernel<kBF16, kWaves>), grid, block, 0, stream, p);
+  return hipGetLastError();
+}
+
+} // namespace attention
+} // namespace wave

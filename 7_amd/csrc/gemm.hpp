@@ -1,0 +1,33 @@
+// gemm.hpp -- host-side launch interface of the tiled / Stream-K GEMM
+// kernels in gemm.hip (used by the C ABI in wave_runtime.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace wave {
+namespace gemm {
+
+struct GemmArgs {
+  const void *A = nullptr;  // [M x K] row-major, f16 or bf16
+  const void *B = nullptr;  // [N x K] row-major, same type as A
+  void *C = nullptr;        // [M x N] row-major or [N x M] (column-major)
+  int M = 0, N = 0, K = 0;
+  int in_dtype = 1;         // wave::kF16 / wave::kBF16
+  int out_dtype = 1;        // wave::kF32 / kF16 / kBF16
+  bool col_major = false;
+  int group_m = 0;          // tile-row group size; 0 = default (4)
+  void *scratch = nullptr;  // Stream-K fp32 partials (workers*2*256*256)
+  void *counters = nullptr; // Stream-K per-tile arrival counters (zeroed)
+  int workers = 0;          // > 0 selects the Stream-K kernel
+  bool force_masked = false;
+};
+
+constexpr int kTileEdge = 256;
+constexpr int kKStage = 64;
+
+int tiles_for(int extent);
+int k_iterations(int K);
+hipError_t launch(const GemmArgs &args, hipStream_t stream);
+
+} // namespace gemm
+} // namespace wave

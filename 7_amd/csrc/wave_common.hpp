@@ -1,0 +1,97 @@
+// wave_common.hpp -- shared CDNA4 (gfx950) device helpers for the GEMM and
+// flash-attention kernels: vector types, MFMA wrappers, LDS address helpers,
+// the asynchronous global->LDS DMA issue, and output conversions.
+//
+// Everything here is written for wave64 gfx950 only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wave {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Element type codes of the C ABI (include/wave_runtime.h).
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+// v_mfma_f32_32x32x16_{f16,bf16}: D[32x32] += A[32x16] * B[16x32].
+// Lane l supplies A[l%32][8*(l/32) .. +8] and B[8*(l/32) .. +8][l%32] as
+// eight packed 16-bit values; accumulator register r of lane l holds
+// D[8*(r/4) + 4*(l/32) + r%4][l%32].
+template <int DT>
+__device__ __forceinline__ f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (DT == kF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(
+        __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
+        0);
+}
+
+// 32-bit LDS byte address of a __shared__ object (address space 3).
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
+}
+
+// Direct global->LDS copy of 16 bytes per lane (global_load_lds_dwordx4).
+// Lane l's 16 bytes land at LDS byte lds + 16*l, so one call fills a
+// contiguous 1 KiB LDS window.  `lds` and `base` must be wave-uniform; the
+// per-lane source is base + voff.  Issued from inline asm so that the
+// compiler does not insert its own conservative vmcnt waits in front of the
+// LDS reads of the *other* buffer; callers synchronise explicitly with
+// vm_wait_barrier().  No memory clobber: the DMA only writes an LDS buffer
+// that no instruction between two barriers reads, so LDS reads of the
+// current buffer may be scheduled around it.  M0 is written here and nowhere
+// else in these kernels.
+__device__ __forceinline__ void dma16(uint32_t lds, const void *base,
+                                      uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\t"
+               "s_nop 0\n\t"
+               "global_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds), "v"(voff), "s"(base));
+}
+
+// Wait until this wave's outstanding vector-memory operations (including the
+// LDS DMA above) have completed, then join the workgroup barrier.  The asm
+// memory clobber also stops the compiler moving LDS accesses across it.
+__device__ __forceinline__ void vm_wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ uint32_t uniform(uint32_t v) {
+  return __builtin_amdgcn_readfirstlane(v);
+}
+
+// Round-to-nearest-even float -> 16-bit storage.
+template <int DT> __device__ __forceinline__ uint16_t to_bits(float v) {
+  if constexpr (DT == kF16)
+    return __builtin_bit_cast(uint16_t, (_Float16)v);
+  else
+    return __builtin_bit_cast(uint16_t, (__bf16)v);
+}
+
+template <int DT> __device__ __forceinline__ float from_bits(uint16_t v) {
+  if constexpr (DT == kF16)
+    return (float)__builtin_bit_cast(_Float16, v);
+  else
+    return __builtin_bit_cast(float, (uint32_t)v << 16);
+}
+
+// Pack two floats into one dword of 16-bit values (lo, hi), RNE.
+template <int DT> __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return (uint32_t)to_bits<DT>(lo) | ((uint32_t)to_bits<DT>(hi) << 16);
+}
+
+} // namespace wave

@@ -1,0 +1,288 @@
+// wave_runtime.cpp -- the C ABI of libwave_runtime.so (include/wave_runtime.h).
+//
+// Validates every request on the host before any HIP call, maps it onto the
+// kernels in gemm_kernels.hpp / attention_kernels.hpp / fa_small.hip, and
+// reports failures as status codes plus a per-thread message.  Also carries
+// the reference's seven memref -> pointer shims (runtime/wave_runtime.cpp:
+// 27-74) unchanged in behaviour.
+#include "../../include/wave_runtime.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "attention.hpp"
+#include "gemm.hpp"
+
+namespace {
+
+thread_local char g_error[512] = "";
+
+int fail(int status, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int hip_status(hipError_t e, const char *what) {
+  if (e == hipSuccess)
+    return WAVE_OK;
+  return fail((int)e, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool is_in_dtype(int t) { return t == WAVE_F16 || t == WAVE_BF16; }
+bool is_out_dtype(int t) { return t == WAVE_F32 || t == WAVE_F16 || t == WAVE_BF16; }
+
+// Shared GEMM argument checks.  Per-lane DMA offsets inside one 256-row
+// panel are 32-bit: 256 * K * 2 bytes must stay below 2^32.
+int check_gemm(const void *A, const void *B, const void *C, int M, int N, int K,
+               int in_dtype, int out_dtype, int c_layout) {
+  if (!A || !B || !C)
+    return fail(WAVE_ERR_INVALID, "gemm: null A, B or C");
+  if (M <= 0 || N <= 0 || K <= 0)
+    return fail(WAVE_ERR_INVALID, "gemm: M=%d N=%d K=%d must be positive", M, N, K);
+  if (!is_in_dtype(in_dtype))
+    return fail(WAVE_ERR_INVALID, "gemm: input dtype %d is not f16/bf16", in_dtype);
+  if (!is_out_dtype(out_dtype))
+    return fail(WAVE_ERR_INVALID, "gemm: output dtype %d is not f32/f16/bf16", out_dtype);
+  if (c_layout != WAVE_ROW_MAJOR && c_layout != WAVE_COL_MAJOR)
+    return fail(WAVE_ERR_INVALID, "gemm: layout %d is not row/column-major", c_layout);
+  if ((uint64_t)K * 2u * 256u >= (1ull << 32))
+    return fail(WAVE_ERR_UNSUPPORTED, "gemm: K=%d exceeds 2^23", K);
+  return WAVE_OK;
+}
+
+int streamk_sizes(int M, int N, int workers, size_t *scratch, size_t *counters) {
+  if (M <= 0 || N <= 0)
+    return fail(WAVE_ERR_INVALID, "streamk: M=%d N=%d must be positive", M, N);
+  if (workers <= 0)
+    return fail(WAVE_ERR_INVALID, "streamk: workers=%d must be positive", workers);
+  const size_t tiles = (size_t)wave::gemm::tiles_for(M) * wave::gemm::tiles_for(N);
+  *scratch = (size_t)workers * 2u * 256u * 256u * sizeof(float);
+  *counters = tiles * sizeof(uint32_t);
+  return WAVE_OK;
+}
+
+template <typename T> void *to_global(wave_memref_1d *m) {
+  return static_cast<void *>(static_cast<T *>(m->data) + m->offset);
+}
+
+} // namespace
+
+namespace wave {
+namespace gemm {
+hipError_t zero_counters(uint32_t *counters, size_t count, hipStream_t stream);
+hipError_t count_nonzero(const uint32_t *counters, size_t count, int *result,
+                         hipStream_t stream);
+} // namespace gemm
+} // namespace wave
+
+extern "C" {
+
+void *_mlir_ciface_wave_memref_to_ptr_global_i32(wave_memref_1d *m) {
+  return to_global<int32_t>(m);
+}
+void *_mlir_ciface_wave_memref_to_ptr_global_i8(wave_memref_1d *m) {
+  return to_global<int8_t>(m);
+}
+void *_mlir_ciface_wave_memref_to_ptr_global_f32(wave_memref_1d *m) {
+  return to_global<float>(m);
+}
+void *_mlir_ciface_wave_memref_to_ptr_global_f16(wave_memref_1d *m) {
+  return to_global<uint16_t>(m);
+}
+void *_mlir_ciface_wave_memref_to_ptr_global_bf16(wave_memref_1d *m) {
+  return to_global<uint16_t>(m);
+}
+void *_mlir_ciface_wave_memref_to_ptr_global_i64(wave_memref_1d *m) {
+  return to_global<int64_t>(m);
+}
+void *_mlir_ciface_wave_memref_to_ptr_global_f64(wave_memref_1d *m) {
+  return to_global<double>(m);
+}
+
+int wave_gemm_launch(const void *A, const void *B, void *C, int M, int N, int K,
+                     int in_dtype, int out_dtype, int c_layout, void *stream) {
+  int st = check_gemm(A, B, C, M, N, K, in_dtype, out_dtype, c_layout);
+  if (st != WAVE_OK)
+    return st;
+  wave::gemm::GemmArgs g;
+  g.A = A;
+  g.B = B;
+  g.C = C;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.in_dtype = in_dtype;
+  g.out_dtype = out_dtype;
+  g.col_major = c_layout == WAVE_COL_MAJOR;
+  return hip_status(wave::gemm::launch(g, static_cast<hipStream_t>(stream)),
+                    "wave_gemm_launch");
+}
+
+int wave_gemm_streamk_workspace_bytes(int M, int N, int workers,
+                                      size_t *scratch_bytes,
+                                      size_t *counter_bytes) {
+  if (!scratch_bytes || !counter_bytes)
+    return fail(WAVE_ERR_INVALID, "streamk: null size outputs");
+  return streamk_sizes(M, N, workers, scratch_bytes, counter_bytes);
+}
+
+int wave_gemm_streamk_launch(const void *A, const void *B, void *C, int M,
+                             int N, int K, int in_dtype, int out_dtype,
+                             int c_layout, float *scratch, uint32_t *counters,
+                             int workers, void *stream) {
+  int st = check_gemm(A, B, C, M, N, K, in_dtype, out_dtype, c_layout);
+  if (st != WAVE_OK)
+    return st;
+  if (!scratch || !counters)
+    return fail(WAVE_ERR_INVALID, "streamk: null scratch or counters");
+  const int64_t work = (int64_t)wave::gemm::tiles_for(M) *
+                       wave::gemm::tiles_for(N) * wave::gemm::k_iterations(K);
+  if (work > INT32_MAX)
+    return fail(WAVE_ERR_UNSUPPORTED, "streamk: %lld work units exceed i32",
+                (long long)work);
+  if (workers <= 0 || workers > work)
+    return fail(WAVE_ERR_INVALID, "streamk: workers=%d must be in [1, %lld]",
+                workers, (long long)work);
+  wave::gemm::GemmArgs g;
+  g.A = A;
+  g.B = B;
+  g.C = C;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.in_dtype = in_dtype;
+  g.out_dtype = out_dtype;
+  g.col_major = c_layout == WAVE_COL_MAJOR;
+  g.scratch = scratch;
+  g.counters = counters;
+  g.workers = workers;
+  return hip_status(wave::gemm::launch(g, static_cast<hipStream_t>(stream)),
+                    "wave_gemm_streamk_launch");
+}
+
+int wave_gemm_streamk_workspace_reset(uint32_t *counters, int M, int N,
+                                      void *stream) {
+  if (!counters)
+    return fail(WAVE_ERR_INVALID, "streamk reset: null counters");
+  size_t scratch = 0, bytes = 0;
+  int st = streamk_sizes(M, N, 1, &scratch, &bytes);
+  if (st != WAVE_OK)
+    return st;
+  return hip_status(wave::gemm::zero_counters(counters, bytes / sizeof(uint32_t),
+                                              static_cast<hipStream_t>(stream)),
+                    "wave_gemm_streamk_workspace_reset");
+}
+
+int wave_gemm_streamk_counters_check(const uint32_t *counters, int M, int N,
+                                     void *stream) {
+  if (!counters)
+    return fail(WAVE_ERR_INVALID, "streamk check: null counters");
+  size_t scratch = 0, bytes = 0;
+  int st = streamk_sizes(M, N, 1, &scratch, &bytes);
+  if (st != WAVE_OK)
+    return st;
+  int nonzero = 0;
+  st = hip_status(wave::gemm::count_nonzero(counters, bytes / sizeof(uint32_t),
+                                            &nonzero,
+                                            static_cast<hipStream_t>(stream)),
+                  "wave_gemm_streamk_counters_check");
+  return st != WAVE_OK ? st : nonzero;
+}
+
+int wave_fa_fwd_launch(const void *Q, const void *K, const void *V, void *O,
+                       int batch, int q_heads, int kv_heads, int seq,
+                       int head_dim, int dtype, int causal, float scale,
+                       void *stream) {
+  if (!Q || !K || !V || !O)
+    return fail(WAVE_ERR_INVALID, "fa: null Q, K, V or O");
+  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || seq <= 0)
+    return fail(WAVE_ERR_INVALID, "fa: batch=%d q_heads=%d kv_heads=%d seq=%d must be positive",
+                batch, q_heads, kv_heads, seq);
+  if (q_heads % kv_heads != 0)
+    return fail(WAVE_ERR_INVALID, "fa: q_heads=%d not a multiple of kv_heads=%d",
+                q_heads, kv_heads);
+  if (!is_in_dtype(dtype))
+    return fail(WAVE_ERR_INVALID, "fa: dtype %d is not f16/bf16", dtype);
+  if (causal != 0 && causal != 1)
+    return fail(WAVE_ERR_INVALID, "fa: causal=%d must be 0 or 1", causal);
+  if (!(scale >= 0.f) || scale != scale)
+    return fail(WAVE_ERR_INVALID, "fa: scale must be >= 0");
+  if (head_dim != 128)
+    return fail(WAVE_ERR_UNSUPPORTED, "fa: head_dim=%d (only 128 is built)", head_dim);
+  if ((int64_t)batch * q_heads * ((seq + 127) / 128) > INT32_MAX ||
+      (uint64_t)seq * 256u >= (1ull << 32))
+    return fail(WAVE_ERR_UNSUPPORTED, "fa: problem too large");
+  if ((reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(K) |
+       reinterpret_cast<uintptr_t>(V) | reinterpret_cast<uintptr_t>(O)) & 15)
+    return fail(WAVE_ERR_INVALID, "fa: Q, K, V and O must be 16-byte aligned");
+  wave::attention::FwdArgs a;
+  a.Q = Q;
+  a.K = K;
+  a.V = V;
+  a.O = O;
+  a.batch = batch;
+  a.q_heads = q_heads;
+  a.kv_heads = kv_heads;
+  a.seq_q = seq;
+  a.seq_k = seq;
+  a.head_dim = head_dim;
+  a.dtype = dtype;
+  a.causal = causal;
+  a.scale = scale;
+  return hip_status(wave::attention::launch_fwd(a, static_cast<hipStream_t>(stream)),
+                    "wave_fa_fwd_launch");
+}
+
+int wave_fa_f32_launch(const void *Q, const void *K, const void *V, float *O,
+                       int block_m, int seq_n, int head_dim, void *stream) {
+  if (!Q || !K || !V || !O)
+    return fail(WAVE_ERR_INVALID, "fa_f32: null Q, K, V or O");
+  if (block_m <= 0 || seq_n <= 0 || head_dim <= 0)
+    return fail(WAVE_ERR_INVALID, "fa_f32: block_m=%d seq_n=%d head_dim=%d must be positive",
+                block_m, seq_n, head_dim);
+  if (seq_n > 16384)
+    return fail(WAVE_ERR_UNSUPPORTED, "fa_f32: seq_n=%d exceeds 16384", seq_n);
+  return hip_status(wave::attention::launch_small(Q, K, V, O, block_m, seq_n, head_dim,
+                                                  static_cast<hipStream_t>(stream)),
+                    "wave_fa_f32_launch");
+}
+
+const char *wave_status_string(int status) {
+  switch (status) {
+  case WAVE_OK:
+    return "ok";
+  case WAVE_ERR_INVALID:
+    return "invalid argument";
+  case WAVE_ERR_UNSUPPORTED:
+    return "unsupported configuration";
+  case WAVE_ERR_WORKSPACE:
+    return "Stream-K workspace not reset";
+  default:
+    return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
+  }
+}
+
+const char *wave_last_error(void) { return g_error; }
+
+int wave_device_mfma_peak(int device, double *tflops, double *clock_mhz,
+                          int *compute_units) {
+  if (!tflops || !clock_mhz || !compute_units)
+    return fail(WAVE_ERR_INVALID, "device peak: null output");
+  hipDeviceProp_t prop;
+  int st = hip_status(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+  if (st != WAVE_OK)
+    return st;
+  *compute_units = prop.multiProcessorCount;
+  *clock_mhz = prop.clockRate / 1000.0;
+  *tflops = (double)prop.multiProcessorCount * (prop.clockRate * 1e3) * 4096.0 * 1e-12;
+  return WAVE_OK;
+}
+
+} // extern "C"

@@ -1,0 +1,156 @@
+"""Tensor-level front end of libwave_runtime.so.
+
+PyTorch only provides device memory and the current stream here; all
+arithmetic runs in the library's gfx950 kernels.  Argument errors raise
+ValueError (as the reference's builders do, wave_matmul.py:533-775) and HIP
+failures raise runtime.WaveError.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import runtime as rt
+
+_DT = {torch.float32: rt.F32, torch.float16: rt.F16, torch.bfloat16: rt.BF16}
+_NAMES = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+
+def _dtype(d) -> torch.dtype:
+    return _NAMES[d] if isinstance(d, str) else d
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def gemm(a: torch.Tensor, b: torch.Tensor, *, out_dtype="f16",
+         layout: str = "row", out: torch.Tensor | None = None) -> torch.Tensor:
+    """C = A . B^T with A [M, K] and B [N, K] (f16 or bf16), fp32 accumulate.
+
+    layout "row" returns C as [M, N]; "col" returns the column-major buffer
+    viewed as [N, M] (element (n, m) = C[m, n]).
+    """
+    _need(a, "a")
+    _need(b, "b")
+    if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[1]:
+        raise ValueError("a must be [M, K] and b [N, K]")
+    if a.dtype != b.dtype or a.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("a and b must both be f16 or both bf16")
+    M, K = a.shape
+    N = b.shape[0]
+    odt = _dtype(out_dtype)
+    shape = (M, N) if layout == "row" else (N, M)
+    if out is None:
+        out = torch.empty(shape, dtype=odt, device=a.device)
+    elif tuple(out.shape) != shape or out.dtype != odt:
+        raise ValueError("out has the wrong shape or dtype")
+    _need(out, "out")
+    rt.check(rt.lib().wave_gemm_launch(
+        a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, _DT[a.dtype], _DT[odt],
+        rt.ROW_MAJOR if layout == "row" else rt.COL_MAJOR, _stream(a)))
+    return out
+
+
+def streamk_workspace_bytes(M: int, N: int, workers: int) -> tuple[int, int]:
+    s, c = ctypes.c_size_t(), ctypes.c_size_t()
+    rt.check(rt.lib().wave_gemm_streamk_workspace_bytes(M, N, workers, ctypes.byref(s),
+                                                        ctypes.byref(c)))
+    return s.value, c.value
+
+
+class StreamKWorkspace:
+    """Caller-owned Stream-K workspace: fp32 partial slots + zeroed counters."""
+
+    def __init__(self, M: int, N: int, workers: int, device="cuda"):
+        sb, cb = streamk_workspace_bytes(M, N, workers)
+        self.M, self.N, self.workers = M, N, workers
+        self.scratch = torch.empty(sb // 4, dtype=torch.float32, device=device)
+        self.counters = torch.zeros(cb // 4, dtype=torch.int32, device=device)
+
+    def reset(self) -> None:
+        rt.check(rt.lib().wave_gemm_streamk_workspace_reset(
+            self.counters.data_ptr(), self.M, self.N, _stream(self.counters)))
+
+    def nonzero_counters(self) -> int:
+        r = rt.lib().wave_gemm_streamk_counters_check(
+            self.counters.data_ptr(), self.M, self.N, _stream(self.counters))
+        if r < 0 or r > self.counters.numel():
+            rt.check(r)
+        return r
+
+
+def gemm_streamk(a: torch.Tensor, b: torch.Tensor, workers: int, *,
+                 out_dtype="f16", layout: str = "row",
+                 workspace: StreamKWorkspace | None = None,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """Stream-K C = A . B^T over `workers` persistent workgroups."""
+    _need(a, "a")
+    _need(b, "b")
+    if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[1]:
+        raise ValueError("a must be [M, K] and b [N, K]")
+    if a.dtype != b.dtype or a.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("a and b must both be f16 or both bf16")
+    M, K = a.shape
+    N = b.shape[0]
+    odt = _dtype(out_dtype)
+    shape = (M, N) if layout == "row" else (N, M)
+    if out is None:
+        out = torch.empty(shape, dtype=odt, device=a.device)
+    _need(out, "out")
+    ws = workspace or StreamKWorkspace(M, N, workers, a.device)
+    rt.check(rt.lib().wave_gemm_streamk_launch(
+        a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, _DT[a.dtype], _DT[odt],
+        rt.ROW_MAJOR if layout == "row" else rt.COL_MAJOR, ws.scratch.data_ptr(),
+        ws.counters.data_ptr(), workers, _stream(a)))
+    return out
+
+
+def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
+                    causal: bool = False, scale: float | None = None,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """softmax(Q K^T * scale) V for q [B, Hq, S, D], k/v [B, Hkv, S, D]."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _need(t, n)
+        if t.dim() != 4:
+            raise ValueError(f"{n} must be [batch, heads, seq, head_dim]")
+    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("q, k, v must share an f16 or bf16 dtype")
+    B, Hq, S, D = q.shape
+    if k.shape != v.shape or k.shape[0] != B or k.shape[2] != S or k.shape[3] != D:
+        raise ValueError("k and v must be [batch, kv_heads, seq, head_dim]")
+    Hkv = k.shape[1]
+    if out is None:
+        out = torch.empty_like(q)
+    _need(out, "out")
+    rt.check(rt.lib().wave_fa_fwd_launch(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, Hq, Hkv, S, D,
+        _DT[q.dtype], int(causal), float(scale or 0.0), _stream(q)))
+    return out
+
+
+def flash_attention_f32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                        out: torch.Tensor | None = None) -> torch.Tensor:
+    """The flash_attention_f32 ABI: q [block_m, D] f16 pre-scaled by
+    log2(e)/sqrt(D), k/v [seq_n, D] f16 -> O [block_m, D] f32 (exp2 softmax)."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _need(t, n)
+        if t.dim() != 2 or t.dtype != torch.float16:
+            raise ValueError(f"{n} must be a 2-D f16 tensor")
+    block_m, D = q.shape
+    seq_n = k.shape[0]
+    if out is None:
+        out = torch.empty((block_m, D), dtype=torch.float32, device=q.device)
+    rt.check(rt.lib().wave_fa_f32_launch(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), block_m, seq_n, D,
+        _stream(q)))
+    return out

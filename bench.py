@@ -1,0 +1,183 @@
+#!/usr/bin/env python3
+"""Benchmark of the hot path on one MI355X: prints ONE JSON line.
+
+Headline: f16 GEMM C = A . B^T, M = N = K = 8192,
+A [M x K] and B [N x K] row-major f16 uniform in [-1, 1) from a seeded PRNG,
+fp32 accumulation, f16 row-major C.  One "step" = one launch of the GEMM over
+inputs already resident in HBM.  `value` = 2*M*N*K / mean step time
+(TFLOP/s); the roofline block sets the same rate against the dense f16 MFMA
+peak.  Beside it: the flash-attention forward of configs[3] (B4 H32 S4096
+D128 f16, non-causal; FLOPs 4*B*H*S^2*D as the reference counts them,
+wave-fa-gfx950-runner.cpp:465-467) and the CPU baseline -- the oracle's
+multithreaded C++ GEMM timed on a bounded sample of output rows of the same
+workload on this host's cores.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-fa]
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+MFMA_PEAK_TFLOPS = 2516.6   # MI355X dense f16/bf16: 256 CU x 2.4 GHz x 4096
+HBM_PEAK_GBS = 8000.0
+PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "gemm_f16_8192_traffic.txt")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def read_traffic():
+    """HBM bytes per GEMM launch from the committed rocprofv3 --pmc summary
+    (line `traffic_bytes_per_launch: N`), or None."""
+    try:
+        with open(PROFILE_TRAFFIC) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def time_launches(fn, steps, warmup, torch):
+    """Mean ms per launch over `steps` back-to-back launches, timed with HIP
+    events on the current stream (the stream the kernels are launched on)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def cpu_baseline(a_bits, b_bits, M, N, K, budget_s):
+    """Oracle GEMM (C++, fp32 accumulate, all allowed host threads) on a
+    bounded sample of rows of the same 8192^3 problem."""
+    from oracle import oracle
+    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    rows = 8
+    t0 = time.perf_counter()
+    oracle.gemm_nt_rows(a_bits, b_bits, 0, rows, oracle.F16, threads=threads)
+    dt = time.perf_counter() - t0
+    # scale the sample to roughly `budget_s` of CPU work
+    rows = int(min(M, max(rows, rows * budget_s / max(dt, 1e-3))))
+    t0 = time.perf_counter()
+    oracle.gemm_nt_rows(a_bits, b_bits, 0, rows, oracle.F16, threads=threads)
+    dt = time.perf_counter() - t0
+    return {"value": round(2.0 * rows * N * K / dt / 1e12, 6), "unit": "TFLOP/s",
+            "cores": threads, "kind": "port",
+            "sample": f"rows 0..{rows - 1} of C (={rows}x{N}x{K}) of the 8192^3 f16 GEMM, "
+                      f"{dt:.1f} s, oracle/oracle.cpp gemm_nt_rows"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-fa", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(see DESIGN.md for how the GEMM and attention would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    wave = importlib.import_module("7_amd")
+    wave.runtime.lib()
+    dev = torch.device("cuda:0")
+    peak_dev, clock_mhz, cus = wave.runtime.device_mfma_peak(0)
+    log(f"device: {torch.cuda.get_device_name(0)} CUs={cus} clock={clock_mhz:.0f} MHz "
+        f"derived f16 MFMA peak={peak_dev:.1f} TFLOP/s")
+
+    M = N = K = 8192
+    g = torch.Generator(device="cpu").manual_seed(7)
+    a_h = (torch.rand((M, K), generator=g) * 2 - 1).to(torch.float16)
+    b_h = (torch.rand((N, K), generator=g) * 2 - 1).to(torch.float16)
+    a, b = a_h.to(dev), b_h.to(dev)
+    c = torch.empty((M, N), dtype=torch.float16, device=dev)
+
+    def step():
+        wave.gemm(a, b, out_dtype=torch.float16, out=c)
+
+    ms = time_launches(step, args.steps, args.warmup, torch)
+    flops = 2.0 * M * N * K
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"gemm f16 8192^3: {ms * 1e3:.1f} us/launch, {tflops:.1f} TFLOP/s "
+        f"({100 * tflops / MFMA_PEAK_TFLOPS:.1f}% of {MFMA_PEAK_TFLOPS})")
+
+    secondary = []
+    if not args.no_fa:
+        B, H, S, D = 4, 32, 4096, 128
+        gq = torch.Generator(device="cpu").manual_seed(11)
+        q = torch.randn((B, H, S, D), generator=gq).to(torch.float16).to(dev)
+        k = torch.randn((B, H, S, D), generator=gq).to(torch.float16).to(dev)
+        v = torch.randn((B, H, S, D), generator=gq).to(torch.float16).to(dev)
+        o = torch.empty_like(q)
+        fa_ms = time_launches(lambda: wave.flash_attention(q, k, v, out=o),
+                              max(10, args.steps // 2), 3, torch)
+        fa_tf = 4.0 * B * H * S * S * D / (fa_ms * 1e-3) / 1e12
+        log(f"fa fwd f16 B4 H32 S4096 D128: {fa_ms * 1e3:.1f} us/launch, {fa_tf:.1f} TFLOP/s "
+            f"({100 * fa_tf / MFMA_PEAK_TFLOPS:.1f}%)")
+        secondary.append({"workload": "fa_fwd_f16_b4_h32_s4096_d128_noncausal",
+                          "value": round(fa_tf, 2), "unit": "TFLOP/s",
+                          "ms_per_step": round(fa_ms, 4),
+                          "frac_of_mfma_peak": round(fa_tf / MFMA_PEAK_TFLOPS, 4)})
+        del q, k, v, o
+
+    cpu = None
+    if not args.no_cpu:
+        a_bits = a_h.view(torch.int16).numpy().view(np.uint16)
+        b_bits = b_h.view(torch.int16).numpy().view(np.uint16)
+        cpu = cpu_baseline(a_bits, b_bits, M, N, K, args.cpu_budget)
+        log(f"cpu baseline: {cpu['value']} TFLOP/s on {cpu['cores']} threads ({cpu['sample']})")
+
+    line = {
+        "metric": "TFLOP/s + % gfx950 MFMA peak: f16 GEMM 8192^3, FA fwd S=4096 D=128",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic: A, B uniform [-1, 1) f16, torch CPU generator seed 7",
+        "config": {"workload": "gemm_f16_8192x8192x8192", "M": M, "N": N, "K": K,
+                   "A": "M x K row-major", "B": "N x K row-major", "C": "f16 row-major",
+                   "accumulate": "fp32"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
+                     "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+                     "traffic": read_traffic()},
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+        "device_derived_peak_tflops": round(peak_dev, 1),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,130 @@
+/*
+ * wave_runtime.h -- C ABI of libwave_runtime.so, the MI355X-native (gfx950)
+ * drop-in for the reference's GEMM / Stream-K / flash-attention hot path.
+ *
+ * Plain pointers and sizes only: device buffers are caller-owned device
+ * memory, `stream` is a hipStream_t passed as void* (NULL = the null
+ * stream).  No entry point allocates; every launch entry point validates
+ * its arguments before touching the GPU.
+ *
+ * Return codes: WAVE_OK (0); a negative WAVE_ERR_* for argument errors
+ * (the reference runners exit 2 on these: wave-matmul-calibrate-runner.cpp
+ * :65-68 `die`); a positive hipError_t value for HIP failures (the runners
+ * exit 1: runner.cpp:620-625 `checkHip`).  wave_last_error() returns a
+ * message for the last failure on the calling thread.
+ */
+#ifndef WAVE_RUNTIME_H
+#define WAVE_RUNTIME_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types (f16/bf16 inputs; f32/f16/bf16 GEMM output). */
+enum { WAVE_F32 = 0, WAVE_F16 = 1, WAVE_BF16 = 2 };
+/* GEMM output layouts: C[m*N+n] or C[n*M+m]
+ * (runner.cpp:32 OutputLayout::RowMajor / ColumnMajor). */
+enum { WAVE_ROW_MAJOR = 0, WAVE_COL_MAJOR = 1 };
+/* Status codes. */
+enum {
+  WAVE_OK = 0,
+  WAVE_ERR_INVALID = -1,     /* bad argument (null pointer, size, dtype)  */
+  WAVE_ERR_UNSUPPORTED = -2, /* valid request outside what is built       */
+  WAVE_ERR_WORKSPACE = -3    /* Stream-K counters not zero / too small    */
+};
+
+/* ---- reference shims, byte-compatible --------------------------------
+ * runtime/wave_runtime.cpp:27-74: MLIR StridedMemRefType<T,1> descriptor
+ * -> device pointer data + offset (offset in elements of T). */
+typedef struct {
+  void *base;
+  void *data;
+  int64_t offset;
+  int64_t sizes[1];
+  int64_t strides[1];
+} wave_memref_1d;
+
+void *_mlir_ciface_wave_memref_to_ptr_global_i32(wave_memref_1d *m);
+void *_mlir_ciface_wave_memref_to_ptr_global_i8(wave_memref_1d *m);
+void *_mlir_ciface_wave_memref_to_ptr_global_f32(wave_memref_1d *m);
+void *_mlir_ciface_wave_memref_to_ptr_global_f16(wave_memref_1d *m);
+void *_mlir_ciface_wave_memref_to_ptr_global_bf16(wave_memref_1d *m);
+void *_mlir_ciface_wave_memref_to_ptr_global_i64(wave_memref_1d *m);
+void *_mlir_ciface_wave_memref_to_ptr_global_f64(wave_memref_1d *m);
+
+/* ---- tiled GEMM --------------------------------------------------------
+ * C = A . B^T: A [M x K] row-major, B [N x K] row-major (the reference's
+ * "column-major K x N" B, python/mlir/dialects/wave_matmul.py:329-333),
+ * fp32 accumulation, one RNE rounding to the output type.  Replaces the
+ * kernel `wmma_f16_matmul_tiled(A, B, C, trip)` (wave_matmul.py:11415-11430,
+ * launched by wave-matmul-calibrate-runner.cpp:1852-1856) for any M, N, K
+ * > 0 and f16/bf16 input; the reference bakes M/N/K into each kernel and
+ * requires the tiling to divide them. */
+int wave_gemm_launch(const void *A, const void *B, void *C, int M, int N,
+                     int K, int in_dtype, int out_dtype, int c_layout,
+                     void *stream);
+
+/* ---- Stream-K GEMM ------------------------------------------------------
+ * Same C as wave_gemm_launch, computed by `workers` persistent workgroups
+ * over the (tile, 64-wide K step) work list (wave_matmul.py:77-165).
+ * Replaces `gfx950_f16_streamk_gemm(A, B, C, scratch, counters, workers)`
+ * (wave_matmul.py:11521-11567; runner.cpp:1781-1834).  The reference
+ * requires f16 in/out, column-major C, M,N % 256 == 0 and K % 64 == 0
+ * (runner.cpp:424-440); this one takes any shape, dtype and layout.
+ * Workspace (caller-owned, runner.cpp:393-412): scratch holds two fp32
+ * 256x256 tiles per worker and needs no initialisation; counters hold one
+ * uint32 per 256x256 output tile and must be zero before the first launch;
+ * each launch leaves them zero again.  One launch in flight per workspace. */
+int wave_gemm_streamk_workspace_bytes(int M, int N, int workers,
+                                      size_t *scratch_bytes,
+                                      size_t *counter_bytes);
+int wave_gemm_streamk_launch(const void *A, const void *B, void *C, int M,
+                             int N, int K, int in_dtype, int out_dtype,
+                             int c_layout, float *scratch, uint32_t *counters,
+                             int workers, void *stream);
+/* Zero the counters (after a failed or interrupted launch; Stream-K design
+ * doc docs/Gfx950StreamKSameKernelReductionDesign.md:98-101). */
+int wave_gemm_streamk_workspace_reset(uint32_t *counters, int M, int N,
+                                      void *stream);
+/* Synchronise `stream` and count non-zero counters (runner.cpp:1718-1742
+ * checkStreamKCounters).  Returns the count (0 = clean) or an error. */
+int wave_gemm_streamk_counters_check(const uint32_t *counters, int M, int N,
+                                     void *stream);
+
+/* ---- flash-attention forward --------------------------------------------
+ * O = softmax(Q K^T * scale) V.  Q, O: [batch][q_heads][seq][head_dim];
+ * K, V: [batch][kv_heads][seq][head_dim]; dtype f16 or bf16 for all four;
+ * fp32 row max / sum.  kv head = q head / (q_heads / kv_heads).  causal
+ * masks key > query.  scale <= 0 selects 1/sqrt(head_dim).  Replaces the
+ * kernel `flash_attention_bf16_gfx950(Q, K, V, O)` (wave_flash_attention.py
+ * :1697-1728; wave-fa-gfx950-runner.cpp:396-402: grid (seq/256,
+ * batch*heads)), which is bf16, non-causal, q_heads == kv_heads and
+ * seq % 256 == 0 only.  head_dim must be 128. */
+int wave_fa_fwd_launch(const void *Q, const void *K, const void *V, void *O,
+                       int batch, int q_heads, int kv_heads, int seq,
+                       int head_dim, int dtype, int causal, float scale,
+                       void *stream);
+
+/* ---- flash_attention_f32 ------------------------------------------------
+ * Replaces `flash_attention_f32(Q, K, V, O)` (wave_attention.py:1406-1441;
+ * wave-fa-calibrate-runner.cpp:346-361): Q [block_m][head_dim] f16
+ * pre-scaled by log2(e)/sqrt(head_dim), K, V [seq_n][head_dim] f16,
+ * O [block_m][head_dim] f32 = softmax2(Q K^T) V with exp2.  seq_n <= 16384. */
+int wave_fa_f32_launch(const void *Q, const void *K, const void *V, float *O,
+                       int block_m, int seq_n, int head_dim, void *stream);
+
+/* ---- diagnostics ---------------------------------------------------------- */
+const char *wave_status_string(int status);
+const char *wave_last_error(void);
+/* Dense f16/bf16 MFMA peak (TFLOP/s) of `device` derived from
+ * hipDeviceProp_t (CUs x clock x 4096 FLOP/clk/CU) and its clock in MHz. */
+int wave_device_mfma_peak(int device, double *tflops, double *clock_mhz,
+                          int *compute_units);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* WAVE_RUNTIME_H */

@@ -1,6 +1,8 @@
+import importlib
 import os
 import sys
 
+import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -17,3 +19,31 @@ def oracle():
     from oracle import oracle as o
     o.lib()
     return o
+
+
+@pytest.fixture(scope="session")
+def wave():
+    """The product package (libwave_runtime.so through ctypes)."""
+    w = importlib.import_module("7_amd")
+    w.runtime.lib()
+    return w
+
+
+@pytest.fixture(scope="session")
+def dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
+    return torch.device("cuda:0")
+
+
+def to_dev(bits: np.ndarray, dtype, device):
+    """uint16 bit patterns (oracle output) -> device tensor of `dtype`."""
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(bits, dtype=np.uint16).view(np.int16))
+    return t.view(dtype).to(device)
+
+
+def to_bits(t) -> np.ndarray:
+    """16-bit device tensor -> host uint16 bit patterns."""
+    import torch
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)

@@ -1,0 +1,132 @@
+"""GPU parity of the flash-attention kernels against the oracle.
+
+* wave_fa_fwd_launch vs oracle.attention_rows (double-precision softmax,
+  the reference runner's computeAttentionRow, wave-fa-gfx950-runner.cpp
+  :247-279, extended with the causal mask and the GQA head map).  Tolerance:
+  BASELINE.json's 2e-2 on O (the reference runner uses 3e-2, :388).
+* The reference's own inputs (bucket generator x 0.125 / 0.25, bf16,
+  runner :194-202), all rows of small problems, the sampled heads/rows of
+  large ones (runner :204-232), and --zero-qk (every row = mean of V).
+* wave_fa_f32_launch vs oracle.fa_f32_reference at the runner tolerance
+  3e-3 (wave-fa-calibrate-runner.cpp:251-273).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import to_bits, to_dev
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+TDT = {1: torch.float16, 2: torch.bfloat16}
+
+
+def run_fa(wave, oracle, dev, q, k, v, dt, B, Hq, Hkv, S, causal, heads, rows):
+    """q, k, v: uint16 bit arrays [B*H*S*D]; checks (head, row) pairs."""
+    D = 128
+    qt = to_dev(q, TDT[dt], dev).view(B, Hq, S, D)
+    kt = to_dev(k, TDT[dt], dev).view(B, Hkv, S, D)
+    vt = to_dev(v, TDT[dt], dev).view(B, Hkv, S, D)
+    o = wave.flash_attention(qt, kt, vt, causal=causal)
+    torch.cuda.synchronize()
+    got = oracle.bits_to_f32(to_bits(o).reshape(B * Hq, S, D), dt)
+    hh, rr = np.meshgrid(np.asarray(heads), np.asarray(rows), indexing="ij")
+    hh, rr = hh.ravel(), rr.ravel()
+    ref = oracle.attention_rows(q, k, v, dtype=dt, batch=B, q_heads=Hq, kv_heads=Hkv,
+                                seq_q=S, seq_k=S, head_dim=D, causal=causal,
+                                scale=1.0 / math.sqrt(D), heads=hh, rows=rr)
+    err = np.abs(got[hh, rr] - ref)
+    assert np.all(np.isfinite(got[hh, rr]))
+    return float(err.max())
+
+
+def normal_bits(n, dt, seed):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    t = torch.randn(n, generator=g).to(TDT[dt])
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("seq", [256, 512])
+@pytest.mark.parametrize("iscale", [1, 4])
+def test_reference_inputs_all_rows(wave, oracle, dev, seq, iscale):
+    """wave_flash_attention_gfx950_runtime.mlir:3-38: B1 H1 S256, adaptive
+    input scale 4; bf16 bucket inputs, every row checked."""
+    n = seq * 128
+    q, k, v = oracle.fa_gfx950_inputs(n, 0, iscale)
+    err = run_fa(wave, oracle, dev, q, k, v, 2, 1, 1, 1, seq, False, [0], range(seq))
+    assert err <= TOL, err
+
+
+def test_zero_qk_rows_are_mean_v(wave, oracle, dev):
+    n = 2 * 512 * 128
+    q, k, v = oracle.fa_gfx950_inputs(n, 3, 1, zero_qk=True)
+    qt = to_dev(q, torch.bfloat16, dev).view(1, 2, 512, 128)
+    kt = to_dev(k, torch.bfloat16, dev).view(1, 2, 512, 128)
+    vt = to_dev(v, torch.bfloat16, dev).view(1, 2, 512, 128)
+    o = wave.flash_attention(qt, kt, vt).float().cpu()
+    mean = vt.float().mean(dim=2, keepdim=True).cpu()
+    assert float((o - mean).abs().max()) <= 1e-2
+
+
+@pytest.mark.parametrize("dt", [1, 2])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("B,Hq,Hkv,S", [(1, 2, 2, 128), (2, 4, 2, 320), (1, 8, 1, 200),
+                                        (1, 1, 1, 64), (1, 2, 1, 1000), (1, 1, 1, 7)])
+def test_small_problems_all_rows(wave, oracle, dev, dt, causal, B, Hq, Hkv, S):
+    q = normal_bits(B * Hq * S * 128, dt, 1)
+    k = normal_bits(B * Hkv * S * 128, dt, 2)
+    v = normal_bits(B * Hkv * S * 128, dt, 3)
+    err = run_fa(wave, oracle, dev, q, k, v, dt, B, Hq, Hkv, S, causal,
+                 range(B * Hq), range(S))
+    assert err <= TOL, err
+
+
+def test_config4_f16_b4_h32_s4096(wave, oracle, dev):
+    """non-causal f16, N(0,1), sampled heads and rows."""
+    B, H, S = 4, 32, 4096
+    n = B * H * S * 128
+    q, k, v = (normal_bits(n, 1, s) for s in (11, 12, 13))
+    heads = oracle.fa_reference_heads(B * H)
+    rows = oracle.fa_reference_rows(S) + [1, 255, 256, 1000, 4000]
+    err = run_fa(wave, oracle, dev, q, k, v, 1, B, H, H, S, False, heads, sorted(set(rows)))
+    assert err <= TOL, err
+
+
+def test_config5_causal_gqa_bf16_s8192(wave, oracle, dev):
+    """causal, 64 query heads over 8 KV heads, S=8192."""
+    B, Hq, Hkv, S = 1, 64, 8, 8192
+    q = normal_bits(B * Hq * S * 128, 2, 21)
+    k = normal_bits(B * Hkv * S * 128, 2, 22)
+    v = normal_bits(B * Hkv * S * 128, 2, 23)
+    heads = [0, 7, 8, 31, 63]
+    rows = sorted(set(oracle.fa_reference_rows(S) + [1, 63, 64, 4097, 8191]))
+    err = run_fa(wave, oracle, dev, q, k, v, 2, B, Hq, Hkv, S, True, heads, rows)
+    assert err <= TOL, err
+
+
+def test_key_permutation_invariance(wave, dev):
+    """Non-causal attention is invariant under a joint permutation of the
+    key/value rows (a size-independent property at a large shape)."""
+    g = torch.Generator(device="cpu").manual_seed(4)
+    q = torch.randn(1, 4, 2048, 128, generator=g).to(torch.float16).to(dev)
+    k = torch.randn(1, 4, 2048, 128, generator=g).to(torch.float16).to(dev)
+    v = torch.randn(1, 4, 2048, 128, generator=g).to(torch.float16).to(dev)
+    perm = torch.randperm(2048, generator=g).to(dev)
+    o1 = wave.flash_attention(q, k, v).float()
+    o2 = wave.flash_attention(q, k[:, :, perm].contiguous(), v[:, :, perm].contiguous()).float()
+    assert float((o1 - o2).abs().max()) <= 5e-3
+
+
+@pytest.mark.parametrize("bm,sn,hd,seed", [(16, 16, 32, 11), (16, 32, 32, 11),
+                                           (16, 64, 64, 3), (16, 256, 128, 5),
+                                           (8, 100, 32, 2)])
+def test_flash_attention_f32_abi(wave, oracle, dev, bm, sn, hd, seed):
+    q, k, v = oracle.fa_f32_inputs(bm, sn, hd, seed)
+    o = wave.flash_attention_f32(to_dev(q, torch.float16, dev), to_dev(k, torch.float16, dev),
+                                 to_dev(v, torch.float16, dev))
+    ref = oracle.fa_f32_reference(q, k, v)
+    assert float(np.abs(o.cpu().numpy() - ref).max()) <= 3e-3

@@ -1,0 +1,106 @@
+"""GPU parity of the Stream-K GEMM (wave_gemm_streamk_launch).
+
+Mirrors test/Integration/wave_gfx950_streamk_f16_runtime.mlir:3-80: split
+(5 workers) and aligned (2 workers) partitions of 512x512x256, random and
+HPL inputs, column-major f16 output, many launches reusing one workspace,
+and the post-run "counters are zero" check (runner.cpp:1718-1742).  Bucket
+inputs make the fp32 sums exact, so results are compared bitwise with the
+oracle and with the tiled kernel; the fixed-order reduction makes repeated
+launches bit-identical.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import to_bits, to_dev
+
+pytestmark = pytest.mark.gpu
+
+TDT = {1: torch.float16, 2: torch.bfloat16}
+
+
+def inputs(oracle, dev, M, N, K, dt, seed=5, mode=None):
+    mode = oracle.MODE_RANDOM if mode is None else mode
+    a = oracle.gemm_inputs(M, K, dt, seed, 0, mode)
+    b = oracle.gemm_inputs(N, K, dt, seed, 1, mode)
+    return a, b, to_dev(a, TDT[dt], dev), to_dev(b, TDT[dt], dev)
+
+
+@pytest.mark.parametrize("workers", [5, 2, 1, 3, 7, 16])
+@pytest.mark.parametrize("mode", ["random", "hpl"])
+def test_reference_streamk_cases(wave, oracle, dev, workers, mode):
+    M = N = 512
+    K = 256
+    m = oracle.MODE_RANDOM if mode == "random" else oracle.MODE_HPL
+    a, b, da, db = inputs(oracle, dev, M, N, K, 1, mode=m)
+    ws = wave.StreamKWorkspace(M, N, workers, dev)
+    c = wave.gemm_streamk(da, db, workers, out_dtype=torch.float16, layout="col",
+                          workspace=ws)
+    torch.cuda.synchronize()
+    ref = oracle.round_output(oracle.gemm_nt(a, b, 1), 1)
+    got = to_bits(c.t().contiguous())
+    if mode == "random":
+        assert np.array_equal(got, ref)
+    else:
+        # HPL values are not dyadic-exact; runner tolerance 1e-2 + 1e-3|exp|
+        g = oracle.f16_bits_to_f32(got)
+        e = oracle.f16_bits_to_f32(ref)
+        assert np.all(np.abs(g - e) <= 1e-2 + 1e-3 * np.abs(e))
+    assert ws.nonzero_counters() == 0
+
+
+def test_workspace_reuse_many_launches(wave, oracle, dev):
+    M = N = 512
+    K = 256
+    a, b, da, db = inputs(oracle, dev, M, N, K, 1)
+    ws = wave.StreamKWorkspace(M, N, 5, dev)
+    first = wave.gemm_streamk(da, db, 5, out_dtype=torch.float16, workspace=ws)
+    out = torch.empty_like(first)
+    for _ in range(200):
+        wave.gemm_streamk(da, db, 5, out_dtype=torch.float16, workspace=ws, out=out)
+    torch.cuda.synchronize()
+    assert torch.equal(first, out)
+    assert ws.nonzero_counters() == 0
+    ref = oracle.round_output(oracle.gemm_nt(a, b, 1), 1)
+    assert np.array_equal(to_bits(first), ref)
+
+
+@pytest.mark.parametrize("in_dt", [1, 2])
+@pytest.mark.parametrize("out_dt", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape,workers", [((128, 1024, 2048), 40), ((300, 520, 700), 9),
+                                           ((257, 255, 4100), 13), ((1024, 1024, 1024), 64)])
+def test_ragged_streamk_matches_tiled(wave, oracle, dev, in_dt, out_dt, shape, workers):
+    M, N, K = shape
+    a, b, da, db = inputs(oracle, dev, M, N, K, in_dt, seed=11)
+    sk = wave.gemm_streamk(da, db, workers, out_dtype=out_dt)
+    tiled = wave.gemm(da, db, out_dtype=out_dt)
+    torch.cuda.synchronize()
+    assert torch.equal(sk, tiled)
+
+
+def test_dirty_counters_are_detected_and_reset(wave, oracle, dev):
+    """Failure contract: counters must start at zero (Stream-K design doc
+    :98-101).  Dirty them from the host, see the check report it, reset."""
+    M = N = 512
+    ws = wave.StreamKWorkspace(M, N, 5, dev)
+    ws.counters.fill_(3)
+    assert ws.nonzero_counters() == 4
+    ws.reset()
+    assert ws.nonzero_counters() == 0
+
+
+def test_config3_streamk_bf16(wave, oracle, dev):
+    """BASELINE config 3a through Stream-K: 128x8192x8192 bf16 has only 32
+    output tiles, so 256 workers split the K loop of every tile."""
+    M, N, K = 128, 8192, 8192
+    g = torch.Generator(device="cpu").manual_seed(3)
+    a = (torch.randn((M, K), generator=g) / np.sqrt(K)).to(torch.bfloat16)
+    b = (torch.randn((N, K), generator=g) / np.sqrt(K)).to(torch.bfloat16)
+    c = wave.gemm_streamk(a.to(dev), b.to(dev), 256, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    abits = a.view(torch.int16).numpy().view(np.uint16)
+    bbits = b.view(torch.int16).numpy().view(np.uint16)
+    got = c.float().cpu().numpy()
+    ref = oracle.gemm_nt_rows(abits, bbits, 0, M, 2)
+    assert float(np.abs(got - ref).max()) <= 2e-3 * np.sqrt(K)
