@@ -80,7 +80,7 @@ hipError_t count_nonzero(const uint32_t *counters, size_t count, int *result,
 }
 
 int tiles_for(int extent) { return (extent + kTile - 1) / kTile; }
-int k_iterations(int K) { return (K + kBK - 1) / kBK; }
+int k_iterations(int K) { return (K + kSKUnit - 1) / kSKUnit; }
 
 hipError_t launch(const GemmArgs &g, hipStream_t stream) {
   Params p{};
@@ -102,7 +102,7 @@ hipError_t launch(const GemmArgs &g, hipStream_t stream) {
   p.counters = static_cast<uint32_t *>(g.counters);
   p.workers = g.workers;
   const bool fast = (g.M % kTile == 0) && (g.N % kTile == 0) &&
-                    (g.K % kBK == 0) && aligned_to(g.A, 16) &&
+                    (g.K % DefaultCfg::BK == 0) && aligned_to(g.A, 16) &&
                     aligned_to(g.B, 16) && p.c_vec_ok && !g.force_masked;
   int mode = 1;
   if (fast)

@@ -10,16 +10,17 @@
 // docs/Gfx950StreamKSameKernelReductionDesign.md:33-101 protocol).
 //
 // Design (one CTA = one 256x256 output tile, 4 waves of 64 lanes):
-//  * K is consumed 64 elements at a time.  Each stage holds A and B tiles of
-//    256 rows x 128 bytes (32 KiB each) in LDS; two stages double-buffer the
-//    K loop (128 KiB of the 160 KiB LDS).
+//  * K is consumed BK (32 or 64) elements per LDS stage.  A stage holds A and
+//    B tiles of 256 rows x 2*BK bytes; NSTAGE stages form a ring (BK=32 x 4
+//    or BK=64 x 2 = 128 KiB of the 160 KiB LDS), so the DMA for stage i+3
+//    (resp. i+1) is in flight while stage i is multiplied.
 //  * Aligned shapes fill LDS with global_load_lds_dwordx4 (no VGPR staging);
 //    ragged shapes stage through VGPRs with bounds checks and zero fill.
-//  * LDS rows are 8 chunks of 16 bytes; chunk c of row r is stored at
-//    position c ^ swz(r), swz(r) = (r ^ (r >> 3)) & 7, so the 16 rows read by
-//    one ds_read_b128 quarter-wave hit distinct banks for both 32- and
-//    64-bank LDS models.  The swizzle is applied on the global side of the
-//    DMA (lane l fetches the chunk that belongs at LDS slot l).
+//  * LDS rows are BK/8 chunks of 16 bytes; chunk c of row r is stored at
+//    c ^ swz(r) so the rows read together by one ds_read_b128 hit distinct
+//    banks (rocprofv3 SQ_LDS_BANK_CONFLICT = 0).  The swizzle is applied on
+//    the global side of the DMA (lane l fetches the chunk that belongs at
+//    LDS slot l).
 //  * Each wave owns a 128x128 sub-tile = 4x4 MFMA 32x32x16 tiles (256 fp32
 //    accumulators per lane).  MFMA operands are chosen so that each lane's
 //    4 consecutive accumulator registers are 4 consecutive elements of C's
@@ -32,20 +33,46 @@
 #include "gemm.hpp"
 #include "wave_common.hpp"
 
+#ifndef WAVE_GEMM_BK
+#define WAVE_GEMM_BK 32
+#endif
+#ifndef WAVE_GEMM_NSTAGE
+#define WAVE_GEMM_NSTAGE 4
+#endif
+
 namespace wave {
 namespace gemm {
 
 constexpr int kTile = 256;
-constexpr int kBK = 64;
-constexpr int kRowBytes = kBK * 2;                 // 128
-constexpr int kOperandBytes = kTile * kRowBytes;   // 32 KiB
-constexpr int kStageBytes = 2 * kOperandBytes;     // 64 KiB
-constexpr int kSmemBytes = 2 * kStageBytes;        // 128 KiB
 constexpr int kThreads = 256;
 constexpr int kTileElems = kTile * kTile;
+constexpr int kSKUnit = 64;  // Stream-K work unit: 64 K elements of one tile
 
-__device__ __forceinline__ uint32_t swz(uint32_t row) {
-  return (row ^ (row >> 3)) & 7u;
+// LDS ring geometry for BK elements of K per stage and NSTAGE stages.
+template <int BK_, int NSTAGE_> struct Cfg {
+  static constexpr int BK = BK_;
+  static constexpr int NSTAGE = NSTAGE_;
+  static constexpr int RB = BK * 2;              // bytes per operand row
+  static constexpr int CPR = BK / 8;             // 16-byte chunks per row
+  static constexpr int KS = BK / 16;             // MFMA K slices per stage
+  static constexpr int OPB = kTile * RB;         // bytes per operand tile
+  static constexpr int STAGE = 2 * OPB;          // A + B
+  static constexpr int SMEM = NSTAGE * STAGE;
+  static constexpr int DMA = OPB / 1024 / 4;     // DMA issues per wave per operand
+  static constexpr int ROWS_PER_DMA = 1024 / RB; // rows filled by one issue
+  static_assert(SMEM <= 160 * 1024, "LDS ring exceeds 160 KiB");
+};
+using DefaultCfg = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE>;
+
+// Chunk swizzle.  8 chunks/row: 16 consecutive rows (one 64-bank pass or
+// two 32-bank passes of ds_read_b128) get distinct 16-byte slots.  4
+// chunks/row (64-byte rows, two rows per 128 bytes): same property with the
+// row parity / row%4 taken into account.
+template <int CPR> __device__ __forceinline__ uint32_t swz(uint32_t row) {
+  if constexpr (CPR == 8)
+    return (row ^ (row >> 3)) & 7u;
+  else
+    return ((row >> 1) ^ (row >> 3)) & 3u;
 }
 
 struct Params {
@@ -112,8 +139,9 @@ __device__ __forceinline__ u32x4 load_chunk(const uint16_t *row, int k, int K) {
   return v;
 }
 
-// Accumulate C-tile (m0, n0) over K stages [kt_begin, kt_end) into acc.
-template <int IN_DT, bool COL_MAJOR, bool MASKED, int VEC>
+// Accumulate C-tile (m0, n0) over K steps [kt_begin, kt_end) (in units of
+// C::BK elements) into acc.
+template <class C, int IN_DT, bool COL_MAJOR, bool MASKED, int VEC>
 __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
                                          int kt_begin, int kt_end,
                                          uint8_t *smem, f32x16 (&acc)[4][4]) {
@@ -123,8 +151,8 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
   const uint32_t wp = COL_MAJOR ? wave_m : wave_n;
   const uint32_t wq = COL_MAJOR ? wave_n : wave_m;
   // P operand (rows of the MFMA result) comes from B for row-major C.
-  constexpr uint32_t kPBuf = COL_MAJOR ? 0 : kOperandBytes;
-  constexpr uint32_t kQBuf = COL_MAJOR ? kOperandBytes : 0;
+  constexpr uint32_t kPBuf = COL_MAJOR ? 0 : C::OPB;
+  constexpr uint32_t kQBuf = COL_MAJOR ? C::OPB : 0;
 
   // Fragment read offsets: row r of the operand tile, chunk (2*kk + hi).
   uint32_t poff[4], pswz[4], qoff[4], qswz[4];
@@ -132,126 +160,177 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
   for (int t = 0; t < 4; ++t) {
     const uint32_t pr = wp * 128 + t * 32 + (lane & 31);
     const uint32_t qr = wq * 128 + t * 32 + (lane & 31);
-    poff[t] = kPBuf + pr * kRowBytes;
-    qoff[t] = kQBuf + qr * kRowBytes;
-    pswz[t] = swz(pr) ^ (lane >> 5);
-    qswz[t] = swz(qr) ^ (lane >> 5);
+    poff[t] = kPBuf + pr * C::RB;
+    qoff[t] = kQBuf + qr * C::RB;
+    pswz[t] = swz<C::CPR>(pr) ^ (lane >> 5);
+    qswz[t] = swz<C::CPR>(qr) ^ (lane >> 5);
   }
 
   // Fragments of one 16-wide K slice: 4 P tiles + 4 Q tiles, 16 bytes each.
   struct Frag {
     u32x4 p[4], q[4];
   };
-  auto read_frags = [&](Frag &f, uint32_t stage, int kk) {
-    const uint8_t *s = smem + stage * kStageBytes;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      f.p[t] = *reinterpret_cast<const u32x4 *>(
-          s + poff[t] + (((uint32_t)(2 * kk) ^ pswz[t]) << 4));
-      f.q[t] = *reinterpret_cast<const u32x4 *>(
-          s + qoff[t] + (((uint32_t)(2 * kk) ^ qswz[t]) << 4));
-    }
+  // Fragment j of a slice: j = 0..3 -> Q tile j, j = 4..7 -> P tile j-4.
+  auto read_one = [&](Frag &f, uint32_t stage, int kk, int j) {
+    const uint8_t *s = smem + stage * C::STAGE;
+    const uint32_t x = (uint32_t)(2 * kk);
+    if (j < 4)
+      f.q[j] = *reinterpret_cast<const u32x4 *>(s + qoff[j] + ((x ^ qswz[j]) << 4));
+    else
+      f.p[j - 4] = *reinterpret_cast<const u32x4 *>(s + poff[j - 4] +
+                                                    ((x ^ pswz[j - 4]) << 4));
   };
-  auto mma = [&](const Frag &f) {
+  auto read_frags = [&](Frag &f, uint32_t stage, int kk) {
 #pragma unroll
-    for (int tp = 0; tp < 4; ++tp)
+    for (int j = 0; j < 8; ++j)
+      read_one(f, stage, kk, j);
+  };
+  // One K slice as 4 explicitly ordered groups: group tp issues the LDS
+  // reads of next-slice fragments 2tp, 2tp+1 (Q tiles first: the next
+  // slice's first MFMA row needs all four), the 4 MFMAs of P row tp, and
+  // hook(tp) (the DMA issues assigned to that group).  sched_barrier keeps
+  // the compiler from regrouping them, so DMA and LDS traffic stay spread
+  // through the MFMA stream.
+  auto step = [&](const Frag &cur, Frag &nxt, bool read, uint32_t nstage,
+                  int nkk, auto hook) {
+#pragma unroll
+    for (int tp = 0; tp < 4; ++tp) {
+      if (read) {
+        read_one(nxt, nstage, nkk, 2 * tp);
+        read_one(nxt, nstage, nkk, 2 * tp + 1);
+      }
 #pragma unroll
       for (int tq = 0; tq < 4; ++tq)
-        acc[tp][tq] = mfma32x32x16<IN_DT>(f.p[tp], f.q[tq], acc[tp][tq]);
-  };
-  // Interleave the 8 fragment reads of the next slice with the 16 MFMAs of
-  // the current one (1 LDS read : 2 MFMAs).
-  auto interleave = [&]() {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+        acc[tp][tq] = mfma32x32x16<IN_DT>(cur.p[tp], cur.q[tq], acc[tp][tq]);
+      hook(tp);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
-  // Slices 0..2 of `stage`, prefetching slices 1..3.  On return f[1] holds
-  // slice 3, which the caller multiplies after the stage barrier while the
-  // next stage's slice 0 is read into f[0].
+  auto no_hook = [](int) {};
+  // Slices 0..KS-2 of `stage`, prefetching slices 1..KS-1.  On return
+  // f[kLast] holds the last slice, which the caller multiplies after the
+  // stage barrier while the next stage's slice 0 is read into f[0].
   Frag f[2];
-  auto body = [&](uint32_t stage) {
+  constexpr int kLast = (C::KS - 1) & 1;
+  auto body_h = [&](uint32_t stage, auto hook) {
 #pragma unroll
-    for (int kk = 0; kk < 3; ++kk) {
-      read_frags(f[(kk + 1) & 1], stage, kk + 1);
-      mma(f[kk & 1]);
-      interleave();
-    }
+    for (int kk = 0; kk + 1 < C::KS; ++kk)
+      step(f[kk & 1], f[(kk + 1) & 1], true, stage, kk + 1,
+           [&](int tp) { hook(kk * 4 + tp); });
   };
+  auto body = [&](uint32_t stage) { body_h(stage, no_hook); };
 
   const int nk = kt_end - kt_begin;
   if (nk <= 0)
     return;
 
   if constexpr (!MASKED) {
-    // Global byte offsets of this lane's 8 DMA chunks (same for A and B).
+    // Global byte offsets of this lane's DMA chunks (same for A and B).
     const uint32_t rowbytes = (uint32_t)p.K * 2u;
-    uint32_t goff[8];
+    uint32_t goff[C::DMA];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t r = wave * 64 + i * 8 + (lane >> 3);
-      goff[i] = r * rowbytes + (((lane & 7) ^ swz(r)) << 4);
+    for (int i = 0; i < C::DMA; ++i) {
+      const uint32_t r = (wave * C::DMA + i) * C::ROWS_PER_DMA + lane / C::CPR;
+      goff[i] = r * rowbytes + (((lane % C::CPR) ^ swz<C::CPR>(r)) << 4);
     }
     const char *a_tile =
         reinterpret_cast<const char *>(p.A) + (size_t)m0 * rowbytes;
     const char *b_tile =
         reinterpret_cast<const char *>(p.B) + (size_t)n0 * rowbytes;
-    const uint32_t lds0 = lds_addr(smem) + wave * 8 * 1024;
-    auto issue = [&](uint32_t stage, int kt) {
-      const char *ab = a_tile + (size_t)kt * kRowBytes;
-      const char *bb = b_tile + (size_t)kt * kRowBytes;
-      const uint32_t l = lds0 + stage * kStageBytes;
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        dma16(l + i * 1024, ab, goff[i]);
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        dma16(l + kOperandBytes + i * 1024, bb, goff[i]);
+    const uint32_t lds0 = lds_addr(smem) + wave * C::DMA * 1024;
+    // DMA d of one stage (0 <= d < 2*DMA): A chunks first, then B.
+    auto issue_one = [&](uint32_t stage, int kt, int d) {
+      const uint32_t l = lds0 + stage * C::STAGE;
+      if (d < C::DMA)
+        dma16(l + d * 1024, a_tile + (size_t)kt * C::RB, goff[d]);
+      else
+        dma16(l + C::OPB + (d - C::DMA) * 1024, b_tile + (size_t)kt * C::RB,
+              goff[d - C::DMA]);
     };
-    issue(0, kt_begin);
+    auto issue = [&](uint32_t stage, int kt) {
+#pragma unroll
+      for (int d = 0; d < 2 * C::DMA; ++d)
+        issue_one(stage, kt, d);
+    };
+    // Steady-state DMA schedule: the D2 issues of the prefetched stage are
+    // spread over the G1 MFMA row groups before the stage barrier and (with
+    // three or more stages) the G2 = 4 groups after it: issue d follows
+    // group d*G/D2.  At the barrier of iteration i stage i+1 must be
+    // complete; issued after it are stages i+2 .. i+NSTAGE-2 and the P
+    // pre-barrier issues of stage i+NSTAGE-1, hence vmcnt(D2*(NSTAGE-3)+P).
+    constexpr int D2 = 2 * C::DMA;
+    constexpr int G1 = (C::KS - 1) * 4;
+    constexpr int G2 = C::NSTAGE >= 3 ? 4 : 0;
+    constexpr int G = G1 + G2;
+    constexpr int P = (G1 * D2 + G - 1) / G;  // #d with d*G/D2 < G1
+    constexpr int kVm = D2 * (C::NSTAGE - 3) + P;
+    static_assert(kVm >= 0 && kVm < 64, "vmcnt budget");
+    auto issue_groups = [&](uint32_t stage, int kt, int g) {
+#pragma unroll
+      for (int d = 0; d < D2; ++d)
+        if (d * G / D2 == g)
+          issue_one(stage, kt, d);
+    };
+    // Prologue: stages 0 .. NSTAGE-2 in flight, wait for stage 0.
+#pragma unroll
+    for (int s = 0; s + 1 < C::NSTAGE; ++s)
+      if (s < nk)
+        issue(s, kt_begin + s);
     vm_wait_barrier();
     read_frags(f[0], 0, 0);
-    // All but the last stage: the next stage's DMA is issued unconditionally
-    // so it shares a basic block with (and is scheduled among) the MFMAs.
-    for (int i = 0; i + 1 < nk; ++i) {
-      const uint32_t stage = i & 1;
-      issue(stage ^ 1, kt_begin + i + 1);
+    uint32_t stage = 0;
+    int i = 0;
+    for (; i + C::NSTAGE - 1 < nk; ++i) {
+      const uint32_t ahead = (stage + C::NSTAGE - 1) % C::NSTAGE;
+      const int kt_ahead = kt_begin + i + C::NSTAGE - 1;
+      body_h(stage, [&](int g) { issue_groups(ahead, kt_ahead, g); });
+      if constexpr (G1 == 0 || G2 == 0) {
+        // All issues fit before the barrier (or none did): none pending.
+        if constexpr (G1 == 0)
+          issue(ahead, kt_ahead);
+      }
+      vm_wait_barrier<kVm>();
+      stage = (stage + 1) % C::NSTAGE;
+      step(f[kLast], f[0], true, stage, 0,
+           [&](int tp) { issue_groups(ahead, kt_ahead, G1 + tp); });
+    }
+    // Drain: nothing more to issue; wait for everything.
+    for (; i + 1 < nk; ++i) {
       body(stage);
       vm_wait_barrier();
-      read_frags(f[0], stage ^ 1, 0);
-      mma(f[1]);
-      interleave();
+      stage = (stage + 1) % C::NSTAGE;
+      step(f[kLast], f[0], true, stage, 0, no_hook);
     }
-    body((nk - 1) & 1);
-    mma(f[1]);
+    body(stage);
+    step(f[kLast], f[0], false, 0, 0, no_hook);
     vm_wait_barrier();
   } else {
-    // VGPR-staged loads with bounds checks (ragged M/N/K, unaligned K).
-    const uint16_t *arow[8], *brow[8];
-    int kcol[8];
+    // VGPR-staged loads with bounds checks (ragged M/N/K, unaligned K);
+    // two LDS stages, the next stage held in VGPRs during the current one.
+    constexpr int kChunks = C::DMA;  // per operand per thread
+    const uint16_t *arow[kChunks], *brow[kChunks];
+    int kcol[kChunks];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = wave * 64 + i * 8 + (lane >> 3);
-      kcol[i] = (int)(((lane & 7) ^ swz(r)) * 8);
+    for (int i = 0; i < kChunks; ++i) {
+      const int r = (wave * C::DMA + i) * C::ROWS_PER_DMA + lane / C::CPR;
+      kcol[i] = (int)(((lane % C::CPR) ^ swz<C::CPR>(r)) * 8);
       arow[i] = (m0 + r < p.M) ? p.A + (size_t)(m0 + r) * p.K : nullptr;
       brow[i] = (n0 + r < p.N) ? p.B + (size_t)(n0 + r) * p.K : nullptr;
     }
-    u32x4 ra[8], rb[8];
+    u32x4 ra[kChunks], rb[kChunks];
     auto load = [&](int kt) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        ra[i] = load_chunk<VEC>(arow[i], kt * kBK + kcol[i], p.K);
-        rb[i] = load_chunk<VEC>(brow[i], kt * kBK + kcol[i], p.K);
+      for (int i = 0; i < kChunks; ++i) {
+        ra[i] = load_chunk<VEC>(arow[i], kt * C::BK + kcol[i], p.K);
+        rb[i] = load_chunk<VEC>(brow[i], kt * C::BK + kcol[i], p.K);
       }
     };
     auto store = [&](uint32_t stage) {
-      uint8_t *s = smem + stage * kStageBytes + (wave * 8 * 1024) + lane * 16;
+      uint8_t *s = smem + stage * C::STAGE + (wave * C::DMA * 1024) + lane * 16;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < kChunks; ++i) {
         *reinterpret_cast<u32x4 *>(s + i * 1024) = ra[i];
-        *reinterpret_cast<u32x4 *>(s + kOperandBytes + i * 1024) = rb[i];
+        *reinterpret_cast<u32x4 *>(s + C::OPB + i * 1024) = rb[i];
       }
     };
     load(kt_begin);
@@ -266,9 +345,7 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       if (i + 1 < nk)
         store(stage ^ 1);
       lds_barrier();
-      if (i + 1 < nk)
-        read_frags(f[0], stage ^ 1, 0);
-      mma(f[1]);
+      step(f[kLast], f[0], i + 1 < nk, stage ^ 1, 0, no_hook);
     }
   }
 }
@@ -335,7 +412,8 @@ __device__ __forceinline__ void store_tile(const Params &p, int m0, int n0,
 
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
 __global__ __launch_bounds__(kThreads, 1) void tiled_kernel(Params p) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes];
+  using C = DefaultCfg;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::SMEM];
   int tm, tn;
   tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, true, tm, tn);
   const int m0 = tm * kTile, n0 = tn * kTile;
@@ -345,8 +423,8 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_kernel(Params p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       acc[i][j] = f32x16{};
-  const int kt_n = (p.K + kBK - 1) / kBK;
-  mainloop<IN_DT, COL_MAJOR, MASKED, VEC>(p, m0, n0, 0, kt_n, smem, acc);
+  const int kt_n = (p.K + C::BK - 1) / C::BK;
+  mainloop<C, IN_DT, COL_MAJOR, MASKED, VEC>(p, m0, n0, 0, kt_n, smem, acc);
   store_tile<OUT_DT, COL_MAJOR, MASKED>(p, m0, n0, [&](int tp, int tq, int g) {
     return f32x4{acc[tp][tq][4 * g], acc[tp][tq][4 * g + 1],
                  acc[tp][tq][4 * g + 2], acc[tp][tq][4 * g + 3]};
@@ -354,7 +432,7 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------- Stream-K
-// Work unit = (tile, 64-wide K stage); W = T * I units split into `workers`
+// Work unit = (tile, 64-wide K step); W = T * I units split into `workers`
 // contiguous intervals (wave_matmul.py:88-101): worker w owns
 // [w*q + min(w, r), +q + (w < r)) with q = W / workers, r = W % workers.
 struct Interval {
@@ -389,11 +467,14 @@ __device__ __forceinline__ int sk_slot(int total, int workers, int w, int tile,
 // reducing are fully coalesced and need no coordinate math.
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
 __global__ __launch_bounds__(kThreads, 1) void streamk_kernel(Params p) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes];
+  using C = DefaultCfg;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::SMEM];
   __shared__ int arrival;
   const int worker = blockIdx.x;
   const int tiles = p.tiles_m * p.tiles_n;
-  const int iters = (p.K + kBK - 1) / kBK;
+  const int iters = (p.K + kSKUnit - 1) / kSKUnit;
+  const int ksteps = (p.K + C::BK - 1) / C::BK;  // mainloop steps per tile
+  constexpr int kStepsPerUnit = kSKUnit / C::BK;
   const int total = tiles * iters;
   const Interval iv = sk_interval(total, p.workers, worker);
   const bool aligned = (total % p.workers == 0) && ((total / p.workers) % iters == 0);
@@ -410,8 +491,8 @@ __global__ __launch_bounds__(kThreads, 1) void streamk_kernel(Params p) {
     int tm, tn;
     tile_coords(tile, p.tiles_m, p.tiles_n, p.group_m, false, tm, tn);
     zero();
-    mainloop<IN_DT, COL_MAJOR, MASKED, VEC>(p, tm * kTile, tn * kTile, 0,
-                                            iters, smem, acc);
+    mainloop<C, IN_DT, COL_MAJOR, MASKED, VEC>(p, tm * kTile, tn * kTile, 0,
+                                               ksteps, smem, acc);
     store_tile<OUT_DT, COL_MAJOR, MASKED>(
         p, tm * kTile, tn * kTile, [&](int tp, int tq, int g) {
           return f32x4{acc[tp][tq][4 * g], acc[tp][tq][4 * g + 1],
@@ -440,8 +521,9 @@ __global__ __launch_bounds__(kThreads, 1) void streamk_kernel(Params p) {
     int tm, tn;
     tile_coords(tile, p.tiles_m, p.tiles_n, p.group_m, false, tm, tn);
     zero();
-    mainloop<IN_DT, COL_MAJOR, MASKED, VEC>(p, tm * kTile, tn * kTile, kb, ke,
-                                            smem, acc);
+    mainloop<C, IN_DT, COL_MAJOR, MASKED, VEC>(
+        p, tm * kTile, tn * kTile, kb * kStepsPerUnit,
+        min(ke * kStepsPerUnit, ksteps), smem, acc);
     // Publish this worker's fp32 partial.
     float *mine = p.scratch + ((size_t)worker * 2 + slot) * kTileElems;
 #pragma unroll

@@ -62,8 +62,12 @@ __device__ __forceinline__ void dma16(uint32_t lds, const void *base,
 // Wait until this wave's outstanding vector-memory operations (including the
 // LDS DMA above) have completed, then join the workgroup barrier.  The asm
 // memory clobber also stops the compiler moving LDS accesses across it.
-__device__ __forceinline__ void vm_wait_barrier() {
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+// VMCNT: how many of this wave's most recent vector-memory operations may
+// still be in flight (DMA issued in order completes in order).
+template <int VMCNT = 0> __device__ __forceinline__ void vm_wait_barrier() {
+  static_assert(VMCNT >= 0 && VMCNT < 64, "vmcnt field is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(VMCNT)
+               : "memory");
 }
 
 __device__ __forceinline__ void lds_barrier() {

@@ -73,15 +73,20 @@ def cpu_baseline(a_bits, b_bits, M, N, K, budget_s):
     bounded sample of rows of the same 8192^3 problem."""
     from oracle import oracle
     threads = max(1, min(len(os.sched_getaffinity(0)), 16))
-    rows = 8
-    t0 = time.perf_counter()
-    oracle.gemm_nt_rows(a_bits, b_bits, 0, rows, oracle.F16, threads=threads)
-    dt = time.perf_counter() - t0
-    # scale the sample to roughly `budget_s` of CPU work
-    rows = int(min(M, max(rows, rows * budget_s / max(dt, 1e-3))))
-    t0 = time.perf_counter()
-    oracle.gemm_nt_rows(a_bits, b_bits, 0, rows, oracle.F16, threads=threads)
-    dt = time.perf_counter() - t0
+    rows, dt = 8, 0.0
+    while True:  # grow the sample until it takes >= 1 s, then scale to budget
+        t0 = time.perf_counter()
+        oracle.gemm_nt_rows(a_bits, b_bits, 0, rows, oracle.F16, threads=threads)
+        dt = time.perf_counter() - t0
+        if dt >= 1.0 or rows >= M:
+            break
+        rows = min(M, rows * 4)
+    target = int(min(M, rows * budget_s / dt))
+    if target > rows:
+        rows = target
+        t0 = time.perf_counter()
+        oracle.gemm_nt_rows(a_bits, b_bits, 0, rows, oracle.F16, threads=threads)
+        dt = time.perf_counter() - t0
     return {"value": round(2.0 * rows * N * K / dt / 1e12, 6), "unit": "TFLOP/s",
             "cores": threads, "kind": "port",
             "sample": f"rows 0..{rows - 1} of C (={rows}x{N}x{K}) of the 8192^3 f16 GEMM, "
@@ -96,6 +101,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fa", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--workload", choices=["all", "gemm", "fa", "copy"], default="all",
+                    help="gemm / fa: run only that kernel (for profiler passes); copy: "
+                         "a 1 GiB device copy used to calibrate rocprofv3 byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -110,6 +118,15 @@ def main():
     log(f"device: {torch.cuda.get_device_name(0)} CUs={cus} clock={clock_mhz:.0f} MHz "
         f"derived f16 MFMA peak={peak_dev:.1f} TFLOP/s")
 
+    if args.workload == "copy":
+        src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        ms = time_launches(lambda: dst.copy_(src), args.steps, args.warmup, torch)
+        log(f"copy 1 GiB: {ms:.3f} ms, {2 * 4 * src.numel() / (ms * 1e-3) / 1e9:.0f} GB/s")
+        return
+    if args.workload == "fa":
+        args.no_cpu = True
+
     M = N = K = 8192
     g = torch.Generator(device="cpu").manual_seed(7)
     a_h = (torch.rand((M, K), generator=g) * 2 - 1).to(torch.float16)
@@ -120,13 +137,16 @@ def main():
     def step():
         wave.gemm(a, b, out_dtype=torch.float16, out=c)
 
-    ms = time_launches(step, args.steps, args.warmup, torch)
+    ms = time_launches(step, args.steps if args.workload != "fa" else 1,
+                       args.warmup if args.workload != "fa" else 0, torch)
     flops = 2.0 * M * N * K
     tflops = flops / (ms * 1e-3) / 1e12
     log(f"gemm f16 8192^3: {ms * 1e3:.1f} us/launch, {tflops:.1f} TFLOP/s "
         f"({100 * tflops / MFMA_PEAK_TFLOPS:.1f}% of {MFMA_PEAK_TFLOPS})")
 
     secondary = []
+    if args.workload == "gemm":
+        args.no_fa = True
     if not args.no_fa:
         B, H, S, D = 4, 32, 4096, 128
         gq = torch.Generator(device="cpu").manual_seed(11)
