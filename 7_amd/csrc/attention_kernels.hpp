@@ -23,7 +23,12 @@
 //  * K tiles (64 keys x 256 B) arrive by global_load_lds_dwordx4 with an XOR
 //    swizzle (chunk c of row r at c ^ (r & 15)); V tiles are loaded into
 //    VGPRs one tile ahead, transposed in registers and written to LDS as
-//    V^T rows of 64 keys (+16 B padding, 144 B pitch).  Two stages.
+//    V^T rows of 64 keys (+16 B padding, 144 B pitch).  Two buffers each;
+//    K runs one tile ahead of V (see the pipeline below).
+//  * Software pipeline inside each wave: the MFMAs of S(t+1) are
+//    interleaved with the exp2 VALU work of tile t, and the PV MFMAs of
+//    tile t with the row max of tile t+1, so the matrix pipe and the VALU
+//    stay busy at the same time.
 //  * exp2 with the scale folded into one FMA; the running max is only
 //    raised (and O rescaled) when a tile's max exceeds it by more than 8
 //    (log2 units), as in the reference's lazy rescale
@@ -44,7 +49,6 @@ constexpr int kKRowBytes = kD * 2;               // 256
 constexpr int kKBytes = kBN * kKRowBytes;        // 16 KiB
 constexpr int kVtPitch = kBN * 2 + 16;           // 144 B per d row of V^T
 constexpr int kVtBytes = kD * kVtPitch;          // 18 KiB
-constexpr int kStageBytes = kKBytes + kVtBytes;  // 34 KiB
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleThreshold = 8.0f;
 
@@ -74,7 +78,9 @@ __device__ __forceinline__ void block_coords(const Params &p, int &bh, int &qb) 
 template <int DT, int NW>
 __global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(Params p) {
   static_assert(NW == 4, "V^T transpose mapping assumes 256 threads");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStageBytes];
+  // LDS: K ring [2][64 keys][256 B] (XOR-swizzled chunks), then the V^T
+  // ring [2][128 d][144 B].
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kKBytes + 2 * kVtBytes];
   constexpr int kRows = 32 * NW;
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63;
@@ -85,7 +91,8 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(Params p) {
   const int hkv = hq / (p.q_heads / p.kv_heads);
   const uint16_t *Qh = p.Q + ((size_t)bh * p.seq_q) * kD;
   const uint16_t *Kh = p.K + ((size_t)(b * p.kv_heads + hkv) * p.seq_k) * kD;
-  const uint16_t *Vh = p.V + ((size_t)(b * p.kv_heads + hkv) * p.seq_k) * kD;
+  const char *Vh =
+      reinterpret_cast<const char *>(p.V + ((size_t)(b * p.kv_heads + hkv) * p.seq_k) * kD);
   uint16_t *Oh = p.O + ((size_t)bh * p.seq_q) * kD;
 
   const int q0 = qb * kRows;
@@ -109,7 +116,8 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(Params p) {
     kend = min(kend, q0 + kRows);
   const int ntiles = (kend + kBN - 1) / kBN;
 
-  // K DMA: wave w fills rows 16w .. 16w+15 of the tile (4 x 1 KiB).
+  // K DMA: wave w fills rows 16w .. 16w+15 of the tile (4 x 1 KiB).  Rows
+  // past seq_k re-read the last key (masked out of the softmax).
   uint32_t kgoff[4];
   int krow[4];
 #pragma unroll
@@ -118,35 +126,34 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(Params p) {
     kgoff[i] = ((lane & 15) ^ (krow[i] & 15)) << 4;
   }
   const uint32_t lds0 = lds_addr(smem);
-  auto issue_k = [&](uint32_t stage, int kt) {
+  auto issue_k = [&](uint32_t buf, int kt) {
     const int k0 = kt * kBN;
-    const uint32_t l = lds0 + stage * kStageBytes + wave * 4 * 1024;
+    const uint32_t l = lds0 + buf * kKBytes + wave * 4 * 1024;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      // Rows past seq_k re-read the last key (masked out of the softmax).
       const int key = min(k0 + krow[i], p.seq_k - 1);
       dma16(l + i * 1024, Kh, (uint32_t)key * kKRowBytes + kgoff[i]);
     }
   };
 
-  // V: thread t loads keys 4g..4g+3 (g = t % 16) of d-chunk c = t / 16.
+  // V: thread t loads keys 4g..4g+3 (g = t % 16) of d-chunk c = t / 16 into
+  // VGPRs one tile ahead.  Keys past seq_k re-read the last key: their P is 0.
   const int vg = threadIdx.x & 15, vc = threadIdx.x >> 4;
   u32x4 vr[4];
   auto load_v = [&](int kt) {
     const int k0 = kt * kBN + 4 * vg;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int key = k0 + i;
-      vr[i] = key < p.seq_k
-                  ? *reinterpret_cast<const u32x4 *>(Vh + (size_t)key * kD + 8 * vc)
-                  : u32x4{0u, 0u, 0u, 0u};
+      const uint32_t key = (uint32_t)min(k0 + i, p.seq_k - 1);
+      vr[i] = *reinterpret_cast<const u32x4 *>(Vh + key * kKRowBytes + 16 * vc);
     }
   };
   // V^T position of key group g: 16-key group G = g/4 stored as
   // [0-3, 8-11, 4-7, 12-15].
   const int vpos = 16 * (vg >> 2) + 4 * ((vg & 1) * 2 + ((vg >> 1) & 1));
-  auto store_v = [&](uint32_t stage) {
-    uint8_t *s = smem + stage * kStageBytes + kKBytes + vpos * 2;
+  uint8_t *const vt0 = smem + 2 * kKBytes;
+  auto store_v = [&](uint32_t buf) {
+    uint8_t *s = vt0 + buf * kVtBytes + vpos * 2;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       // d = 8*vc + 2e (low halves) and 8*vc + 2e + 1 (high halves).
@@ -160,7 +167,6 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(Params p) {
     }
   };
 
-  // Fragment addressing (per lane).
   const uint32_t kr = lane & 31;                     // key row within block
   const uint32_t vt_row = (lane & 31) * kVtPitch;    // d row within d-tile
 
@@ -168,107 +174,236 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(Params p) {
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     o[i] = f32x16{};
+  // Row sums on the matrix pipe: ones[32 x 16] . P^T gives, in every
+  // accumulator register of lane l, the sum of P over the slice for query
+  // l%32.  Only register 0 is read (and rescaled); it sums exactly the
+  // 16-bit P values that multiply V.
+  f32x16 lacc = f32x16{};
+  const u32x4 ones = {kOnePair<DT>, kOnePair<DT>, kOnePair<DT>, kOnePair<DT>};
   float m = -__builtin_inff();
-  float lsum = 0.f;
   const float c = p.scale_log2;
 
-  if (ntiles > 0) {
-    issue_k(0, 0);
-    load_v(0);
-    store_v(0);
-    vm_wait_barrier();
-  }
-  for (int t = 0; t < ntiles; ++t) {
-    const uint32_t stage = t & 1;
-    const bool more = t + 1 < ntiles;
-    if (more) {
-      issue_k(stage ^ 1, t + 1);
-      load_v(t + 1);
-    }
-    const uint8_t *ks = smem + stage * kStageBytes;
-    const uint8_t *vs = ks + kKBytes;
-    const int k0 = t * kBN;
-    // Waves whose queries all precede the tile skip it (causal).
-    const bool active = !p.causal || k0 <= qw + 31;
-    if (active) {
-      // S^T = K . Q^T for 2 blocks of 32 keys.
-      f32x16 s[2];
+  // ---- stage primitives ---------------------------------------------------
+  // S^T = K . Q^T for the 2 blocks of 32 keys of the tile in K buffer kb.
+  auto s_mfma = [&](f32x16 (&sc)[2], uint32_t kb) {
+    const uint8_t *ks = smem + kb * kKBytes;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      sc[j] = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        s[j] = f32x16{};
         const uint32_t row = j * 32 + kr;
+        const uint32_t chunk = (2 * kk + half) ^ (row & 15);
+        const u32x4 kf =
+            *reinterpret_cast<const u32x4 *>(ks + row * kKRowBytes + (chunk << 4));
+        sc[j] = mfma32x32x16<DT>(kf, qf[kk], sc[j]);
+      }
+  };
+  // Masks of tile t: causal (key > query) and keys past seq_k.
+  auto mask = [&](f32x16 (&sc)[2], int t) {
+    const int k0 = t * kBN;
+    const bool edge = (k0 + kBN > p.seq_k) || (p.causal && k0 + kBN - 1 > qw);
+    if (edge) {
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-          const uint32_t chunk = (2 * kk + half) ^ (row & 15);
-          const u32x4 kf =
-              *reinterpret_cast<const u32x4 *>(ks + row * kKRowBytes + (chunk << 4));
-          s[j] = mfma32x32x16<DT>(kf, qf[kk], s[j]);
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + 32 * j + 8 * (r >> 2) + 4 * half + (r & 3);
+          if (key >= p.seq_k || (p.causal && key > my_q))
+            sc[j][r] = -__builtin_inff();
+        }
+    }
+  };
+  auto rowmax = [&](const f32x16 (&sc)[2]) {
+    float mx = sc[0][0];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        mx = fmaxf(mx, sc[j][r]);
+    return fmaxf(mx, __shfl_xor(mx, 32)) * c;
+  };
+  // Lazy rescale: raise the running max only when it grows by > 8 (log2).
+  auto update_max = [&](float mx) {
+    const bool need = mx > m + kRescaleThreshold;
+    if (__builtin_amdgcn_ballot_w64(need)) {
+      const float mn = fmaxf(m, mx);
+      const float alpha = (m == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(m - mn);
+      m = mn;
+      lacc[0] *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        o[i] *= alpha;
+    }
+  };
+  // P = exp2(s*c - m), packed to 16 bits as the B operand of O^T += V^T P^T.
+  auto exp_pack = [&](const f32x16 (&sc)[2], u32x4 (&pf)[2][2]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][8 * sl + 2 * e], c, -m));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][8 * sl + 2 * e + 1], c, -m));
+          pf[j][sl][e] = pack2<DT>(p0, p1);
+        }
+  };
+  // O^T += V^T . P^T over 4 d-tiles x 4 key slices (V^T buffer vb), and the
+  // row sums alongside.
+  auto pv_mfma = [&](const u32x4 (&pf)[2][2], uint32_t vb) {
+    const uint8_t *vs = vt0 + vb * kVtBytes;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl) {
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const u32x4 vf = *reinterpret_cast<const u32x4 *>(
+              vs + dt * 32 * kVtPitch + vt_row + (16 * (2 * j + sl) + 8 * half) * 2);
+          o[dt] = mfma32x32x16<DT>(vf, pf[j][sl], o[dt]);
+        }
+        lacc = mfma32x32x16<DT>(ones, pf[j][sl], lacc);
+      }
+  };
+
+  // ---- fused pipeline phases ----------------------------------------------
+  // pin(x): an empty asm use, so x is computed in the step that produces it
+  // (without it, IR-level sinking moves the VALU work next to its uses).
+  auto pin = [](auto x) { asm volatile("" ::"v"(x)); };
+  // Each phase is written as explicit steps of one MFMA plus a share of the
+  // VALU work of the other tile; sched_barrier keeps the steps in order so
+  // the two pipes overlap.  LDS fragment reads run 4 steps ahead.
+  //
+  // Phase 1: S(t+1) = K(t+1) . Q^T (16 MFMAs) with P(t) = exp2(S(t)*c - m)
+  // packed to 16 bits (2 elements per step).
+  auto phase1 = [&](f32x16 (&sn)[2], uint32_t kb, const f32x16 (&sc)[2],
+                    u32x4 (&pf)[2][2]) {
+    const uint8_t *ks = smem + kb * kKBytes;
+    auto kfrag = [&](int i) {  // i = 2*kk + j
+      const uint32_t row = (i & 1) * 32 + kr;
+      const uint32_t chunk = (2 * (i >> 1) + half) ^ (row & 15);
+      return *reinterpret_cast<const u32x4 *>(ks + row * kKRowBytes + (chunk << 4));
+    };
+    u32x4 kf[16];
+    sn[0] = f32x16{};
+    sn[1] = f32x16{};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      kf[i] = kfrag(i);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i + 4 < 16)
+        kf[i + 4] = kfrag(i + 4);
+      sn[i & 1] = mfma32x32x16<DT>(kf[i], qf[i >> 1], sn[i & 1]);
+      const int j = i >> 3, r = (2 * i) & 15;
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][r], c, -m));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][r + 1], c, -m));
+      pf[j][r >> 3][(r & 7) >> 1] = pack2<DT>(p0, p1);
+      pin(pf[j][r >> 3][(r & 7) >> 1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // Phase 2: O^T += V(t)^T . P(t)^T and the row sums (20 MFMAs) with the
+  // row max of S(t+1) and the register transpose of V(t+1) for its LDS
+  // store.  Returns the scaled row max of S(t+1).
+  auto phase2 = [&](const u32x4 (&pf)[2][2], uint32_t vb, const f32x16 (&sn)[2],
+                    bool with_next) {
+    const uint8_t *vs = vt0 + vb * kVtBytes;
+    auto vfrag = [&](int i) {  // i = 4*(2*j + sl) + dt
+      const int g = i >> 2, dt = i & 3;
+      return *reinterpret_cast<const u32x4 *>(vs + dt * 32 * kVtPitch + vt_row +
+                                              (16 * g + 8 * half) * 2);
+    };
+    u32x4 vf[16];
+    float mx = -__builtin_inff();
+    uint32_t tr[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      vf[i] = vfrag(i);
+#pragma unroll
+    for (int q = 0; q < 20; ++q) {
+      const int g = q / 5, w = q % 5;
+      const u32x4 &pb = pf[g >> 1][g & 1];
+      if (w < 4) {
+        const int i = 4 * g + w;
+        if (i + 4 < 16)
+          vf[i + 4] = vfrag(i + 4);
+        o[w] = mfma32x32x16<DT>(vf[i], pb, o[w]);
+      } else {
+        lacc = mfma32x32x16<DT>(ones, pb, lacc);
+      }
+      if (with_next) {
+        // 32 S values -> 16 max3 steps, then 16 perms of the V transpose.
+        if (q < 16) {
+          mx = __builtin_fmaxf(__builtin_fmaxf(mx, sn[q >> 3][(2 * q) & 15]),
+                               sn[q >> 3][((2 * q) & 15) + 1]);
+          pin(mx);
+        }
+        if (q >= 4) {
+          const int e = (q - 4) >> 2, k = (q - 4) & 3;
+          // k: 0 lo01, 1 lo23, 2 hi01, 3 hi23 of dword e
+          const int a = (k & 1) ? 3 : 1, b2 = (k & 1) ? 2 : 0;
+          tr[q - 4] = __builtin_amdgcn_perm(vr[a][e], vr[b2][e],
+                                            (k & 2) ? 0x07060302u : 0x05040100u);
+          pin(tr[q - 4]);
         }
       }
-      // Masks: causal (key > query) and keys past seq_k.
-      const bool edge = (k0 + kBN > p.seq_k) || (p.causal && k0 + kBN - 1 > qw);
-      if (edge) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = k0 + 32 * j + 8 * (r >> 2) + 4 * half + (r & 3);
-            if (key >= p.seq_k || (p.causal && key > my_q))
-              s[j][r] = -__builtin_inff();
-          }
-      }
-      float mx = s[0][0];
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          mx = fmaxf(mx, s[j][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      mx *= c;
-      // Lazy rescale: raise the running max only when it grows by > 8.
-      const bool need = mx > m + kRescaleThreshold;
-      if (__builtin_amdgcn_ballot_w64(need)) {
-        const float mn = fmaxf(m, mx);
-        const float alpha = (m == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(m - mn);
-        m = mn;
-        lsum *= alpha;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          o[i] *= alpha;
-      }
-      // P = exp2(s*c - m), packed to 16 bits as the B operand of O^T += V^T P^T.
-      u32x4 pf[2][2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int sl = 0; sl < 2; ++sl)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][8 * sl + 2 * e], c, -m));
-            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][8 * sl + 2 * e + 1], c, -m));
-            lsum += p0 + p1;
-            pf[j][sl][e] = pack2<DT>(p0, p1);
-          }
-      // O^T += V^T . P^T over 4 d-tiles x 4 key slices.
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int sl = 0; sl < 2; ++sl) {
-            const u32x4 vf = *reinterpret_cast<const u32x4 *>(
-                vs + dt * 32 * kVtPitch + vt_row + (16 * (2 * j + sl) + 8 * half) * 2);
-            o[dt] = mfma32x32x16<DT>(vf, pf[j][sl], o[dt]);
-          }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (more)
-      store_v(stage ^ 1);
+    if (with_next) {
+      uint8_t *sv = vt0 + (vb ^ 1) * kVtBytes + vpos * 2;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d = 8 * vc + 2 * e;
+        *reinterpret_cast<u32x2 *>(sv + d * kVtPitch) = u32x2{tr[4 * e], tr[4 * e + 1]};
+        *reinterpret_cast<u32x2 *>(sv + (d + 1) * kVtPitch) =
+            u32x2{tr[4 * e + 2], tr[4 * e + 3]};
+      }
+    }
+    return fmaxf(mx, __shfl_xor(mx, 32)) * c;
+  };
+
+  // ---- software pipeline over key tiles --------------------------------------
+  // Iteration t: the matrix pipe computes S(t+1) while the VALU turns S(t)
+  // into P(t) (phase 1), then the matrix pipe computes O += V(t) P(t) while
+  // the VALU reduces S(t+1) to its row max and transposes V(t+1) (phase 2).
+  // K runs one tile ahead of V: K(t+2) and V(t+1) are loaded during
+  // iteration t into the buffers that K(t) and V(t-1) left.
+  f32x16 sc[2], sn[2];
+  u32x4 pf[2][2];
+  issue_k(0, 0);
+  load_v(0);
+  vm_wait_barrier();
+  if (ntiles > 1)
+    issue_k(1, 1);
+  s_mfma(sc, 0);
+  store_v(0);
+  mask(sc, 0);
+  update_max(rowmax(sc));
+  vm_wait_barrier();
+  for (int t = 0; t + 1 < ntiles; ++t) {
+    const uint32_t cur = t & 1, nxt = cur ^ 1;
+    load_v(t + 1);
+    if (t + 2 < ntiles)
+      issue_k(cur, t + 2);
+    phase1(sn, nxt, sc, pf);
+    mask(sn, t + 1);
+    const float mx = phase2(pf, cur, sn, true);
+    update_max(mx);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      sc[j] = sn[j];
     vm_wait_barrier();
   }
+  exp_pack(sc, pf);
+  pv_mfma(pf, (ntiles - 1) & 1);
+  const float lsum = lacc[0];
 
   // Normalise and store O[my_q][d], d = 32*dt + 8*(r/4) + 4*half + r%4.
-  const float ltot = lsum + __shfl_xor(lsum, 32);
-  const float inv = ltot > 0.f ? 1.0f / ltot : 0.f;
+  const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
   if (my_q < p.seq_q) {
     uint16_t *orow = Oh + (size_t)my_q * kD + 4 * half;
 #pragma unroll

@@ -93,9 +93,20 @@ template <int DT> __device__ __forceinline__ float from_bits(uint16_t v) {
     return __builtin_bit_cast(float, (uint32_t)v << 16);
 }
 
-// Pack two floats into one dword of 16-bit values (lo, hi), RNE.
+// Pack two floats into one dword of 16-bit values (lo, hi), RNE: one
+// v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 template <int DT> __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return (uint32_t)to_bits<DT>(lo) | ((uint32_t)to_bits<DT>(hi) << 16);
+  const f32x2 v = {lo, hi};
+  if constexpr (DT == kF16)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
+
+// 16-bit bit pattern of 1.0 in both halves of a dword.
+template <int DT> constexpr uint32_t kOnePair = DT == kF16 ? 0x3C003C00u : 0x3F803F80u;
 
 } // namespace wave
