@@ -59,21 +59,41 @@ template <int BK_, int NSTAGE_> struct Cfg {
   static constexpr int STAGE = 2 * OPB;          // A + B
   static constexpr int SMEM = NSTAGE * STAGE;
   static constexpr int DMA = OPB / 1024 / 4;     // DMA issues per wave per operand
-  static constexpr int ROWS_PER_DMA = 1024 / RB; // rows filled by one issue
+  static_assert(OPB == 128 * 128 * (BK / 32), "super-row layout covers BK 32/64");
   static_assert(SMEM <= 160 * 1024, "LDS ring exceeds 160 KiB");
 };
 using DefaultCfg = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE>;
 
-// Chunk swizzle.  8 chunks/row: 16 consecutive rows (one 64-bank pass or
-// two 32-bank passes of ds_read_b128) get distinct 16-byte slots.  4
-// chunks/row (64-byte rows, two rows per 128 bytes): same property with the
-// row parity / row%4 taken into account.
-template <int CPR> __device__ __forceinline__ uint32_t swz(uint32_t row) {
-  if constexpr (CPR == 8)
-    return (row ^ (row >> 3)) & 7u;
-  else
-    return ((row >> 1) ^ (row >> 3)) & 3u;
-}
+// LDS geometry of an operand tile.  The tile is stored as 128-byte
+// "super-rows" of eight 16-byte slots: with BK = 64 super-row R is tile row
+// R; with BK = 32 it holds row R in slots 0-3 and row R + 128 in slots 4-7.
+// Logical slot lc of super-row R lives at physical slot lc ^ swz8(R), so the
+// 16 rows read together by a ds_read_b128 (one logical chunk, consecutive
+// rows) land in 16 distinct 16-byte bank groups: rocprofv3 reports
+// SQ_LDS_BANK_CONFLICT = 0 for this layout, while 64-byte rows with a
+// 2-bit swizzle measured one conflict cycle per LDS cycle.
+__device__ __forceinline__ uint32_t swz8(uint32_t R) { return (R ^ (R >> 3)) & 7u; }
+
+template <class C> struct Geo {
+  // (tile row, 16-byte chunk) -> (super-row, logical slot)
+  static __device__ __forceinline__ uint32_t super_row(uint32_t row) {
+    return C::CPR == 8 ? row : (row & 127u);
+  }
+  static __device__ __forceinline__ uint32_t slot_base(uint32_t row) {
+    return C::CPR == 8 ? 0u : ((row >> 7) << 2);
+  }
+  // Inverse, for the loaders: physical slot p of super-row R holds tile row
+  // row_of(R, p) chunk chunk_of(R, p).
+  static __device__ __forceinline__ uint32_t logical(uint32_t R, uint32_t p) {
+    return p ^ swz8(R);
+  }
+  static __device__ __forceinline__ uint32_t row_of(uint32_t R, uint32_t p) {
+    return C::CPR == 8 ? R : R + 128u * (logical(R, p) >> 2);
+  }
+  static __device__ __forceinline__ uint32_t chunk_of(uint32_t R, uint32_t p) {
+    return C::CPR == 8 ? logical(R, p) : (logical(R, p) & 3u);
+  }
+};
 
 struct Params {
   const uint16_t *A;
@@ -160,10 +180,12 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
   for (int t = 0; t < 4; ++t) {
     const uint32_t pr = wp * 128 + t * 32 + (lane & 31);
     const uint32_t qr = wq * 128 + t * 32 + (lane & 31);
-    poff[t] = kPBuf + pr * C::RB;
-    qoff[t] = kQBuf + qr * C::RB;
-    pswz[t] = swz<C::CPR>(pr) ^ (lane >> 5);
-    qswz[t] = swz<C::CPR>(qr) ^ (lane >> 5);
+    // slot = (slot_base + 2*kk + hi) ^ swz8(R) = (2*kk) ^ [slot_base ^ hi ^ swz8(R)]
+    const uint32_t pR = Geo<C>::super_row(pr), qR = Geo<C>::super_row(qr);
+    poff[t] = kPBuf + pR * 128u;
+    qoff[t] = kQBuf + qR * 128u;
+    pswz[t] = swz8(pR) ^ Geo<C>::slot_base(pr) ^ (lane >> 5);
+    qswz[t] = swz8(qR) ^ Geo<C>::slot_base(qr) ^ (lane >> 5);
   }
 
   // Fragments of one 16-wide K slice: 4 P tiles + 4 Q tiles, 16 bytes each.
@@ -230,8 +252,9 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
     uint32_t goff[C::DMA];
 #pragma unroll
     for (int i = 0; i < C::DMA; ++i) {
-      const uint32_t r = (wave * C::DMA + i) * C::ROWS_PER_DMA + lane / C::CPR;
-      goff[i] = r * rowbytes + (((lane % C::CPR) ^ swz<C::CPR>(r)) << 4);
+      // Lane l of DMA issue i fills physical slot l%8 of super-row R.
+      const uint32_t R = (wave * C::DMA + i) * 8 + (lane >> 3), ps = lane & 7;
+      goff[i] = Geo<C>::row_of(R, ps) * rowbytes + (Geo<C>::chunk_of(R, ps) << 4);
     }
     const char *a_tile =
         reinterpret_cast<const char *>(p.A) + (size_t)m0 * rowbytes;
@@ -312,8 +335,9 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
     int kcol[kChunks];
 #pragma unroll
     for (int i = 0; i < kChunks; ++i) {
-      const int r = (wave * C::DMA + i) * C::ROWS_PER_DMA + lane / C::CPR;
-      kcol[i] = (int)(((lane % C::CPR) ^ swz<C::CPR>(r)) * 8);
+      const uint32_t R = (wave * C::DMA + i) * 8 + (lane >> 3), ps = lane & 7;
+      const int r = (int)Geo<C>::row_of(R, ps);
+      kcol[i] = (int)(Geo<C>::chunk_of(R, ps) * 8);
       arow[i] = (m0 + r < p.M) ? p.A + (size_t)(m0 + r) * p.K : nullptr;
       brow[i] = (n0 + r < p.N) ? p.B + (size_t)(n0 + r) * p.K : nullptr;
     }
