@@ -14,7 +14,7 @@
 //                   [--dtype f16|bf16] [--causal] [--iters N] [--warmup N]
 //                   [--repeats R] [--seed S]
 //
-// Parity is checked by the test suite against the CPU oracle, not here.
+// Parity is checked by the test suite, not here.
 // Exit codes follow the runners: 2 for bad arguments, 1 for HIP failures.
 #include "../../include/wave_runtime.h"
 
