@@ -24,8 +24,18 @@ hipError_t launch_fwd(const FwdArgs &a, hipStream_t stream) {
   p.causal = a.causal;
   const float scale = a.scale > 0.f ? a.scale : 1.0f / std::sqrt((float)a.head_dim);
   p.scale_log2 = scale * kLog2e;
-  const dim3 grid(p.q_blocks * a.batch * a.q_heads);
   const dim3 block(64 * kWaves);
+  if (a.variant == 1) {
+    // 4 waves x 64 query rows per CTA
+    p.q_blocks = (a.seq_q + 255) / 256;
+    const dim3 grid(p.q_blocks * a.batch * a.q_heads);
+    if (a.dtype == kF16)
+      hipLaunchKernelGGL((fwd64_kernel<kF16>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((fwd64_kernel<kBF16>), grid, block, 0, stream, p);
+    return hipGetLastError();
+  }
+  const dim3 grid(p.q_blocks * a.batch * a.q_heads);
   if (a.dtype == kF16)
     hipLaunchKernelGGL((fwd_kernel<kF16, kWaves>), grid, block, 0, stream, p);
   else

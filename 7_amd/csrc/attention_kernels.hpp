@@ -417,5 +417,318 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(Params p) {
   }
 }
 
+// ------------------------------------------------------------------------
+// fwd64_kernel: 4 waves x 64 query rows (two 32-row query blocks per wave),
+// 32-key tiles, one CTA per CU.  Each K and V^T fragment read from LDS feeds
+// two MFMAs (one per query block), halving LDS read traffic per MFMA
+// relative to fwd_kernel.  Same per-lane softmax orientation, V^T key
+// permutation, MFMA row sums, lazy rescale and two-phase intra-wave
+// pipeline.  K: 3-buffer LDS ring (DMA two tiles ahead); V: loaded one tile
+// ahead into VGPRs with explicitly counted loads, transposed into a 2-buffer
+// V^T ring with an 80-byte pitch (16 consecutive d rows -> distinct banks).
+constexpr int kBN2 = 32;                            // keys per tile
+constexpr int kK2Bytes = kBN2 * kKRowBytes;         // 8 KiB
+constexpr int kVt2Pitch = kBN2 * 2 + 16;            // 80 B per d row of V^T
+constexpr int kVt2Bytes = kD * kVt2Pitch;           // 10 KiB
+constexpr int kKRing = 3;
+
+// Global load of 16 bytes per lane whose completion the caller waits for
+// with vm_wait_regs (the compiler does not track it).
+__device__ __forceinline__ u32x4 gload16(const void *base, uint32_t voff) {
+  u32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(v) : "v"(voff), "s"(base));
+  return v;
+}
+// s_waitcnt vmcnt(N) that also "redefines" a and b, so no use of them can be
+// scheduled before the wait.
+template <int N>
+__device__ __forceinline__ void vm_wait_regs(u32x4 &a, u32x4 &b) {
+  asm volatile("s_waitcnt vmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N) : "memory");
+}
+
+template <int DT>
+__global__ __launch_bounds__(256, 1) void fwd64_kernel(Params p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kKRing * kK2Bytes + 2 * kVt2Bytes];
+  constexpr int kRows = 256;
+  const uint32_t wave = uniform(threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t half = lane >> 5;
+  int bh, qb_idx;
+  block_coords<4>(p, bh, qb_idx);
+  const int b = bh / p.q_heads, hq = bh - b * p.q_heads;
+  const int hkv = hq / (p.q_heads / p.kv_heads);
+  const uint16_t *Qh = p.Q + ((size_t)bh * p.seq_q) * kD;
+  const char *Kh = reinterpret_cast<const char *>(
+      p.K + ((size_t)(b * p.kv_heads + hkv) * p.seq_k) * kD);
+  const char *Vh = reinterpret_cast<const char *>(
+      p.V + ((size_t)(b * p.kv_heads + hkv) * p.seq_k) * kD);
+  uint16_t *Oh = p.O + ((size_t)bh * p.seq_q) * kD;
+
+  const int q0 = qb_idx * kRows;
+  const int qw = q0 + wave * 64;  // this wave's first query
+  int my_q[2];
+  my_q[0] = qw + (lane & 31);
+  my_q[1] = qw + 32 + (lane & 31);
+
+  // Q^T fragments of both query blocks.
+  u32x4 qf[2][8];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const bool ok = my_q[g] < p.seq_q;
+    const uint16_t *qrow = Qh + (size_t)(ok ? my_q[g] : 0) * kD + 8 * half;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+      qf[g][kk] = ok ? *reinterpret_cast<const u32x4 *>(qrow + 16 * kk)
+                     : u32x4{0u, 0u, 0u, 0u};
+  }
+
+  int kend = p.seq_k;
+  if (p.causal)
+    kend = min(kend, q0 + kRows);
+  const int ntiles = (kend + kBN2 - 1) / kBN2;
+
+  // K DMA: wave w fills rows 8w .. 8w+7 of the 32-row tile (2 x 1 KiB).
+  uint32_t kgoff[2];
+  int krow[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    krow[i] = (wave * 2 + i) * 4 + (lane >> 4);
+    kgoff[i] = ((lane & 15) ^ (krow[i] & 15)) << 4;
+  }
+  const uint32_t lds0 = lds_addr(smem);
+  auto issue_k = [&](uint32_t buf, int kt) {
+    const uint32_t l = lds0 + buf * kK2Bytes + wave * 2 * 1024;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int key = min(kt * kBN2 + krow[i], p.seq_k - 1);
+      dma16(l + i * 1024, Kh, (uint32_t)key * kKRowBytes + kgoff[i]);
+    }
+  };
+  // V: thread t loads keys 2g, 2g+1 (g = t % 16) of d-chunk c = t / 16.
+  const int vg = threadIdx.x & 15, vc = threadIdx.x >> 4;
+  u32x4 vr[2];
+  auto load_v = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t key = (uint32_t)min(kt * kBN2 + 2 * vg + i, p.seq_k - 1);
+      vr[i] = gload16(Vh, key * kKRowBytes + 16 * vc);
+    }
+  };
+  // V^T position of keys 2g, 2g+1: 16-key groups stored as [0-3,8-11,4-7,12-15].
+  const int vk = (2 * vg) & 15;
+  const int vpos = 16 * (vg >> 3) + (vk < 4 ? vk : vk < 8 ? vk + 4 : vk < 12 ? vk - 4 : vk);
+  uint8_t *const vt0 = smem + kKRing * kK2Bytes;
+  uint32_t tr[8];
+  auto transpose_v = [&](int e) {  // dword e: d = 8*vc + 2e (lo), +1 (hi)
+    tr[2 * e] = __builtin_amdgcn_perm(vr[1][e], vr[0][e], 0x05040100u);
+    tr[2 * e + 1] = __builtin_amdgcn_perm(vr[1][e], vr[0][e], 0x07060302u);
+  };
+  auto store_vt = [&](uint32_t buf) {
+    uint8_t *s = vt0 + buf * kVt2Bytes + vpos * 2;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int d = 8 * vc + 2 * e;
+      *reinterpret_cast<uint32_t *>(s + d * kVt2Pitch) = tr[2 * e];
+      *reinterpret_cast<uint32_t *>(s + (d + 1) * kVt2Pitch) = tr[2 * e + 1];
+    }
+  };
+
+  const uint32_t kr = lane & 31;
+  const uint32_t vt_row = (lane & 31) * kVt2Pitch;
+  f32x16 o[2][4];
+  f32x16 lacc[2];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    lacc[g] = f32x16{};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o[g][i] = f32x16{};
+  }
+  const u32x4 ones = {kOnePair<DT>, kOnePair<DT>, kOnePair<DT>, kOnePair<DT>};
+  float m[2] = {-__builtin_inff(), -__builtin_inff()};
+  const float c = p.scale_log2;
+  auto pin = [](auto x) { asm volatile("" ::"v"(x)); };
+
+  auto kfrag = [&](uint32_t kb, int kk) {
+    const uint32_t chunk = (2 * kk + half) ^ (kr & 15);
+    return *reinterpret_cast<const u32x4 *>(smem + kb * kK2Bytes + kr * kKRowBytes +
+                                            (chunk << 4));
+  };
+  auto mask = [&](f32x16 (&sc)[2], int t) {
+    const int k0 = t * kBN2;
+    const bool edge = (k0 + kBN2 > p.seq_k) || (p.causal && k0 + kBN2 - 1 > qw);
+    if (edge) {
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
+          if (key >= p.seq_k || (p.causal && key > my_q[g]))
+            sc[g][r] = -__builtin_inff();
+        }
+    }
+  };
+  auto update_max = [&](int g, float mx) {
+    const bool need = mx > m[g] + kRescaleThreshold;
+    if (__builtin_amdgcn_ballot_w64(need)) {
+      const float mn = fmaxf(m[g], mx);
+      const float alpha = (m[g] == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(m[g] - mn);
+      m[g] = mn;
+      lacc[g][0] *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        o[g][i] *= alpha;
+    }
+  };
+  auto rowmax = [&](const f32x16 &s) {
+    float mx = s[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r)
+      mx = fmaxf(mx, s[r]);
+    return fmaxf(mx, __shfl_xor(mx, 32)) * c;
+  };
+
+  // Phase 1: S(t+1) (16 MFMAs: 8 K fragments x 2 query blocks) with
+  // P(t) = exp2(S(t)*c - m) (2 elements per step).
+  u32x4 pf[2][2];
+  auto phase1 = [&](f32x16 (&sn)[2], uint32_t kb, const f32x16 (&sc)[2]) {
+    u32x4 kf[8];
+    sn[0] = f32x16{};
+    sn[1] = f32x16{};
+    kf[0] = kfrag(kb, 0);
+    kf[1] = kfrag(kb, 1);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int kk = i >> 1, g = i & 1;
+      if (g == 0 && kk + 2 < 8)
+        kf[kk + 2] = kfrag(kb, kk + 2);
+      sn[g] = mfma32x32x16<DT>(kf[kk], qf[g][kk], sn[g]);
+      const int e = 2 * i, eg = e >> 4, r = e & 15;
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[eg][r], c, -m[eg]));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[eg][r + 1], c, -m[eg]));
+      pf[eg][r >> 3][(r & 7) >> 1] = pack2<DT>(p0, p1);
+      pin(pf[eg][r >> 3][(r & 7) >> 1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // Phase 2: O^T += V^T(t) P^T(t) and row sums (20 MFMAs) with the row max
+  // of S(t+1) and the transpose of V(t+1).  Returns both scaled maxima.
+  float mxo[2];
+  auto phase2 = [&](uint32_t vb, const f32x16 (&sn)[2], bool with_next) {
+    const uint8_t *vs = vt0 + vb * kVt2Bytes;
+    auto vfrag = [&](int sl, int dt) {
+      return *reinterpret_cast<const u32x4 *>(vs + dt * 32 * kVt2Pitch + vt_row +
+                                              (16 * sl + 8 * half) * 2);
+    };
+    u32x4 vf[8];
+    float mx[2] = {-__builtin_inff(), -__builtin_inff()};
+    vf[0] = vfrag(0, 0);
+    vf[1] = vfrag(0, 1);
+    int q = 0;
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) {
+#pragma unroll
+      for (int x = 0; x < 5; ++x) {
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          if (x < 4) {
+            const int fi = sl * 4 + x;
+            if (g == 0 && fi + 2 < 8)
+              vf[fi + 2] = vfrag((fi + 2) >> 2, (fi + 2) & 3);
+            o[g][x] = mfma32x32x16<DT>(vf[fi], pf[g][sl], o[g][x]);
+          } else {
+            lacc[g] = mfma32x32x16<DT>(ones, pf[g][sl], lacc[g]);
+          }
+          if (with_next) {
+            if (q < 16) {
+              const int mg = q >> 3, r = (2 * q) & 15;
+              mx[mg] = __builtin_fmaxf(__builtin_fmaxf(mx[mg], sn[mg][r]), sn[mg][r + 1]);
+              pin(mx[mg]);
+            } else {
+              transpose_v(q - 16);
+              pin(tr[2 * (q - 16)]);
+              pin(tr[2 * (q - 16) + 1]);
+            }
+          }
+          ++q;
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    mxo[0] = fmaxf(mx[0], __shfl_xor(mx[0], 32)) * c;
+    mxo[1] = fmaxf(mx[1], __shfl_xor(mx[1], 32)) * c;
+  };
+
+  // ---- pipeline -----------------------------------------------------------
+  f32x16 sc[2], sn[2];
+  issue_k(0, 0);
+  load_v(0);
+  vm_wait_regs<0>(vr[0], vr[1]);
+  lds_barrier();
+  issue_k(1, min(1, ntiles - 1));
+  issue_k(2, min(2, ntiles - 1));
+  {
+    // S(0), first row maxima, V^T(0).
+    sc[0] = f32x16{};
+    sc[1] = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const u32x4 kf = kfrag(0, kk);
+      sc[0] = mfma32x32x16<DT>(kf, qf[0][kk], sc[0]);
+      sc[1] = mfma32x32x16<DT>(kf, qf[1][kk], sc[1]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      transpose_v(e);
+    store_vt(0);
+    mask(sc, 0);
+    update_max(0, rowmax(sc[0]));
+    update_max(1, rowmax(sc[1]));
+  }
+  vm_wait_barrier<2>();
+  for (int t = 0; t + 1 < ntiles; ++t) {
+    const uint32_t vcur = t & 1;
+    load_v(t + 1);
+    issue_k(t % kKRing, min(t + 3, ntiles - 1));
+    phase1(sn, (t + 1) % kKRing, sc);
+    mask(sn, t + 1);
+    vm_wait_regs<2>(vr[0], vr[1]);  // V(t+1) landed; K DMA may stay in flight
+    phase2(vcur, sn, true);
+    store_vt(vcur ^ 1);
+    update_max(0, mxo[0]);
+    update_max(1, mxo[1]);
+    sc[0] = sn[0];
+    sc[1] = sn[1];
+    vm_wait_barrier<2>();
+  }
+  // Last tile: P and O += V P.
+#pragma unroll
+  for (int e = 0; e < 32; e += 2) {
+    const int eg = e >> 4, r = e & 15;
+    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[eg][r], c, -m[eg]));
+    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[eg][r + 1], c, -m[eg]));
+    pf[eg][r >> 3][(r & 7) >> 1] = pack2<DT>(p0, p1);
+  }
+  phase2((ntiles - 1) & 1, sn, false);
+  vm_wait_barrier();
+
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const float lsum = lacc[g][0];
+    const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+    if (my_q[g] < p.seq_q) {
+      uint16_t *orow = Oh + (size_t)my_q[g] * kD + 4 * half;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg) {
+          const u32x2 w = {pack2<DT>(o[g][dt][4 * gg] * inv, o[g][dt][4 * gg + 1] * inv),
+                           pack2<DT>(o[g][dt][4 * gg + 2] * inv, o[g][dt][4 * gg + 3] * inv)};
+          *reinterpret_cast<u32x2 *>(orow + 32 * dt + 8 * gg) = w;
+        }
+    }
+  }
+}
+
 } // namespace attention
 } // namespace wave

@@ -39,30 +39,39 @@
 #ifndef WAVE_GEMM_NSTAGE
 #define WAVE_GEMM_NSTAGE 4
 #endif
+#ifndef WAVE_GEMM_WAVES
+#define WAVE_GEMM_WAVES 4
+#endif
 
 namespace wave {
 namespace gemm {
 
 constexpr int kTile = 256;
-constexpr int kThreads = 256;
 constexpr int kTileElems = kTile * kTile;
 constexpr int kSKUnit = 64;  // Stream-K work unit: 64 K elements of one tile
 
-// LDS ring geometry for BK elements of K per stage and NSTAGE stages.
-template <int BK_, int NSTAGE_> struct Cfg {
+// LDS ring geometry for BK elements of K per stage and NSTAGE stages, and
+// the wave grid: WAVES waves, WPN along P (the MFMA row / C-contiguous
+// dimension) x WQN along Q, each owning TP x TQ MFMA 32x32 tiles.
+template <int BK_, int NSTAGE_, int WAVES_> struct Cfg {
   static constexpr int BK = BK_;
   static constexpr int NSTAGE = NSTAGE_;
+  static constexpr int WAVES = WAVES_;
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int WPN = 2, WQN = WAVES / 2;
+  static constexpr int TP = 8 / WPN, TQ = 8 / WQN;
+  static_assert(TP == 4 && (TQ == 4 || TQ == 2), "4 or 8 waves");
   static constexpr int RB = BK * 2;              // bytes per operand row
   static constexpr int CPR = BK / 8;             // 16-byte chunks per row
   static constexpr int KS = BK / 16;             // MFMA K slices per stage
   static constexpr int OPB = kTile * RB;         // bytes per operand tile
   static constexpr int STAGE = 2 * OPB;          // A + B
   static constexpr int SMEM = NSTAGE * STAGE;
-  static constexpr int DMA = OPB / 1024 / 4;     // DMA issues per wave per operand
+  static constexpr int DMA = OPB / 1024 / WAVES; // DMA issues per wave per operand
   static_assert(OPB == 128 * 128 * (BK / 32), "super-row layout covers BK 32/64");
   static_assert(SMEM <= 160 * 1024, "LDS ring exceeds 160 KiB");
 };
-using DefaultCfg = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE>;
+using DefaultCfg = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE, WAVE_GEMM_WAVES>;
 
 // LDS geometry of an operand tile.  The tile is stored as 128-byte
 // "super-rows" of eight 16-byte slots: with BK = 64 super-row R is tile row
@@ -164,65 +173,70 @@ __device__ __forceinline__ u32x4 load_chunk(const uint16_t *row, int k, int K) {
 template <class C, int IN_DT, bool COL_MAJOR, bool MASKED, int VEC>
 __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
                                          int kt_begin, int kt_end,
-                                         uint8_t *smem, f32x16 (&acc)[4][4]) {
+                                         uint8_t *smem,
+                                         f32x16 (&acc)[C::TP][C::TQ]) {
+  constexpr int TP = C::TP, TQ = C::TQ, NREAD = TP + TQ;
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63;
-  const uint32_t wave_m = wave >> 1, wave_n = wave & 1;
-  const uint32_t wp = COL_MAJOR ? wave_m : wave_n;
-  const uint32_t wq = COL_MAJOR ? wave_n : wave_m;
+  const uint32_t wp = wave % C::WPN, wq = wave / C::WPN;
   // P operand (rows of the MFMA result) comes from B for row-major C.
   constexpr uint32_t kPBuf = COL_MAJOR ? 0 : C::OPB;
   constexpr uint32_t kQBuf = COL_MAJOR ? C::OPB : 0;
 
   // Fragment read offsets: row r of the operand tile, chunk (2*kk + hi).
-  uint32_t poff[4], pswz[4], qoff[4], qswz[4];
+  // slot = (slot_base + 2*kk + hi) ^ swz8(R) = (2*kk) ^ [slot_base ^ hi ^ swz8(R)]
+  uint32_t poff[TP], pswz[TP], qoff[TQ], qswz[TQ];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const uint32_t pr = wp * 128 + t * 32 + (lane & 31);
-    const uint32_t qr = wq * 128 + t * 32 + (lane & 31);
-    // slot = (slot_base + 2*kk + hi) ^ swz8(R) = (2*kk) ^ [slot_base ^ hi ^ swz8(R)]
-    const uint32_t pR = Geo<C>::super_row(pr), qR = Geo<C>::super_row(qr);
+  for (int t = 0; t < TP; ++t) {
+    const uint32_t pr = wp * (TP * 32) + t * 32 + (lane & 31);
+    const uint32_t pR = Geo<C>::super_row(pr);
     poff[t] = kPBuf + pR * 128u;
-    qoff[t] = kQBuf + qR * 128u;
     pswz[t] = swz8(pR) ^ Geo<C>::slot_base(pr) ^ (lane >> 5);
+  }
+#pragma unroll
+  for (int t = 0; t < TQ; ++t) {
+    const uint32_t qr = wq * (TQ * 32) + t * 32 + (lane & 31);
+    const uint32_t qR = Geo<C>::super_row(qr);
+    qoff[t] = kQBuf + qR * 128u;
     qswz[t] = swz8(qR) ^ Geo<C>::slot_base(qr) ^ (lane >> 5);
   }
 
-  // Fragments of one 16-wide K slice: 4 P tiles + 4 Q tiles, 16 bytes each.
+  // Fragments of one 16-wide K slice: TP P tiles + TQ Q tiles, 16 bytes each.
   struct Frag {
-    u32x4 p[4], q[4];
+    u32x4 p[TP], q[TQ];
   };
-  // Fragment j of a slice: j = 0..3 -> Q tile j, j = 4..7 -> P tile j-4.
+  // Fragment j of a slice: j < TQ -> Q tile j, else P tile j - TQ.
   auto read_one = [&](Frag &f, uint32_t stage, int kk, int j) {
     const uint8_t *s = smem + stage * C::STAGE;
     const uint32_t x = (uint32_t)(2 * kk);
-    if (j < 4)
+    if (j < TQ)
       f.q[j] = *reinterpret_cast<const u32x4 *>(s + qoff[j] + ((x ^ qswz[j]) << 4));
     else
-      f.p[j - 4] = *reinterpret_cast<const u32x4 *>(s + poff[j - 4] +
-                                                    ((x ^ pswz[j - 4]) << 4));
+      f.p[j - TQ] = *reinterpret_cast<const u32x4 *>(s + poff[j - TQ] +
+                                                     ((x ^ pswz[j - TQ]) << 4));
   };
   auto read_frags = [&](Frag &f, uint32_t stage, int kk) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < NREAD; ++j)
       read_one(f, stage, kk, j);
   };
-  // One K slice as 4 explicitly ordered groups: group tp issues the LDS
-  // reads of next-slice fragments 2tp, 2tp+1 (Q tiles first: the next
-  // slice's first MFMA row needs all four), the 4 MFMAs of P row tp, and
-  // hook(tp) (the DMA issues assigned to that group).  sched_barrier keeps
-  // the compiler from regrouping them, so DMA and LDS traffic stay spread
-  // through the MFMA stream.
+  // One K slice as TP explicitly ordered groups: group tp issues its share
+  // of the LDS reads of the next slice's fragments (Q tiles first: the next
+  // slice's first MFMA row needs all of them), the TQ MFMAs of P row tp,
+  // and hook(tp) (the DMA issues assigned to that group).  sched_barrier
+  // keeps the compiler from regrouping them, so DMA and LDS traffic stay
+  // spread through the MFMA stream.
   auto step = [&](const Frag &cur, Frag &nxt, bool read, uint32_t nstage,
                   int nkk, auto hook) {
 #pragma unroll
-    for (int tp = 0; tp < 4; ++tp) {
+    for (int tp = 0; tp < TP; ++tp) {
       if (read) {
-        read_one(nxt, nstage, nkk, 2 * tp);
-        read_one(nxt, nstage, nkk, 2 * tp + 1);
+#pragma unroll
+        for (int j = tp * NREAD / TP; j < (tp + 1) * NREAD / TP; ++j)
+          read_one(nxt, nstage, nkk, j);
       }
 #pragma unroll
-      for (int tq = 0; tq < 4; ++tq)
+      for (int tq = 0; tq < TQ; ++tq)
         acc[tp][tq] = mfma32x32x16<IN_DT>(cur.p[tp], cur.q[tq], acc[tp][tq]);
       hook(tp);
       __builtin_amdgcn_sched_barrier(0);
@@ -395,24 +409,22 @@ __device__ __forceinline__ void store1(void *C, size_t idx, float v) {
 
 // Write one lane's share of the 256x256 tile at (m0, n0).  `get(tp,tq,g)`
 // returns the 4 values of accumulator group g of MFMA tile (tp, tq).
-template <int OUT_DT, bool COL_MAJOR, bool MASKED, typename Get>
+template <class C, int OUT_DT, bool COL_MAJOR, bool MASKED, typename Get>
 __device__ __forceinline__ void store_tile(const Params &p, int m0, int n0,
                                            Get get) {
   const uint32_t wave = threadIdx.x >> 6;
   const uint32_t lane = threadIdx.x & 63;
-  const uint32_t wave_m = wave >> 1, wave_n = wave & 1;
-  const int wp = COL_MAJOR ? wave_m : wave_n;
-  const int wq = COL_MAJOR ? wave_n : wave_m;
+  const int wp = wave % C::WPN, wq = wave / C::WPN;
   const int P0 = COL_MAJOR ? m0 : n0, Q0 = COL_MAJOR ? n0 : m0;
   const int Pext = COL_MAJOR ? p.M : p.N, Qext = COL_MAJOR ? p.N : p.M;
 #pragma unroll
-  for (int tq = 0; tq < 4; ++tq) {
-    const int q = Q0 + wq * 128 + tq * 32 + (lane & 31);
+  for (int tq = 0; tq < C::TQ; ++tq) {
+    const int q = Q0 + wq * (C::TQ * 32) + tq * 32 + (lane & 31);
 #pragma unroll
-    for (int tp = 0; tp < 4; ++tp) {
+    for (int tp = 0; tp < C::TP; ++tp) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int pp = P0 + wp * 128 + tp * 32 + 8 * g + 4 * (lane >> 5);
+        const int pp = P0 + wp * (C::TP * 32) + tp * 32 + 8 * g + 4 * (lane >> 5);
         const f32x4 v = get(tp, tq, g);
         const size_t idx = (size_t)q * p.ldc + pp;
         if constexpr (!MASKED) {
@@ -435,21 +447,21 @@ __device__ __forceinline__ void store_tile(const Params &p, int m0, int n0,
 }
 
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
-__global__ __launch_bounds__(kThreads, 1) void tiled_kernel(Params p) {
+__global__ __launch_bounds__(DefaultCfg::THREADS, 1) void tiled_kernel(Params p) {
   using C = DefaultCfg;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[C::SMEM];
   int tm, tn;
   tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, true, tm, tn);
   const int m0 = tm * kTile, n0 = tn * kTile;
-  f32x16 acc[4][4];
+  f32x16 acc[C::TP][C::TQ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < C::TP; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < C::TQ; ++j)
       acc[i][j] = f32x16{};
   const int kt_n = (p.K + C::BK - 1) / C::BK;
   mainloop<C, IN_DT, COL_MAJOR, MASKED, VEC>(p, m0, n0, 0, kt_n, smem, acc);
-  store_tile<OUT_DT, COL_MAJOR, MASKED>(p, m0, n0, [&](int tp, int tq, int g) {
+  store_tile<C, OUT_DT, COL_MAJOR, MASKED>(p, m0, n0, [&](int tp, int tq, int g) {
     return f32x4{acc[tp][tq][4 * g], acc[tp][tq][4 * g + 1],
                  acc[tp][tq][4 * g + 2], acc[tp][tq][4 * g + 3]};
   });
@@ -486,11 +498,11 @@ __device__ __forceinline__ int sk_slot(int total, int workers, int w, int tile,
   return first_whole ? 0 : 1;
 }
 
-// Per-thread scratch layout: element e (0..4095 of this thread's 256x256
-// share) of thread t lives at slot_base + e * 256 + t, so publishing and
-// reducing are fully coalesced and need no coordinate math.
+// Per-thread scratch layout: element e (0 .. 65536/THREADS - 1) of thread
+// t's share of the 256x256 tile lives at slot_base + e * THREADS + t, so
+// publishing and reducing are fully coalesced and need no coordinate math.
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
-__global__ __launch_bounds__(kThreads, 1) void streamk_kernel(Params p) {
+__global__ __launch_bounds__(DefaultCfg::THREADS, 1) void streamk_kernel(Params p) {
   using C = DefaultCfg;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[C::SMEM];
   __shared__ int arrival;
@@ -503,12 +515,13 @@ __global__ __launch_bounds__(kThreads, 1) void streamk_kernel(Params p) {
   const Interval iv = sk_interval(total, p.workers, worker);
   const bool aligned = (total % p.workers == 0) && ((total / p.workers) % iters == 0);
 
-  f32x16 acc[4][4];
+  constexpr int TP = C::TP, TQ = C::TQ, NT = C::THREADS;
+  f32x16 acc[TP][TQ];
   auto zero = [&]() {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TP; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < TQ; ++j)
         acc[i][j] = f32x16{};
   };
   auto whole_tile = [&](int tile) {
@@ -517,7 +530,7 @@ __global__ __launch_bounds__(kThreads, 1) void streamk_kernel(Params p) {
     zero();
     mainloop<C, IN_DT, COL_MAJOR, MASKED, VEC>(p, tm * kTile, tn * kTile, 0,
                                                ksteps, smem, acc);
-    store_tile<OUT_DT, COL_MAJOR, MASKED>(
+    store_tile<C, OUT_DT, COL_MAJOR, MASKED>(
         p, tm * kTile, tn * kTile, [&](int tp, int tq, int g) {
           return f32x4{acc[tp][tq][4 * g], acc[tp][tq][4 * g + 1],
                        acc[tp][tq][4 * g + 2], acc[tp][tq][4 * g + 3]};
@@ -551,12 +564,12 @@ __global__ __launch_bounds__(kThreads, 1) void streamk_kernel(Params p) {
     // Publish this worker's fp32 partial.
     float *mine = p.scratch + ((size_t)worker * 2 + slot) * kTileElems;
 #pragma unroll
-    for (int tp = 0; tp < 4; ++tp)
+    for (int tp = 0; tp < TP; ++tp)
 #pragma unroll
-      for (int tq = 0; tq < 4; ++tq)
+      for (int tq = 0; tq < TQ; ++tq)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          mine[((tp * 4 + tq) * 16 + r) * kThreads + threadIdx.x] = acc[tp][tq][r];
+          mine[((tp * TQ + tq) * 16 + r) * NT + threadIdx.x] = acc[tp][tq][r];
     ++slot;
     const int first_owner = sk_owner(total, p.workers, tile * iters);
     const int last_owner = sk_owner(total, p.workers, (tile + 1) * iters - 1);
@@ -572,7 +585,7 @@ __global__ __launch_bounds__(kThreads, 1) void streamk_kernel(Params p) {
     // Last arriver: reduce all contributors' partials in worker order (a
     // fixed order, so the result does not depend on arrival order).
     __threadfence();  // acquire the other workers' partials
-    store_tile<OUT_DT, COL_MAJOR, MASKED>(
+    store_tile<C, OUT_DT, COL_MAJOR, MASKED>(
         p, tm * kTile, tn * kTile, [&](int tp, int tq, int g) {
           f32x4 s = {0.f, 0.f, 0.f, 0.f};
           for (int c = first_owner; c <= last_owner; ++c) {
@@ -582,7 +595,7 @@ __global__ __launch_bounds__(kThreads, 1) void streamk_kernel(Params p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
               s[e] += __builtin_nontemporal_load(
-                  part + ((tp * 4 + tq) * 16 + 4 * g + e) * kThreads +
+                  part + ((tp * TQ + tq) * 16 + 4 * g + e) * NT +
                   threadIdx.x);
           }
           return s;
@@ -599,7 +612,7 @@ __global__ __launch_bounds__(kThreads, 1) void streamk_kernel(Params p) {
 // elements per global load.
 template <int IN_DT, int OUT_DT, bool CM, bool SK>
 hipError_t launch_variant(const Params &p, int mode, hipStream_t stream) {
-  const dim3 block(kThreads);
+  const dim3 block(DefaultCfg::THREADS);
   const dim3 grid(SK ? p.workers : p.tiles_m * p.tiles_n);
 #define WAVE_LAUNCH(MASKED, VEC)                                               \
   do {                                                                         \

@@ -137,8 +137,8 @@ template <typename F> double median_us(F launch, int iters, int warmup, int repe
     check_hip(hipEventElapsedTime(&ms, a, b), "elapsed");
     us.push_back(ms * 1000.0 / iters);
   }
-  hipEventDestroy(a);
-  hipEventDestroy(b);
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
   std::sort(us.begin(), us.end());
   return us[us.size() / 2];
 }
