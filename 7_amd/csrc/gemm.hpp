@@ -28,6 +28,9 @@ constexpr int kKStage = 64;
 int tiles_for(int extent);
 int k_iterations(int K);
 hipError_t launch(const GemmArgs &args, hipStream_t stream);
+// Short-M kernel (gemm_skinny.hip): M <= 128, K % 64 == 0, aligned.
+bool skinny_supported(const GemmArgs &args);
+hipError_t launch_skinny(const GemmArgs &args, hipStream_t stream);
 
 } // namespace gemm
 } // namespace wave

@@ -83,6 +83,8 @@ int tiles_for(int extent) { return (extent + kTile - 1) / kTile; }
 int k_iterations(int K) { return (K + kSKUnit - 1) / kSKUnit; }
 
 hipError_t launch(const GemmArgs &g, hipStream_t stream) {
+  if (g.workers == 0 && !g.force_masked && skinny_supported(g))
+    return launch_skinny(g, stream);
   Params p{};
   p.A = static_cast<const uint16_t *>(g.A);
   p.B = static_cast<const uint16_t *>(g.B);

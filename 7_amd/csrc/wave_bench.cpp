@@ -208,12 +208,12 @@ int run_gemm(Opts &o) {
       return 1;
     }
     std::printf("streamk_counter_check: passed\n");
-    hipFree(scratch);
-    hipFree(counters);
+    (void)hipFree(scratch);
+    (void)hipFree(counters);
   }
-  hipFree(A);
-  hipFree(B);
-  hipFree(C);
+  (void)hipFree(A);
+  (void)hipFree(B);
+  (void)hipFree(C);
   return 0;
 }
 
@@ -248,10 +248,10 @@ int run_fa(Opts &o) {
               o.str("--dtype", "f16").c_str(), causal);
   std::printf("per_launch_us: %.3f\n", us);
   std::printf("tflops: %.3f\n", flops / us * 1e-6);
-  hipFree(Q);
-  hipFree(Kd);
-  hipFree(V);
-  hipFree(O);
+  (void)hipFree(Q);
+  (void)hipFree(Kd);
+  (void)hipFree(V);
+  (void)hipFree(O);
   return 0;
 }
 

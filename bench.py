@@ -93,6 +93,39 @@ def cpu_baseline(a_bits, b_bits, M, N, K, budget_s):
                       f"{dt:.1f} s, oracle/oracle.cpp gemm_nt_rows"}
 
 
+def cpu_reference_path(M, N, K, budget_s):
+    """The reference runner's own CPU path (computeExpectedElement, scalar
+    float accumulation; wave-matmul-calibrate-runner.cpp:1586-1597), compiled
+    from the reference sources into oracle/_ref by oracle/Makefile, timed on
+    a few rows of the same 8192^3 f16 problem (its own bucket inputs, which
+    it generates for all of B first; generation is excluded from the timing
+    by subtracting a zero-row call)."""
+    import ctypes
+    path = os.path.join(ROOT, "oracle", "_ref", "libref_matmul.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    f = lib.ref_gemm_expected
+    f.argtypes = [ctypes.c_int] * 7 + [ctypes.c_void_p]
+    f.restype = None
+    rows = 1
+    out = np.empty((64, N), dtype=np.float64)
+    t0 = time.perf_counter()
+    f(0, N, K, 1, 7, 0, 1, out.ctypes.data)  # input generation only
+    gen = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    f(rows, N, K, 1, 7, 0, 1, out.ctypes.data)
+    dt = max(time.perf_counter() - t0 - gen, 1e-6)
+    rows = int(max(1, min(64, rows * budget_s / dt)))
+    t0 = time.perf_counter()
+    f(rows, N, K, 1, 7, 0, 1, out.ctypes.data)
+    dt = max(time.perf_counter() - t0 - gen, 1e-6)
+    return {"value": round(2.0 * rows * N * K / dt / 1e12, 6), "unit": "TFLOP/s",
+            "cores": 1, "kind": "reference",
+            "sample": f"rows 0..{rows - 1} (={rows}x{N}x{K}) through the reference runner's "
+                      f"computeExpectedElement, {dt:.1f} s excluding input generation"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -166,11 +199,15 @@ def main():
         del q, k, v, o
 
     cpu = None
+    ref_cpu = None
     if not args.no_cpu:
         a_bits = a_h.view(torch.int16).numpy().view(np.uint16)
         b_bits = b_h.view(torch.int16).numpy().view(np.uint16)
         cpu = cpu_baseline(a_bits, b_bits, M, N, K, args.cpu_budget)
         log(f"cpu baseline: {cpu['value']} TFLOP/s on {cpu['cores']} threads ({cpu['sample']})")
+        ref_cpu = cpu_reference_path(M, N, K, 6.0)
+        if ref_cpu:
+            log(f"reference CPU path: {ref_cpu['value']} TFLOP/s on 1 thread ({ref_cpu['sample']})")
 
     line = {
         "metric": "TFLOP/s + % gfx950 MFMA peak: f16 GEMM 8192^3, FA fwd S=4096 D=128",
@@ -193,6 +230,7 @@ def main():
                      "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
                      "traffic": read_traffic()},
         "cpu_baseline": cpu,
+        "cpu_reference_path": ref_cpu,
         "secondary": secondary,
         "device_derived_peak_tflops": round(peak_dev, 1),
     }

@@ -175,3 +175,16 @@ def test_repeat_launch_deterministic(wave, oracle, dev):
     for _ in range(5):
         again = wave.gemm(a, b, out_dtype=torch.float32)
         assert torch.equal(first, again)
+
+
+@pytest.mark.parametrize("dt", [1, 2])
+@pytest.mark.parametrize("out_dt", [0, 1, 2])
+@pytest.mark.parametrize("layout", ["row", "col"])
+@pytest.mark.parametrize("shape", [(128, 1024, 512), (1, 2048, 64), (100, 1056, 256),
+                                   (77, 3000, 128), (128, 8192, 1024)])
+def test_short_m_bucket_bit_exact(wave, oracle, dev, dt, out_dt, layout, shape):
+    """M <= 128 with K % 64 == 0 runs the short-M kernel (one CTA per 32
+    columns of N); bucket inputs make it bit-exact like the tiled path."""
+    M, N, K = shape
+    _, _, c, ref = run_gemm(wave, oracle, dev, M, N, K, dt, out_dt, layout, seed=13)
+    assert_exact(oracle, c, ref, out_dt)
