@@ -349,19 +349,19 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(Params p) {
           tr[q - 4] = __builtin_amdgcn_perm(vr[a][e], vr[b2][e],
                                             (k & 2) ? 0x07060302u : 0x05040100u);
           pin(tr[q - 4]);
+          // Dword e of the transpose is complete: store its two V^T rows
+          // now (the buffer's last reader, PV(t-1), finished before the
+          // previous barrier), so only 4 transposed registers are live.
+          if (k == 3) {
+            uint8_t *sv = vt0 + (vb ^ 1) * kVtBytes + vpos * 2;
+            const int d = 8 * vc + 2 * e;
+            *reinterpret_cast<u32x2 *>(sv + d * kVtPitch) = u32x2{tr[4 * e], tr[4 * e + 1]};
+            *reinterpret_cast<u32x2 *>(sv + (d + 1) * kVtPitch) =
+                u32x2{tr[4 * e + 2], tr[4 * e + 3]};
+          }
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-    }
-    if (with_next) {
-      uint8_t *sv = vt0 + (vb ^ 1) * kVtBytes + vpos * 2;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int d = 8 * vc + 2 * e;
-        *reinterpret_cast<u32x2 *>(sv + d * kVtPitch) = u32x2{tr[4 * e], tr[4 * e + 1]};
-        *reinterpret_cast<u32x2 *>(sv + (d + 1) * kVtPitch) =
-            u32x2{tr[4 * e + 2], tr[4 * e + 3]};
-      }
     }
     return fmaxf(mx, __shfl_xor(mx, 32)) * c;
   };
@@ -372,34 +372,44 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(Params p) {
   // the VALU reduces S(t+1) to its row max and transposes V(t+1) (phase 2).
   // K runs one tile ahead of V: K(t+2) and V(t+1) are loaded during
   // iteration t into the buffers that K(t) and V(t-1) left.
-  f32x16 sc[2], sn[2];
+  // The loop is unrolled by two with the score arrays swapping roles, so no
+  // register copies carry S(t+1) into the next iteration.
+  f32x16 sa[2], sb[2];
   u32x4 pf[2][2];
   issue_k(0, 0);
   load_v(0);
   vm_wait_barrier();
   if (ntiles > 1)
     issue_k(1, 1);
-  s_mfma(sc, 0);
+  s_mfma(sa, 0);
   store_v(0);
-  mask(sc, 0);
-  update_max(rowmax(sc));
+  mask(sa, 0);
+  update_max(rowmax(sa));
   vm_wait_barrier();
-  for (int t = 0; t + 1 < ntiles; ++t) {
-    const uint32_t cur = t & 1, nxt = cur ^ 1;
+  // cur = t & 1 is passed as a constant (t is even for sc = sa).
+  auto iteration = [&](int t, uint32_t cur, const f32x16 (&sc)[2], f32x16 (&sn)[2]) {
     load_v(t + 1);
     if (t + 2 < ntiles)
       issue_k(cur, t + 2);
-    phase1(sn, nxt, sc, pf);
+    phase1(sn, cur ^ 1, sc, pf);
     mask(sn, t + 1);
     const float mx = phase2(pf, cur, sn, true);
     update_max(mx);
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      sc[j] = sn[j];
     vm_wait_barrier();
+  };
+  int t = 0;
+  for (; t + 2 < ntiles; t += 2) {
+    iteration(t, 0, sa, sb);
+    iteration(t + 1, 1, sb, sa);
   }
-  exp_pack(sc, pf);
-  pv_mfma(pf, (ntiles - 1) & 1);
+  if (t + 1 < ntiles) {
+    iteration(t, 0, sa, sb);
+    exp_pack(sb, pf);
+    pv_mfma(pf, 1);
+  } else {
+    exp_pack(sa, pf);
+    pv_mfma(pf, 0);
+  }
   const float lsum = lacc[0];
 
   // Normalise and store O[my_q][d], d = 32*dt + 8*(r/4) + 4*half + r%4.

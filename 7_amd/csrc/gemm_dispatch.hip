@@ -2,6 +2,10 @@
 // (aligned DMA path vs masked path, dtype/layout, tiled vs Stream-K).
 #include "gemm_kernels.hpp"
 
+#ifndef WAVE_GEMM_GROUP_M
+#define WAVE_GEMM_GROUP_M 4
+#endif
+
 #include <vector>
 
 namespace wave {
@@ -94,7 +98,7 @@ hipError_t launch(const GemmArgs &g, hipStream_t stream) {
   p.K = g.K;
   p.tiles_m = tiles_for(g.M);
   p.tiles_n = tiles_for(g.N);
-  p.group_m = g.group_m > 0 ? g.group_m : 4;
+  p.group_m = g.group_m > 0 ? g.group_m : WAVE_GEMM_GROUP_M;
   if (p.group_m > p.tiles_m)
     p.group_m = p.tiles_m;
   p.ldc = g.col_major ? g.M : g.N;
