@@ -5,10 +5,6 @@
 
 #include <hip/hip_runtime.h>
 
-#ifndef WAVE_FA_VARIANT
-#define WAVE_FA_VARIANT 0
-#endif
-
 namespace wave {
 namespace attention {
 
@@ -22,7 +18,6 @@ struct FwdArgs {
   int dtype = 1;            // wave::kF16 or wave::kBF16 (Q, K, V and O)
   int causal = 0;           // mask key > query (top-left aligned)
   float scale = 0.f;        // softmax scale; 0 selects 1/sqrt(head_dim)
-  int variant = WAVE_FA_VARIANT;  // 0: 32 query rows per wave (fwd_kernel); 1: 64 (fwd64_kernel)
 };
 
 hipError_t launch_fwd(const FwdArgs &args, hipStream_t stream);

@@ -7,8 +7,6 @@
 namespace wave {
 namespace attention {
 
-constexpr int kWaves = 4;
-
 hipError_t launch_fwd(const FwdArgs &a, hipStream_t stream) {
   Params p{};
   p.Q = static_cast<const uint16_t *>(a.Q);
@@ -20,26 +18,16 @@ hipError_t launch_fwd(const FwdArgs &a, hipStream_t stream) {
   p.kv_heads = a.kv_heads;
   p.seq_q = a.seq_q;
   p.seq_k = a.seq_k;
-  p.q_blocks = (a.seq_q + 32 * kWaves - 1) / (32 * kWaves);
+  p.q_blocks = (a.seq_q + 32 * kPPWaves - 1) / (32 * kPPWaves);
   p.causal = a.causal;
   const float scale = a.scale > 0.f ? a.scale : 1.0f / std::sqrt((float)a.head_dim);
   p.scale_log2 = scale * kLog2e;
-  const dim3 block(64 * kWaves);
-  if (a.variant == 1) {
-    // 4 waves x 64 query rows per CTA
-    p.q_blocks = (a.seq_q + 255) / 256;
-    const dim3 grid(p.q_blocks * a.batch * a.q_heads);
-    if (a.dtype == kF16)
-      hipLaunchKernelGGL((fwd64_kernel<kF16>), grid, block, 0, stream, p);
-    else
-      hipLaunchKernelGGL((fwd64_kernel<kBF16>), grid, block, 0, stream, p);
-    return hipGetLastError();
-  }
-  const dim3 grid(p.q_blocks * a.batch * a.q_heads);
+  // 8 waves x 32 query rows per CTA, two ping-pong groups of 4 waves.
+  const dim3 grid(p.q_blocks * a.batch * a.q_heads), block(64 * kPPWaves);
   if (a.dtype == kF16)
-    hipLaunchKernelGGL((fwd_kernel<kF16, kWaves>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((fwd_pp_kernel<kF16>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((fwd_kernel<kBF16, kWaves>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((fwd_pp_kernel<kBF16>), grid, block, 0, stream, p);
   return hipGetLastError();
 }
 

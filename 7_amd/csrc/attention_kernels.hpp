@@ -8,7 +8,8 @@
 // tools/wave-fa-calibrate/wave-fa-gfx950-runner.cpp:396-402), generalised to
 // f16 / bf16, causal masking and GQA.
 //
-// Design (one CTA = 32*NW query rows of one head, NW waves of 64 lanes):
+// Design (one CTA = 256 query rows of one head, 8 waves of 64 lanes, one
+// CTA per CU):
 //  * Each wave owns 32 query rows and computes S^T = K . Q^T with
 //    v_mfma_f32_32x32x16 (A = K rows from LDS, B = Q fragments held in
 //    VGPRs for the whole kernel).  In that orientation lane l owns query
@@ -21,24 +22,27 @@
 //    h, which is exactly one MFMA K slice once V^T is stored with each
 //    16-key group permuted as [0-3, 8-11, 4-7, 12-15].
 //  * K tiles (64 keys x 256 B) arrive by global_load_lds_dwordx4 with an XOR
-//    swizzle (chunk c of row r at c ^ (r & 15)); V tiles are loaded into
-//    VGPRs one tile ahead, transposed in registers and written to LDS as
-//    V^T rows of 64 keys (+16 B padding, 144 B pitch).  Two buffers each;
-//    K runs one tile ahead of V (see the pipeline below).
-//  * Software pipeline inside each wave: the MFMAs of S(t+1) are
-//    interleaved with the exp2 VALU work of tile t, and the PV MFMAs of
-//    tile t with the row max of tile t+1, so the matrix pipe and the VALU
-//    stay busy at the same time.
+//    swizzle (chunk c of row r at c ^ (r & 15)) into a 4-tile ring; V tiles
+//    are loaded into VGPRs, transposed in registers and written to LDS as
+//    V^T rows of 64 keys (+16 B padding, 144 B pitch) into a 2-tile ring.
+//  * The two groups of 4 waves alternate between a matrix-only segment (the
+//    MFMAs of S(t+1) and O += V(t) P(t)) and a vector-only segment (the
+//    softmax of the next tile), one segment apart, so every SIMD pairs one
+//    wave's MFMA stream with the other wave's softmax (fwd_pp_kernel).
 //  * exp2 with the scale folded into one FMA; the running max is only
 //    raised (and O rescaled) when a tile's max exceeds it by more than 8
 //    (log2 units), as in the reference's lazy rescale
-//    (wave_flash_attention.py:557-583); P stays below 2^8.
+//    (wave_flash_attention.py:557-583); P stays below 2^8.  Row sums are
+//    v_dot2 products of the packed 16-bit P with ones, so they sum exactly
+//    the values that multiply V.
 //  * CTAs of one head are placed on the same XCD so its K/V stay in that
 //    XCD's L2; causal grids start with the longest query blocks.
 #pragma once
 
 #include "attention.hpp"
 #include "wave_common.hpp"
+
+#include <type_traits>
 
 namespace wave {
 namespace attention {
@@ -75,18 +79,83 @@ __device__ __forceinline__ void block_coords(const Params &p, int &bh, int &qb) 
     qb = p.q_blocks - 1 - qb;  // longest rows first
 }
 
-template <int DT, int NW>
-__global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(Params p) {
-  static_assert(NW == 4, "V^T transpose mapping assumes 256 threads");
-  // LDS: K ring [2][64 keys][256 B] (XOR-swizzled chunks), then the V^T
-  // ring [2][128 d][144 B].
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kKBytes + 2 * kVtBytes];
-  constexpr int kRows = 32 * NW;
+// ------------------------------------------------------------------------
+// fwd_pp_kernel: 8 waves x 32 query rows per CTA (256 rows, one CTA per
+// CU), run as two groups of four waves -- A = waves 0-3, B = waves 4-7;
+// wave w shares SIMD w % 4 with wave w + 4 -- that the workgroup barriers
+// keep one segment apart ("ping-pong"):
+//
+//   segment   2t          2t+1        2t+2
+//   group A   G(t)        SM(t+1)     G(t+1)
+//   group B   SM(t)       G(t)        SM(t+1)
+//
+// G(t), matrix only: S(t+1) = K(t+1) . Q^T and O^T += V(t)^T . P(t)^T,
+// 32 MFMAs fed from LDS.  SM(t), vector only: mask and row max of S(t),
+// the lazy rescale of O, P(t) = exp2(S(t) * c - m) packed to 16 bits, the
+// row sums of P(t) (v_dot2 on the packed values), half of a V^T transpose
+// and this wave's share of a K DMA.  Each SIMD therefore always pairs one
+// wave's MFMA stream with the other wave's softmax.  All 8 waves share each
+// K and V^T tile, so per query row the K/V traffic from L2 and the
+// transpose work are half of fwd_kernel's.
+//
+// Buffers (the unrolled loop makes every index a compile-time constant):
+//  * K ring of 4 tiles, tile j in buffer j % 4, read in G(j-1) (segments
+//    2j-2 and 2j-1).  Both groups issue K(j) in SM(j-3) (segments 2j-5 and
+//    2j-6), after the last read of K(j-4); each wave's next V wait (next
+//    SM) completes its share before the barrier that precedes G(j-1).
+//  * V^T ring of 2 tiles, V^T(j) read in G(j) (segments 2j, 2j+1).  A
+//    writes its half (d rows 0-63) in SM(j) (segment 2j-1), B its half (d
+//    rows 64-127) in SM(j-1) (segment 2j-2); the buffer's previous tile
+//    V^T(j-2) was last read in segment 2j-3.
+// Both groups run the same code: B joins one extra barrier before its loop
+// (its idle segment 0); after the last G only A joins a barrier (it pairs
+// with the end of B's last SM).  Barriers per wave: 2 * ntiles + 1.
+constexpr int kPPWaves = 8;
+constexpr int kKRingPP = 4;
+#ifndef WAVE_FA_PF
+#define WAVE_FA_PF 4  // LDS fragment prefetch depth (MFMAs) in G
+#endif
+#ifndef WAVE_FA_TAIL
+#define WAVE_FA_TAIL 8  // PV MFMAs of G(t) issued at the start of SM(t+1)
+#endif
+template <int N> using I_ = std::integral_constant<int, N>;
+
+template <int DT>
+__device__ __forceinline__ float dot2_ones(uint32_t pk, float acc) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  if constexpr (DT == kF16)
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pk),
+                                  __builtin_bit_cast(h2, kOnePair<DT>), acc, false);
+  else
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, pk),
+                                           __builtin_bit_cast(b2, kOnePair<DT>), acc, false);
+}
+
+// 16-byte LDS load / 4-byte LDS store at a 32-bit LDS byte address.
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
+__device__ __forceinline__ u32x4 lds_load16(uint32_t a) { return *(lds_u32x4 *)(uintptr_t)a; }
+__device__ __forceinline__ void lds_store4(uint32_t a, uint32_t v) { *(lds_u32 *)(uintptr_t)a = v; }
+// Hide v's value from constant folding, so that base + constant address
+// expressions keep the constant in the instruction's 16-bit offset field.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm("" : "+v"(v));
+  return v;
+}
+
+template <int DT>
+__global__ __launch_bounds__(512, 1) void fwd_pp_kernel(Params p) {
+  // LDS: K ring [4][64 keys][256 B] (XOR-swizzled chunks), V^T ring
+  // [2][128 d][144 B].
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kKRingPP * kKBytes + 2 * kVtBytes];
+  constexpr int kRows = 32 * kPPWaves;
   const uint32_t wave = uniform(threadIdx.x >> 6);
+  const uint32_t grp = wave >> 2;
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t half = lane >> 5;
   int bh, qb;
-  block_coords<NW>(p, bh, qb);
+  block_coords<kPPWaves>(p, bh, qb);
   const int b = bh / p.q_heads, hq = bh - b * p.q_heads;
   const int hkv = hq / (p.q_heads / p.kv_heads);
   const uint16_t *Qh = p.Q + ((size_t)bh * p.seq_q) * kD;
@@ -96,10 +165,9 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(Params p) {
   uint16_t *Oh = p.O + ((size_t)bh * p.seq_q) * kD;
 
   const int q0 = qb * kRows;
-  const int qw = q0 + wave * 32;             // this wave's first query
-  const int my_q = qw + (lane & 31);          // this lane's query
+  const int qw = q0 + wave * 32;
+  const int my_q = qw + (lane & 31);
 
-  // Q^T fragments: lane supplies Q[my_q][16*kk + 8*half .. +8].
   u32x4 qf[8];
   {
     const bool ok = my_q < p.seq_q;
@@ -110,98 +178,142 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(Params p) {
                   : u32x4{0u, 0u, 0u, 0u};
   }
 
-  // Key range.  Causal: keys <= last query of the block.
   int kend = p.seq_k;
   if (p.causal)
     kend = min(kend, q0 + kRows);
   const int ntiles = (kend + kBN - 1) / kBN;
 
-  // K DMA: wave w fills rows 16w .. 16w+15 of the tile (4 x 1 KiB).  Rows
-  // past seq_k re-read the last key (masked out of the softmax).
-  uint32_t kgoff[4];
-  int krow[4];
+  // K DMA: wave w fills rows 8w .. 8w+7 of a tile (2 x 1 KiB).  Rows past
+  // seq_k re-read the last key (masked out of the softmax).  Tiles past the
+  // last one are issued too (clamped, never read), so the DMA needs no
+  // branch; the kernel drains them before it ends.
+  uint32_t kgoff[2];
+  int krow[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    krow[i] = (wave * 4 + i) * 4 + (lane >> 4);
+  for (int i = 0; i < 2; ++i) {
+    krow[i] = (wave * 2 + i) * 4 + (lane >> 4);
     kgoff[i] = ((lane & 15) ^ (krow[i] & 15)) << 4;
   }
   const uint32_t lds0 = lds_addr(smem);
-  auto issue_k = [&](uint32_t buf, int kt) {
-    const int k0 = kt * kBN;
-    const uint32_t l = lds0 + buf * kKBytes + wave * 4 * 1024;
+  auto issue_k = [&](int kt) {
+    const uint32_t l = lds0 + (kt & (kKRingPP - 1)) * kKBytes + wave * 2048;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = min(k0 + krow[i], p.seq_k - 1);
+    for (int i = 0; i < 2; ++i) {
+      const int key = min(kt * kBN + krow[i], p.seq_k - 1);
       dma16(l + i * 1024, Kh, (uint32_t)key * kKRowBytes + kgoff[i]);
     }
   };
 
-  // V: thread t loads keys 4g..4g+3 (g = t % 16) of d-chunk c = t / 16 into
-  // VGPRs one tile ahead.  Keys past seq_k re-read the last key: their P is 0.
-  const int vg = threadIdx.x & 15, vc = threadIdx.x >> 4;
-  u32x4 vr[4];
+  // V: group g transposes d rows 64g .. 64g+63.  Thread tg of the group
+  // loads keys 2kp, 2kp+1 (kp = tg % 32) of d chunk dc = 8g + tg / 32.
+  const int tg = threadIdx.x & 255;
+  const int kp = tg & 31, dc = 8 * grp + (tg >> 5);
+  u32x4 vr[2];
   auto load_v = [&](int kt) {
-    const int k0 = kt * kBN + 4 * vg;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t key = (uint32_t)min(k0 + i, p.seq_k - 1);
-      vr[i] = *reinterpret_cast<const u32x4 *>(Vh + key * kKRowBytes + 16 * vc);
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t key = (uint32_t)min(kt * kBN + 2 * kp + i, p.seq_k - 1);
+      vr[i] = *reinterpret_cast<const u32x4 *>(Vh + key * kKRowBytes + 16 * dc);
     }
   };
-  // V^T position of key group g: 16-key group G = g/4 stored as
-  // [0-3, 8-11, 4-7, 12-15].
-  const int vpos = 16 * (vg >> 2) + 4 * ((vg & 1) * 2 + ((vg >> 1) & 1));
-  uint8_t *const vt0 = smem + 2 * kKBytes;
-  auto store_v = [&](uint32_t buf) {
-    uint8_t *s = vt0 + buf * kVtBytes + vpos * 2;
+  // V^T column of key 2kp: 16-key groups stored as [0-3, 8-11, 4-7, 12-15].
+  const int k2 = 2 * kp, blk = (k2 >> 2) & 3;
+  const int vpos = 16 * (k2 >> 4) + 4 * (((blk & 1) << 1) | (blk >> 1)) + (k2 & 3);
+  constexpr uint32_t kVtOff = kKRingPP * kKBytes;
+  // Per-lane LDS bases; buffer, fragment and row offsets (< 64 KiB) are
+  // added as immediates.
+  const uint32_t kr = lane & 31;
+  const uint32_t vt_store = opaque(lds0 + kVtOff + (uint32_t)(8 * dc) * kVtPitch + 2 * vpos);
+  const uint32_t vt_read = opaque(lds0 + kVtOff + kr * kVtPitch + 16 * half);
+  uint32_t kread[8];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      // d = 8*vc + 2e (low halves) and 8*vc + 2e + 1 (high halves).
-      const uint32_t lo01 = __builtin_amdgcn_perm(vr[1][e], vr[0][e], 0x05040100u);
-      const uint32_t lo23 = __builtin_amdgcn_perm(vr[3][e], vr[2][e], 0x05040100u);
-      const uint32_t hi01 = __builtin_amdgcn_perm(vr[1][e], vr[0][e], 0x07060302u);
-      const uint32_t hi23 = __builtin_amdgcn_perm(vr[3][e], vr[2][e], 0x07060302u);
-      const int d = 8 * vc + 2 * e;
-      *reinterpret_cast<u32x2 *>(s + d * kVtPitch) = u32x2{lo01, lo23};
-      *reinterpret_cast<u32x2 *>(s + (d + 1) * kVtPitch) = u32x2{hi01, hi23};
-    }
-  };
-
-  const uint32_t kr = lane & 31;                     // key row within block
-  const uint32_t vt_row = (lane & 31) * kVtPitch;    // d row within d-tile
+  for (int kk = 0; kk < 8; ++kk)
+    kread[kk] = opaque(lds0 + kr * kKRowBytes + (((2 * kk + half) ^ (kr & 15)) << 4));
+  // V^T(t+1+grp) is stored in SM(t+1): buffer ((t+1) & 1) ^ grp.
+  const uint32_t vst_par[2] = {opaque(vt_store + grp * kVtBytes),
+                               opaque(vt_store + (grp ^ 1) * kVtBytes)};
 
   f32x16 o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     o[i] = f32x16{};
-  // Row sums on the matrix pipe: ones[32 x 16] . P^T gives, in every
-  // accumulator register of lane l, the sum of P over the slice for query
-  // l%32.  Only register 0 is read (and rescaled); it sums exactly the
-  // 16-bit P values that multiply V.
-  f32x16 lacc = f32x16{};
-  const u32x4 ones = {kOnePair<DT>, kOnePair<DT>, kOnePair<DT>, kOnePair<DT>};
+  float lsum = 0.f;
   float m = -__builtin_inff();
   const float c = p.scale_log2;
+  // pin(x): x must be computed before this point (keeps each segment's work
+  // on its side of the barrier that follows).
+  auto pin = [](auto x) { asm volatile("" ::"v"(x)); };
 
-  // ---- stage primitives ---------------------------------------------------
-  // S^T = K . Q^T for the 2 blocks of 32 keys of the tile in K buffer kb.
-  auto s_mfma = [&](f32x16 (&sc)[2], uint32_t kb) {
-    const uint8_t *ks = smem + kb * kKBytes;
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      sc[j] = f32x16{};
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const uint32_t row = j * 32 + kr;
-        const uint32_t chunk = (2 * kk + half) ^ (row & 15);
-        const u32x4 kf =
-            *reinterpret_cast<const u32x4 *>(ks + row * kKRowBytes + (chunk << 4));
-        sc[j] = mfma32x32x16<DT>(kf, qf[kk], sc[j]);
-      }
+  auto kfrag = [&](uint32_t kb, int i) {  // i = 2*kk + j: key row 32j + kr
+    return lds_load16(kread[i >> 1] + kb * kKBytes + (i & 1) * 32 * kKRowBytes);
   };
-  // Masks of tile t: causal (key > query) and keys past seq_k.
+  auto vfrag = [&](uint32_t vb, int i) {  // i = 4*(2*j + sl) + dt
+    const int g = i >> 2, dt = i & 3;
+    return lds_load16(vt_read + vb * kVtBytes + dt * 32 * kVtPitch + 32 * g);
+  };
+  u32x4 pf[2][2];
+
+  // G(t): S(t+1) (when NEXT) from K buffer KB and O += V^T(t) P(t) from
+  // V^T buffer VB as one explicit pipeline: the LDS fragment of MFMA
+  // i + kPF is read in step i.  MFMA order (NEXT): S0 PV0 S1 PV1 ...
+  // S(15-kTail) PV(15-kTail), then S(16-kTail) .. S15, then the kTail PV
+  // MFMAs PV(16-kTail) .. PV15, which are issued at the start of the next
+  // SM (pv_tail) with their fragments already in registers.
+  constexpr int kPF = WAVE_FA_PF, kTail = WAVE_FA_TAIL;
+  static_assert(kTail >= 0 && kTail <= 16 && kPF >= 1, "G pipeline shape");
+  u32x4 tailf[kTail > 0 ? kTail : 1];
+  auto seg_g = [&](auto next_tag, auto kb_tag, auto vb_tag, f32x16 (&sn)[2]) {
+    constexpr bool NEXT = decltype(next_tag)::value;
+    constexpr uint32_t KB = decltype(kb_tag)::value;
+    constexpr uint32_t VB = decltype(vb_tag)::value;
+    constexpr int NM = NEXT ? 32 : 16;           // MFMAs incl. the deferred tail
+    constexpr int NI = NM - (NEXT ? kTail : 0);  // issued here
+    constexpr int NP = 16 - kTail;               // S/PV pairs at the front
+    // Position i -> (is S, step index).
+    auto is_s = [&](int i) { return NEXT && (i < 2 * NP ? !(i & 1) : i < 2 * NP + kTail); };
+    auto step = [&](int i) {
+      if (!NEXT)
+        return i;
+      return i < 2 * NP ? i >> 1 : i < 2 * NP + kTail ? i - NP : i - NP - kTail;
+    };
+    auto frag = [&](int i) { return is_s(i) ? kfrag(KB, step(i)) : vfrag(VB, step(i)); };
+    u32x4 f[NM];
+#pragma unroll
+    for (int i = 0; i < kPF && i < NM; ++i)
+      f[i] = frag(i);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      if (i + kPF < NM)
+        f[i + kPF] = frag(i + kPF);
+      const int si = step(i);
+      if (is_s(i)) {
+        sn[si & 1] = mfma32x32x16<DT>(f[i], qf[si >> 1], si < 2 ? f32x16{} : sn[si & 1]);
+      } else {
+        const int g = si >> 2, dt = si & 3;
+        o[dt] = mfma32x32x16<DT>(f[i], pf[g >> 1][g & 1], o[dt]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // Tail fragments the pipeline has not read yet (kTail > kPF).
+#pragma unroll
+    for (int i = NI + kPF; i < NM; ++i)
+      f[i] = frag(i);
+    if constexpr (NEXT) {
+#pragma unroll
+      for (int k = 0; k < kTail; ++k)
+        tailf[k] = f[NI + k];
+    }
+  };
+  // The deferred PV MFMAs PV(16-kTail) .. PV15 of the previous G.
+  auto pv_tail = [&]() {
+#pragma unroll
+    for (int k = 0; k < kTail; ++k) {
+      const int v = 16 - kTail + k;
+      const int g = v >> 2, dt = v & 3;
+      o[dt] = mfma32x32x16<DT>(tailf[k], pf[g >> 1][g & 1], o[dt]);
+    }
+  };
+
   auto mask = [&](f32x16 (&sc)[2], int t) {
     const int k0 = t * kBN;
     const bool edge = (k0 + kBN > p.seq_k) || (p.causal && k0 + kBN - 1 > qw);
@@ -216,15 +328,6 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(Params p) {
         }
     }
   };
-  auto rowmax = [&](const f32x16 (&sc)[2]) {
-    float mx = sc[0][0];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        mx = fmaxf(mx, sc[j][r]);
-    return fmaxf(mx, __shfl_xor(mx, 32)) * c;
-  };
   // Lazy rescale: raise the running max only when it grows by > 8 (log2).
   auto update_max = [&](float mx) {
     const bool need = mx > m + kRescaleThreshold;
@@ -232,14 +335,22 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(Params p) {
       const float mn = fmaxf(m, mx);
       const float alpha = (m == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(m - mn);
       m = mn;
-      lacc[0] *= alpha;
+      lsum *= alpha;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         o[i] *= alpha;
     }
   };
-  // P = exp2(s*c - m), packed to 16 bits as the B operand of O^T += V^T P^T.
-  auto exp_pack = [&](const f32x16 (&sc)[2], u32x4 (&pf)[2][2]) {
+  // Softmax of tile t (scores in sc): max, rescale, P(t) -> pf, row sums.
+  auto softmax = [&](f32x16 (&sc)[2], int t) {
+    mask(sc, t);
+    float mx = sc[0][0];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        mx = fmaxf(mx, sc[j][r]);
+    update_max(fmaxf(mx, __shfl_xor(mx, 32)) * c);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -247,173 +358,119 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(Params p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][8 * sl + 2 * e], c, -m));
-          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][8 * sl + 2 * e + 1], c, -m));
+          const float p1 =
+              __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][8 * sl + 2 * e + 1], c, -m));
           pf[j][sl][e] = pack2<DT>(p0, p1);
         }
-  };
-  // O^T += V^T . P^T over 4 d-tiles x 4 key slices (V^T buffer vb), and the
-  // row sums alongside.
-  auto pv_mfma = [&](const u32x4 (&pf)[2][2], uint32_t vb) {
-    const uint8_t *vs = vt0 + vb * kVtBytes;
+    // Row sums in two independent v_dot2 chains.
+    float l1 = 0.f;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int sl = 0; sl < 2; ++sl) {
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-          const u32x4 vf = *reinterpret_cast<const u32x4 *>(
-              vs + dt * 32 * kVtPitch + vt_row + (16 * (2 * j + sl) + 8 * half) * 2);
-          o[dt] = mfma32x32x16<DT>(vf, pf[j][sl], o[dt]);
-        }
-        lacc = mfma32x32x16<DT>(ones, pf[j][sl], lacc);
+      for (int e = 0; e < 4; ++e) {
+        lsum = dot2_ones<DT>(pf[j][0][e], lsum);
+        l1 = dot2_ones<DT>(pf[j][1][e], l1);
       }
+    lsum += l1;
+    pin(lsum);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl)
+        pin(pf[j][sl]);
   };
-
-  // ---- fused pipeline phases ----------------------------------------------
-  // pin(x): an empty asm use, so x is computed in the step that produces it
-  // (without it, IR-level sinking moves the VALU work next to its uses).
-  auto pin = [](auto x) { asm volatile("" ::"v"(x)); };
-  // Each phase is written as explicit steps of one MFMA plus a share of the
-  // VALU work of the other tile; sched_barrier keeps the steps in order so
-  // the two pipes overlap.  LDS fragment reads run 4 steps ahead.
-  //
-  // Phase 1: S(t+1) = K(t+1) . Q^T (16 MFMAs) with P(t) = exp2(S(t)*c - m)
-  // packed to 16 bits (2 elements per step).
-  auto phase1 = [&](f32x16 (&sn)[2], uint32_t kb, const f32x16 (&sc)[2],
-                    u32x4 (&pf)[2][2]) {
-    const uint8_t *ks = smem + kb * kKBytes;
-    auto kfrag = [&](int i) {  // i = 2*kk + j
-      const uint32_t row = (i & 1) * 32 + kr;
-      const uint32_t chunk = (2 * (i >> 1) + half) ^ (row & 15);
-      return *reinterpret_cast<const u32x4 *>(ks + row * kKRowBytes + (chunk << 4));
-    };
-    u32x4 kf[16];
-    sn[0] = f32x16{};
-    sn[1] = f32x16{};
+  // This group's half of a V^T tile (from vr) at store base vst.
+  auto store_vt = [&](uint32_t vst) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      kf[i] = kfrag(i);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (i + 4 < 16)
-        kf[i + 4] = kfrag(i + 4);
-      sn[i & 1] = mfma32x32x16<DT>(kf[i], qf[i >> 1], sn[i & 1]);
-      const int j = i >> 3, r = (2 * i) & 15;
-      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][r], c, -m));
-      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][r + 1], c, -m));
-      pf[j][r >> 3][(r & 7) >> 1] = pack2<DT>(p0, p1);
-      pin(pf[j][r >> 3][(r & 7) >> 1]);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int e = 0; e < 4; ++e) {
+      lds_store4(vst + 2 * e * kVtPitch, __builtin_amdgcn_perm(vr[1][e], vr[0][e], 0x05040100u));
+      lds_store4(vst + (2 * e + 1) * kVtPitch,
+                 __builtin_amdgcn_perm(vr[1][e], vr[0][e], 0x07060302u));
     }
   };
-  // Phase 2: O^T += V(t)^T . P(t)^T and the row sums (20 MFMAs) with the
-  // row max of S(t+1) and the register transpose of V(t+1) for its LDS
-  // store.  Returns the scaled row max of S(t+1).
-  auto phase2 = [&](const u32x4 (&pf)[2][2], uint32_t vb, const f32x16 (&sn)[2],
-                    bool with_next) {
-    const uint8_t *vs = vt0 + vb * kVtBytes;
-    auto vfrag = [&](int i) {  // i = 4*(2*j + sl) + dt
-      const int g = i >> 2, dt = i & 3;
-      return *reinterpret_cast<const u32x4 *>(vs + dt * 32 * kVtPitch + vt_row +
-                                              (16 * g + 8 * half) * 2);
-    };
-    u32x4 vf[16];
-    float mx = -__builtin_inff();
-    uint32_t tr[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      vf[i] = vfrag(i);
-#pragma unroll
-    for (int q = 0; q < 20; ++q) {
-      const int g = q / 5, w = q % 5;
-      const u32x4 &pb = pf[g >> 1][g & 1];
-      if (w < 4) {
-        const int i = 4 * g + w;
-        if (i + 4 < 16)
-          vf[i + 4] = vfrag(i + 4);
-        o[w] = mfma32x32x16<DT>(vf[i], pb, o[w]);
-      } else {
-        lacc = mfma32x32x16<DT>(ones, pb, lacc);
-      }
-      if (with_next) {
-        // 32 S values -> 16 max3 steps, then 16 perms of the V transpose.
-        if (q < 16) {
-          mx = __builtin_fmaxf(__builtin_fmaxf(mx, sn[q >> 3][(2 * q) & 15]),
-                               sn[q >> 3][((2 * q) & 15) + 1]);
-          pin(mx);
-        }
-        if (q >= 4) {
-          const int e = (q - 4) >> 2, k = (q - 4) & 3;
-          // k: 0 lo01, 1 lo23, 2 hi01, 3 hi23 of dword e
-          const int a = (k & 1) ? 3 : 1, b2 = (k & 1) ? 2 : 0;
-          tr[q - 4] = __builtin_amdgcn_perm(vr[a][e], vr[b2][e],
-                                            (k & 2) ? 0x07060302u : 0x05040100u);
-          pin(tr[q - 4]);
-          // Dword e of the transpose is complete: store its two V^T rows
-          // now (the buffer's last reader, PV(t-1), finished before the
-          // previous barrier), so only 4 transposed registers are live.
-          if (k == 3) {
-            uint8_t *sv = vt0 + (vb ^ 1) * kVtBytes + vpos * 2;
-            const int d = 8 * vc + 2 * e;
-            *reinterpret_cast<u32x2 *>(sv + d * kVtPitch) = u32x2{tr[4 * e], tr[4 * e + 1]};
-            *reinterpret_cast<u32x2 *>(sv + (d + 1) * kVtPitch) =
-                u32x2{tr[4 * e + 2], tr[4 * e + 3]};
-          }
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    return fmaxf(mx, __shfl_xor(mx, 32)) * c;
+
+  // One iteration t < ntiles - 1: G(t), barrier, SM(t+1), barrier.
+  // PH = t % 4 fixes the buffer offsets.
+  auto iter = [&](auto ph_tag, int t, f32x16 (&sn)[2]) {
+    constexpr int PH = decltype(ph_tag)::value;
+    load_v(t + 1 + (int)grp);
+    seg_g(std::true_type{}, std::integral_constant<uint32_t, (PH + 1) % kKRingPP>{},
+          std::integral_constant<uint32_t, PH & 1>{}, sn);
+    // G only reads LDS, and the next writer of what it read (a V^T or K
+    // buffer) comes after the barrier that ends the following SM, which
+    // waits for LDS.  So this barrier does not wait for G's last fragment
+    // reads (the deferred tail's), which complete under the next SM.
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    pv_tail();
+    softmax(sn, t + 1);
+    store_vt(vst_par[(PH + 1) & 1]);  // first use of vr: waits for the loads
+    issue_k(t + 4);                   // after the V wait (see the K ring)
+    lds_barrier();
   };
 
-  // ---- software pipeline over key tiles --------------------------------------
-  // Iteration t: the matrix pipe computes S(t+1) while the VALU turns S(t)
-  // into P(t) (phase 1), then the matrix pipe computes O += V(t) P(t) while
-  // the VALU reduces S(t+1) to its row max and transposes V(t+1) (phase 2).
-  // K runs one tile ahead of V: K(t+2) and V(t+1) are loaded during
-  // iteration t into the buffers that K(t) and V(t-1) left.
-  // The loop is unrolled by two with the score arrays swapping roles, so no
-  // register copies carry S(t+1) into the next iteration.
-  f32x16 sa[2], sb[2];
-  u32x4 pf[2][2];
-  issue_k(0, 0);
+  // ---- prologue (all waves): K(0..3), V^T(0), B's half of V^T(1), S(0)
+  // and its softmax --------------------------------------------------------
+  f32x16 sa[2];
+  issue_k(0);
+  issue_k(1);
+  issue_k(2);
   load_v(0);
   vm_wait_barrier();
-  if (ntiles > 1)
-    issue_k(1, 1);
-  s_mfma(sa, 0);
-  store_v(0);
-  mask(sa, 0);
-  update_max(rowmax(sa));
-  vm_wait_barrier();
-  // cur = t & 1 is passed as a constant (t is even for sc = sa).
-  auto iteration = [&](int t, uint32_t cur, const f32x16 (&sc)[2], f32x16 (&sn)[2]) {
-    load_v(t + 1);
-    if (t + 2 < ntiles)
-      issue_k(cur, t + 2);
-    phase1(sn, cur ^ 1, sc, pf);
-    mask(sn, t + 1);
-    const float mx = phase2(pf, cur, sn, true);
-    update_max(mx);
-    vm_wait_barrier();
-  };
+  store_vt(vt_store);
+  if (grp == 1) {
+    load_v(1);
+    store_vt(vt_store + kVtBytes);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    sa[i & 1] = mfma32x32x16<DT>(kfrag(0, i), qf[i >> 1], i < 2 ? f32x16{} : sa[i & 1]);
+  issue_k(3);
+  softmax(sa, 0);
+  lds_barrier();
+  if (grp == 1)  // group B's idle segment 0
+    lds_barrier();
+
+  // ---- main loop, unrolled by 4 (K ring); leaves with t = ntiles - 1 -----
   int t = 0;
-  for (; t + 2 < ntiles; t += 2) {
-    iteration(t, 0, sa, sb);
-    iteration(t + 1, 1, sb, sa);
+  for (;; t += 4) {
+    if (t + 1 >= ntiles)
+      break;
+    iter(I_<0>{}, t, sa);
+    if (t + 2 >= ntiles) {
+      t += 1;
+      break;
+    }
+    iter(I_<1>{}, t + 1, sa);
+    if (t + 3 >= ntiles) {
+      t += 2;
+      break;
+    }
+    iter(I_<2>{}, t + 2, sa);
+    if (t + 4 >= ntiles) {
+      t += 3;
+      break;
+    }
+    iter(I_<3>{}, t + 3, sa);
   }
-  if (t + 1 < ntiles) {
-    iteration(t, 0, sa, sb);
-    exp_pack(sb, pf);
-    pv_mfma(pf, 1);
-  } else {
-    exp_pack(sa, pf);
-    pv_mfma(pf, 0);
-  }
-  const float lsum = lacc[0];
+  // Last tile: G = PV(t) only (V^T buffer t & 1).
+  if (t & 1)
+    seg_g(std::false_type{}, std::integral_constant<uint32_t, 0>{},
+          std::integral_constant<uint32_t, 1>{}, sa);
+  else
+    seg_g(std::false_type{}, std::integral_constant<uint32_t, 0>{},
+          std::integral_constant<uint32_t, 0>{}, sa);
+  if (grp == 0)
+    lds_barrier();
+  // K DMA issued for tiles past the end may still be in flight: let it land
+  // before the workgroup's LDS can be handed to another workgroup.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // Normalise and store O[my_q][d], d = 32*dt + 8*(r/4) + 4*half + r%4.
-  const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+  // Lanes l and l^32 hold the sums of complementary key halves.
+  const float total = lsum + __shfl_xor(lsum, 32);
+  const float inv = total > 0.f ? 1.0f / total : 0.f;
   if (my_q < p.seq_q) {
     uint16_t *orow = Oh + (size_t)my_q * kD + 4 * half;
 #pragma unroll
@@ -424,319 +481,6 @@ __global__ __launch_bounds__(NW * 64, 2) void fwd_kernel(Params p) {
                          pack2<DT>(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv)};
         *reinterpret_cast<u32x2 *>(orow + 32 * dt + 8 * g) = w;
       }
-  }
-}
-
-// ------------------------------------------------------------------------
-// fwd64_kernel: 4 waves x 64 query rows (two 32-row query blocks per wave),
-// 32-key tiles, one CTA per CU.  Each K and V^T fragment read from LDS feeds
-// two MFMAs (one per query block), halving LDS read traffic per MFMA
-// relative to fwd_kernel.  Same per-lane softmax orientation, V^T key
-// permutation, MFMA row sums, lazy rescale and two-phase intra-wave
-// pipeline.  K: 3-buffer LDS ring (DMA two tiles ahead); V: loaded one tile
-// ahead into VGPRs with explicitly counted loads, transposed into a 2-buffer
-// V^T ring with an 80-byte pitch (16 consecutive d rows -> distinct banks).
-constexpr int kBN2 = 32;                            // keys per tile
-constexpr int kK2Bytes = kBN2 * kKRowBytes;         // 8 KiB
-constexpr int kVt2Pitch = kBN2 * 2 + 16;            // 80 B per d row of V^T
-constexpr int kVt2Bytes = kD * kVt2Pitch;           // 10 KiB
-constexpr int kKRing = 3;
-
-// Global load of 16 bytes per lane whose completion the caller waits for
-// with vm_wait_regs (the compiler does not track it).
-__device__ __forceinline__ u32x4 gload16(const void *base, uint32_t voff) {
-  u32x4 v;
-  asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(v) : "v"(voff), "s"(base));
-  return v;
-}
-// s_waitcnt vmcnt(N) that also "redefines" a and b, so no use of them can be
-// scheduled before the wait.
-template <int N>
-__device__ __forceinline__ void vm_wait_regs(u32x4 &a, u32x4 &b) {
-  asm volatile("s_waitcnt vmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N) : "memory");
-}
-
-template <int DT>
-__global__ __launch_bounds__(256, 1) void fwd64_kernel(Params p) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kKRing * kK2Bytes + 2 * kVt2Bytes];
-  constexpr int kRows = 256;
-  const uint32_t wave = uniform(threadIdx.x >> 6);
-  const uint32_t lane = threadIdx.x & 63;
-  const uint32_t half = lane >> 5;
-  int bh, qb_idx;
-  block_coords<4>(p, bh, qb_idx);
-  const int b = bh / p.q_heads, hq = bh - b * p.q_heads;
-  const int hkv = hq / (p.q_heads / p.kv_heads);
-  const uint16_t *Qh = p.Q + ((size_t)bh * p.seq_q) * kD;
-  const char *Kh = reinterpret_cast<const char *>(
-      p.K + ((size_t)(b * p.kv_heads + hkv) * p.seq_k) * kD);
-  const char *Vh = reinterpret_cast<const char *>(
-      p.V + ((size_t)(b * p.kv_heads + hkv) * p.seq_k) * kD);
-  uint16_t *Oh = p.O + ((size_t)bh * p.seq_q) * kD;
-
-  const int q0 = qb_idx * kRows;
-  const int qw = q0 + wave * 64;  // this wave's first query
-  int my_q[2];
-  my_q[0] = qw + (lane & 31);
-  my_q[1] = qw + 32 + (lane & 31);
-
-  // Q^T fragments of both query blocks.
-  u32x4 qf[2][8];
-#pragma unroll
-  for (int g = 0; g < 2; ++g) {
-    const bool ok = my_q[g] < p.seq_q;
-    const uint16_t *qrow = Qh + (size_t)(ok ? my_q[g] : 0) * kD + 8 * half;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-      qf[g][kk] = ok ? *reinterpret_cast<const u32x4 *>(qrow + 16 * kk)
-                     : u32x4{0u, 0u, 0u, 0u};
-  }
-
-  int kend = p.seq_k;
-  if (p.causal)
-    kend = min(kend, q0 + kRows);
-  const int ntiles = (kend + kBN2 - 1) / kBN2;
-
-  // K DMA: wave w fills rows 8w .. 8w+7 of the 32-row tile (2 x 1 KiB).
-  uint32_t kgoff[2];
-  int krow[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    krow[i] = (wave * 2 + i) * 4 + (lane >> 4);
-    kgoff[i] = ((lane & 15) ^ (krow[i] & 15)) << 4;
-  }
-  const uint32_t lds0 = lds_addr(smem);
-  auto issue_k = [&](uint32_t buf, int kt) {
-    const uint32_t l = lds0 + buf * kK2Bytes + wave * 2 * 1024;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int key = min(kt * kBN2 + krow[i], p.seq_k - 1);
-      dma16(l + i * 1024, Kh, (uint32_t)key * kKRowBytes + kgoff[i]);
-    }
-  };
-  // V: thread t loads keys 2g, 2g+1 (g = t % 16) of d-chunk c = t / 16.
-  const int vg = threadIdx.x & 15, vc = threadIdx.x >> 4;
-  u32x4 vr[2];
-  auto load_v = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t key = (uint32_t)min(kt * kBN2 + 2 * vg + i, p.seq_k - 1);
-      vr[i] = gload16(Vh, key * kKRowBytes + 16 * vc);
-    }
-  };
-  // V^T position of keys 2g, 2g+1: 16-key groups stored as [0-3,8-11,4-7,12-15].
-  const int vk = (2 * vg) & 15;
-  const int vpos = 16 * (vg >> 3) + (vk < 4 ? vk : vk < 8 ? vk + 4 : vk < 12 ? vk - 4 : vk);
-  uint8_t *const vt0 = smem + kKRing * kK2Bytes;
-  uint32_t tr[8];
-  auto transpose_v = [&](int e) {  // dword e: d = 8*vc + 2e (lo), +1 (hi)
-    tr[2 * e] = __builtin_amdgcn_perm(vr[1][e], vr[0][e], 0x05040100u);
-    tr[2 * e + 1] = __builtin_amdgcn_perm(vr[1][e], vr[0][e], 0x07060302u);
-  };
-  auto store_vt = [&](uint32_t buf) {
-    uint8_t *s = vt0 + buf * kVt2Bytes + vpos * 2;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int d = 8 * vc + 2 * e;
-      *reinterpret_cast<uint32_t *>(s + d * kVt2Pitch) = tr[2 * e];
-      *reinterpret_cast<uint32_t *>(s + (d + 1) * kVt2Pitch) = tr[2 * e + 1];
-    }
-  };
-
-  const uint32_t kr = lane & 31;
-  const uint32_t vt_row = (lane & 31) * kVt2Pitch;
-  f32x16 o[2][4];
-  f32x16 lacc[2];
-#pragma unroll
-  for (int g = 0; g < 2; ++g) {
-    lacc[g] = f32x16{};
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      o[g][i] = f32x16{};
-  }
-  const u32x4 ones = {kOnePair<DT>, kOnePair<DT>, kOnePair<DT>, kOnePair<DT>};
-  float m[2] = {-__builtin_inff(), -__builtin_inff()};
-  const float c = p.scale_log2;
-  auto pin = [](auto x) { asm volatile("" ::"v"(x)); };
-
-  auto kfrag = [&](uint32_t kb, int kk) {
-    const uint32_t chunk = (2 * kk + half) ^ (kr & 15);
-    return *reinterpret_cast<const u32x4 *>(smem + kb * kK2Bytes + kr * kKRowBytes +
-                                            (chunk << 4));
-  };
-  auto mask = [&](f32x16 (&sc)[2], int t) {
-    const int k0 = t * kBN2;
-    const bool edge = (k0 + kBN2 > p.seq_k) || (p.causal && k0 + kBN2 - 1 > qw);
-    if (edge) {
-#pragma unroll
-      for (int g = 0; g < 2; ++g)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
-          if (key >= p.seq_k || (p.causal && key > my_q[g]))
-            sc[g][r] = -__builtin_inff();
-        }
-    }
-  };
-  auto update_max = [&](int g, float mx) {
-    const bool need = mx > m[g] + kRescaleThreshold;
-    if (__builtin_amdgcn_ballot_w64(need)) {
-      const float mn = fmaxf(m[g], mx);
-      const float alpha = (m[g] == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(m[g] - mn);
-      m[g] = mn;
-      lacc[g][0] *= alpha;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        o[g][i] *= alpha;
-    }
-  };
-  auto rowmax = [&](const f32x16 &s) {
-    float mx = s[0];
-#pragma unroll
-    for (int r = 1; r < 16; ++r)
-      mx = fmaxf(mx, s[r]);
-    return fmaxf(mx, __shfl_xor(mx, 32)) * c;
-  };
-
-  // Phase 1: S(t+1) (16 MFMAs: 8 K fragments x 2 query blocks) with
-  // P(t) = exp2(S(t)*c - m) (2 elements per step).
-  u32x4 pf[2][2];
-  auto phase1 = [&](f32x16 (&sn)[2], uint32_t kb, const f32x16 (&sc)[2]) {
-    u32x4 kf[8];
-    sn[0] = f32x16{};
-    sn[1] = f32x16{};
-    kf[0] = kfrag(kb, 0);
-    kf[1] = kfrag(kb, 1);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int kk = i >> 1, g = i & 1;
-      if (g == 0 && kk + 2 < 8)
-        kf[kk + 2] = kfrag(kb, kk + 2);
-      sn[g] = mfma32x32x16<DT>(kf[kk], qf[g][kk], sn[g]);
-      const int e = 2 * i, eg = e >> 4, r = e & 15;
-      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[eg][r], c, -m[eg]));
-      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[eg][r + 1], c, -m[eg]));
-      pf[eg][r >> 3][(r & 7) >> 1] = pack2<DT>(p0, p1);
-      pin(pf[eg][r >> 3][(r & 7) >> 1]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-  // Phase 2: O^T += V^T(t) P^T(t) and row sums (20 MFMAs) with the row max
-  // of S(t+1) and the transpose of V(t+1).  Returns both scaled maxima.
-  float mxo[2];
-  auto phase2 = [&](uint32_t vb, const f32x16 (&sn)[2], bool with_next) {
-    const uint8_t *vs = vt0 + vb * kVt2Bytes;
-    auto vfrag = [&](int sl, int dt) {
-      return *reinterpret_cast<const u32x4 *>(vs + dt * 32 * kVt2Pitch + vt_row +
-                                              (16 * sl + 8 * half) * 2);
-    };
-    u32x4 vf[8];
-    float mx[2] = {-__builtin_inff(), -__builtin_inff()};
-    vf[0] = vfrag(0, 0);
-    vf[1] = vfrag(0, 1);
-    int q = 0;
-#pragma unroll
-    for (int sl = 0; sl < 2; ++sl) {
-#pragma unroll
-      for (int x = 0; x < 5; ++x) {
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-          if (x < 4) {
-            const int fi = sl * 4 + x;
-            if (g == 0 && fi + 2 < 8)
-              vf[fi + 2] = vfrag((fi + 2) >> 2, (fi + 2) & 3);
-            o[g][x] = mfma32x32x16<DT>(vf[fi], pf[g][sl], o[g][x]);
-          } else {
-            lacc[g] = mfma32x32x16<DT>(ones, pf[g][sl], lacc[g]);
-          }
-          if (with_next) {
-            if (q < 16) {
-              const int mg = q >> 3, r = (2 * q) & 15;
-              mx[mg] = __builtin_fmaxf(__builtin_fmaxf(mx[mg], sn[mg][r]), sn[mg][r + 1]);
-              pin(mx[mg]);
-            } else {
-              transpose_v(q - 16);
-              pin(tr[2 * (q - 16)]);
-              pin(tr[2 * (q - 16) + 1]);
-            }
-          }
-          ++q;
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      }
-    }
-    mxo[0] = fmaxf(mx[0], __shfl_xor(mx[0], 32)) * c;
-    mxo[1] = fmaxf(mx[1], __shfl_xor(mx[1], 32)) * c;
-  };
-
-  // ---- pipeline -----------------------------------------------------------
-  f32x16 sc[2], sn[2];
-  issue_k(0, 0);
-  load_v(0);
-  vm_wait_regs<0>(vr[0], vr[1]);
-  lds_barrier();
-  issue_k(1, min(1, ntiles - 1));
-  issue_k(2, min(2, ntiles - 1));
-  {
-    // S(0), first row maxima, V^T(0).
-    sc[0] = f32x16{};
-    sc[1] = f32x16{};
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      const u32x4 kf = kfrag(0, kk);
-      sc[0] = mfma32x32x16<DT>(kf, qf[0][kk], sc[0]);
-      sc[1] = mfma32x32x16<DT>(kf, qf[1][kk], sc[1]);
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      transpose_v(e);
-    store_vt(0);
-    mask(sc, 0);
-    update_max(0, rowmax(sc[0]));
-    update_max(1, rowmax(sc[1]));
-  }
-  vm_wait_barrier<2>();
-  for (int t = 0; t + 1 < ntiles; ++t) {
-    const uint32_t vcur = t & 1;
-    load_v(t + 1);
-    issue_k(t % kKRing, min(t + 3, ntiles - 1));
-    phase1(sn, (t + 1) % kKRing, sc);
-    mask(sn, t + 1);
-    vm_wait_regs<2>(vr[0], vr[1]);  // V(t+1) landed; K DMA may stay in flight
-    phase2(vcur, sn, true);
-    store_vt(vcur ^ 1);
-    update_max(0, mxo[0]);
-    update_max(1, mxo[1]);
-    sc[0] = sn[0];
-    sc[1] = sn[1];
-    vm_wait_barrier<2>();
-  }
-  // Last tile: P and O += V P.
-#pragma unroll
-  for (int e = 0; e < 32; e += 2) {
-    const int eg = e >> 4, r = e & 15;
-    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[eg][r], c, -m[eg]));
-    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[eg][r + 1], c, -m[eg]));
-    pf[eg][r >> 3][(r & 7) >> 1] = pack2<DT>(p0, p1);
-  }
-  phase2((ntiles - 1) & 1, sn, false);
-  vm_wait_barrier();
-
-#pragma unroll
-  for (int g = 0; g < 2; ++g) {
-    const float lsum = lacc[g][0];
-    const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
-    if (my_q[g] < p.seq_q) {
-      uint16_t *orow = Oh + (size_t)my_q[g] * kD + 4 * half;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int gg = 0; gg < 4; ++gg) {
-          const u32x2 w = {pack2<DT>(o[g][dt][4 * gg] * inv, o[g][dt][4 * gg + 1] * inv),
-                           pack2<DT>(o[g][dt][4 * gg + 2] * inv, o[g][dt][4 * gg + 3] * inv)};
-          *reinterpret_cast<u32x2 *>(orow + 32 * dt + 8 * gg) = w;
-        }
-    }
   }
 }
 
