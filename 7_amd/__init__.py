@@ -5,14 +5,16 @@ The package directory name starts with a digit, so import it with
 ``importlib.import_module("7_amd")``.  The compute lives in
 ``libwave_runtime.so`` (hand-written HIP, C ABI in include/wave_runtime.h);
 ``ops`` wraps it for torch tensors and ``runtime`` is the ctypes binding.
+``code_object`` loads the reference-ABI code objects (``hsaco/*.hsaco``:
+the reference's kernel symbols, one shape each) with hipModuleLoad.
 """
 
-from . import runtime
+from . import code_object, runtime
 from .ops import (StreamKWorkspace, flash_attention, flash_attention_f32, gemm,
                   gemm_streamk, streamk_workspace_bytes)
 from .runtime import WaveError
 
 __all__ = [
-    "runtime", "gemm", "gemm_streamk", "StreamKWorkspace", "streamk_workspace_bytes",
+    "runtime", "code_object", "gemm", "gemm_streamk", "StreamKWorkspace", "streamk_workspace_bytes",
     "flash_attention", "flash_attention_f32", "WaveError",
 ]

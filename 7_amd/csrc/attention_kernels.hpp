@@ -65,10 +65,9 @@ struct Params {
   float scale_log2;  // softmax scale * log2(e)
 };
 
-template <int NW>
-__device__ __forceinline__ void block_coords(const Params &p, int &bh, int &qb) {
+// Linear CTA id -> (batch*head, query block).
+__device__ __forceinline__ void block_coords(const Params &p, int raw, int &bh, int &qb) {
   const int total = p.q_blocks * p.batch * p.q_heads;
-  const int raw = blockIdx.x;
   // Dispatch puts CTA i on XCD i % 8; make consecutive pids share an XCD.
   int pid = raw;
   if ((total & 7) == 0)
@@ -144,18 +143,21 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
   return v;
 }
 
+// LDS of one CTA: K ring [4][64 keys][256 B] (XOR-swizzled chunks), V^T ring
+// [2][128 d][144 B].
+constexpr int kPPSmem = kKRingPP * kKBytes + 2 * kVtBytes;
+
+// CTA `raw` of a grid of q_blocks * batch * q_heads CTAs of 512 threads.
+// smem: kPPSmem bytes of 1024-byte-aligned LDS.
 template <int DT>
-__global__ __launch_bounds__(512, 1) void fwd_pp_kernel(Params p) {
-  // LDS: K ring [4][64 keys][256 B] (XOR-swizzled chunks), V^T ring
-  // [2][128 d][144 B].
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kKRingPP * kKBytes + 2 * kVtBytes];
+__device__ __forceinline__ void fwd_pp_cta(const Params &p, int raw, uint8_t *smem) {
   constexpr int kRows = 32 * kPPWaves;
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t grp = wave >> 2;
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t half = lane >> 5;
   int bh, qb;
-  block_coords<kPPWaves>(p, bh, qb);
+  block_coords(p, raw, bh, qb);
   const int b = bh / p.q_heads, hq = bh - b * p.q_heads;
   const int hkv = hq / (p.q_heads / p.kv_heads);
   const uint16_t *Qh = p.Q + ((size_t)bh * p.seq_q) * kD;
@@ -482,6 +484,12 @@ __global__ __launch_bounds__(512, 1) void fwd_pp_kernel(Params p) {
         *reinterpret_cast<u32x2 *>(orow + 32 * dt + 8 * g) = w;
       }
   }
+}
+
+template <int DT>
+__global__ __launch_bounds__(512, 1) void fwd_pp_kernel(Params p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kPPSmem];
+  fwd_pp_cta<DT>(p, blockIdx.x, smem);
 }
 
 } // namespace attention

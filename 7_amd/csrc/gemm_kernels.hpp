@@ -446,12 +446,13 @@ __device__ __forceinline__ void store_tile(const Params &p, int m0, int n0,
   }
 }
 
+// One 256x256 output tile: CTA `raw` of a grid of tiles_m * tiles_n CTAs.
+// smem: DefaultCfg::SMEM bytes of 1024-byte-aligned LDS.
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
-__global__ __launch_bounds__(DefaultCfg::THREADS, 1) void tiled_kernel(Params p) {
+__device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *smem) {
   using C = DefaultCfg;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::SMEM];
   int tm, tn;
-  tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, p.group_m, true, tm, tn);
+  tile_coords(raw, p.tiles_m, p.tiles_n, p.group_m, true, tm, tn);
   const int m0 = tm * kTile, n0 = tn * kTile;
   f32x16 acc[C::TP][C::TQ];
 #pragma unroll
@@ -465,6 +466,12 @@ __global__ __launch_bounds__(DefaultCfg::THREADS, 1) void tiled_kernel(Params p)
     return f32x4{acc[tp][tq][4 * g], acc[tp][tq][4 * g + 1],
                  acc[tp][tq][4 * g + 2], acc[tp][tq][4 * g + 3]};
   });
+}
+
+template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
+__global__ __launch_bounds__(DefaultCfg::THREADS, 1) void tiled_kernel(Params p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[DefaultCfg::SMEM];
+  tiled_cta<IN_DT, OUT_DT, COL_MAJOR, MASKED, VEC>(p, blockIdx.x, smem);
 }
 
 // ---------------------------------------------------------------- Stream-K
@@ -501,12 +508,12 @@ __device__ __forceinline__ int sk_slot(int total, int workers, int w, int tile,
 // Per-thread scratch layout: element e (0 .. 65536/THREADS - 1) of thread
 // t's share of the 256x256 tile lives at slot_base + e * THREADS + t, so
 // publishing and reducing are fully coalesced and need no coordinate math.
+// Worker `worker` of p.workers.  smem: DefaultCfg::SMEM bytes of
+// 1024-byte-aligned LDS; arrival: one int of LDS.
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
-__global__ __launch_bounds__(DefaultCfg::THREADS, 1) void streamk_kernel(Params p) {
+__device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t *smem,
+                                            int *arrival) {
   using C = DefaultCfg;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::SMEM];
-  __shared__ int arrival;
-  const int worker = blockIdx.x;
   const int tiles = p.tiles_m * p.tiles_n;
   const int iters = (p.K + kSKUnit - 1) / kSKUnit;
   const int ksteps = (p.K + C::BK - 1) / C::BK;  // mainloop steps per tile
@@ -577,10 +584,10 @@ __global__ __launch_bounds__(DefaultCfg::THREADS, 1) void streamk_kernel(Params 
     __threadfence();  // release the partial at device scope
     __syncthreads();
     if (threadIdx.x == 0)
-      arrival = __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_ACQ_REL,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+      *arrival = __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_ACQ_REL,
+                                        __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    if (arrival != parts - 1)
+    if (*arrival != parts - 1)
       continue;
     // Last arriver: reduce all contributors' partials in worker order (a
     // fixed order, so the result does not depend on arrival order).
@@ -605,6 +612,13 @@ __global__ __launch_bounds__(DefaultCfg::THREADS, 1) void streamk_kernel(Params 
       __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELEASE,
                          __HIP_MEMORY_SCOPE_AGENT);
   }
+}
+
+template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
+__global__ __launch_bounds__(DefaultCfg::THREADS, 1) void streamk_kernel(Params p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[DefaultCfg::SMEM];
+  __shared__ int arrival;
+  streamk_cta<IN_DT, OUT_DT, COL_MAJOR, MASKED, VEC>(p, blockIdx.x, smem, &arrival);
 }
 
 // ------------------------------------------------------------- launchers

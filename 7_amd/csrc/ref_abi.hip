@@ -1,0 +1,191 @@
+// ref_abi.hip -- the reference's device-side kernel ABI, for code objects
+// that its runners and host flows load with hipModuleLoad.
+//
+// The reference compiles one kernel per shape and launches it by symbol with
+// bare-pointer arguments (gpu-to-llvm{use-bare-pointers-for-kernels=true};
+// examples/wave/common.py:279-288).  This file gives the same symbols and
+// argument lists; the shape and element types are compile-time constants set
+// with -D when the code object is built (Makefile target `hsaco`):
+//
+//   wmma_f16_matmul_tiled(const T* A, const T* B, C_t* C, int32 trip)
+//     (wave_matmul.py:11415-11427, :6954-6982; runner.cpp:1790-1791).
+//     -DWAVE_ABI_GEMM -DWAVE_ABI_M= -DWAVE_ABI_N= -DWAVE_ABI_K=
+//     -DWAVE_ABI_IN=kF16|kBF16 -DWAVE_ABI_OUT=kF32|kF16|kBF16 -DWAVE_ABI_CM=0|1
+//   gfx950_f16_streamk_gemm(const f16* A, const f16* B, f16* C, f32* scratch,
+//                           u32* counters, int32 workers)
+//     (wave_matmul.py:11556-11567; runner.cpp:1811-1816; column-major C,
+//     runner.cpp:433-440).  -DWAVE_ABI_SK -DWAVE_ABI_SK_M= _N= _K=
+//   flash_attention_bf16_gfx950(const bf16* Q, const bf16* K, const bf16* V,
+//                               bf16* O)
+//     (wave_flash_attention.py:1723-1728; runner wave-fa-gfx950-runner.cpp
+//     :396-402).  -DWAVE_ABI_FA -DWAVE_ABI_FA_B= -DWAVE_ABI_FA_H= -DWAVE_ABI_FA_S=
+//   flash_attention_f32(const f16* Q, const f16* K, const f16* V, f32* O)
+//     (wave_attention.py:1436-1441; runner wave-fa-calibrate-runner.cpp
+//     :346-361).  -DWAVE_ABI_FA32 -DWAVE_ABI_FA32_M= _N= _D=
+//
+// Launch contract (what the reference's runners pass):
+//  * wmma_f16_matmul_tiled: any grid (the runner's (M_blocks, N_blocks) for
+//    its tiling); CTAs walk this build's 256x256 tiles in a grid-stride loop.
+//    Block 256 threads and >= 131072 bytes of dynamic LDS (the reference's
+//    gfx950 4-wave profile passes exactly that).  `trip` is accepted and
+//    unused: the K loop length follows from the baked K.
+//  * gfx950_f16_streamk_gemm: grid (workers), block 256, >= 131076 bytes of
+//    dynamic LDS; workspace as wave_gemm_streamk_workspace_bytes.
+//  * flash_attention_bf16_gfx950: grid (S/256, B*H), block 512, >= 102400
+//    bytes of dynamic LDS (the reference's 8-wave profile passes 136192).
+//    Non-causal, one KV head per query head, scale 1/sqrt(128).
+//  * flash_attention_f32: grid (1,1,1), any block size up to 1024; LDS is
+//    static.
+// A launch with another block size or grid than the one stated, or with
+// less dynamic LDS than stated, returns without writing anything; so does a
+// GEMM launch whose A/B (16 bytes) or C (4 elements) lack the alignment its
+// load path needs (hipMalloc'd buffers always have it).  The FA runner's
+// default --dynamic-lds (68096, its 4-wave setting) is too small for this
+// 8-wave kernel: pass --threads 512 --dynamic-lds 136192.
+#include "attention_kernels.hpp"
+#include "fa_small.hpp"
+#include "gemm_kernels.hpp"
+
+using namespace wave;
+
+namespace {
+[[maybe_unused]] __device__ __forceinline__ bool aligned16(const void *p) {
+  return ((uintptr_t)p & 15u) == 0;
+}
+// The baked shape reaches the kernel body as an opaque scalar, so the body
+// compiles exactly as in the shape-generic library kernels (constant shapes
+// would let the compiler specialise the tile loops, at a register cost).
+[[maybe_unused]] __device__ __forceinline__ int runtime_int(int v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+// Dynamic LDS bytes of this launch: the hidden_dynamic_lds_size implicit
+// kernel argument (code object v5, offset 120 of the implicit arguments).
+[[maybe_unused]] __device__ __forceinline__ uint32_t dynamic_lds_bytes() {
+  return *reinterpret_cast<const uint32_t *>(
+      static_cast<const char *>(__builtin_amdgcn_implicitarg_ptr()) + 120);
+}
+} // namespace
+
+#ifdef WAVE_ABI_GEMM
+extern "C" __global__ __launch_bounds__(256, 1) void wmma_f16_matmul_tiled(
+    const uint16_t *A, const uint16_t *B, void *C, int trip) {
+  using namespace wave::gemm;
+  static_assert(DefaultCfg::THREADS == 256, "tile kernel is built for 4 waves");
+  extern __shared__ __attribute__((aligned(1024))) uint8_t dsmem[];
+  (void)trip;
+  if (blockDim.x != 256 || blockDim.y != 1 || blockDim.z != 1 ||
+      dynamic_lds_bytes() < (uint32_t)DefaultCfg::SMEM)
+    return;
+  constexpr int M = WAVE_ABI_M, N = WAVE_ABI_N, K = WAVE_ABI_K;
+  constexpr bool CM = WAVE_ABI_CM != 0;
+  constexpr int OUT_BYTES = WAVE_ABI_OUT == kF32 ? 4 : 2;
+  static_assert(M > 0 && N > 0 && K > 0, "shape");
+  Params p{};
+  p.A = A;
+  p.B = B;
+  p.C = C;
+  p.M = runtime_int(M);
+  p.N = runtime_int(N);
+  p.K = runtime_int(K);
+  p.tiles_m = (p.M + kTile - 1) / kTile;
+  p.tiles_n = (p.N + kTile - 1) / kTile;
+  p.group_m = min(4, p.tiles_m);
+  p.ldc = CM ? p.M : p.N;
+  p.c_vec_ok = (p.ldc % 4 == 0) && (((uintptr_t)C % (4 * OUT_BYTES)) == 0);
+  // One load path per code object, chosen from the baked shape like the
+  // host dispatcher does: the DMA fast path for whole tiles, else the masked
+  // path with 16-byte (K % 8 == 0) or 2-byte loads.
+  constexpr bool kFast = M % kTile == 0 && N % kTile == 0 && K % DefaultCfg::BK == 0 &&
+                         (CM ? M : N) % 4 == 0;
+  constexpr int kVec = kFast || K % 8 == 0 ? 8 : 1;
+  if (kVec == 8 && !(aligned16(A) && aligned16(B)))
+    return;
+  if (kFast && !p.c_vec_ok)
+    return;
+  const int tiles = p.tiles_m * p.tiles_n;
+  const int ctas = gridDim.x * gridDim.y;
+  for (int raw = blockIdx.y * gridDim.x + blockIdx.x; raw < tiles; raw += ctas)
+    tiled_cta<WAVE_ABI_IN, WAVE_ABI_OUT, CM, !kFast, kVec>(p, raw, dsmem);
+}
+#endif
+
+#ifdef WAVE_ABI_SK
+extern "C" __global__ __launch_bounds__(256, 1) void gfx950_f16_streamk_gemm(
+    const uint16_t *A, const uint16_t *B, uint16_t *C, float *scratch, uint32_t *counters,
+    int workers) {
+  using namespace wave::gemm;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t dsmem[];
+  if (blockDim.x != 256 || blockDim.y != 1 || blockDim.z != 1 || workers <= 0 ||
+      (int)gridDim.x != workers || dynamic_lds_bytes() < (uint32_t)DefaultCfg::SMEM + 4)
+    return;
+  constexpr int M = WAVE_ABI_SK_M, N = WAVE_ABI_SK_N, K = WAVE_ABI_SK_K;
+  static_assert(M > 0 && N > 0 && K > 0, "shape");
+  Params p{};
+  p.A = A;
+  p.B = B;
+  p.C = C;
+  p.M = runtime_int(M);
+  p.N = runtime_int(N);
+  p.K = runtime_int(K);
+  p.tiles_m = (p.M + kTile - 1) / kTile;
+  p.tiles_n = (p.N + kTile - 1) / kTile;
+  p.group_m = min(4, p.tiles_m);
+  p.ldc = p.M;  // column-major C
+  p.c_vec_ok = (M % 4 == 0) && (((uintptr_t)C % 8) == 0);
+  p.scratch = scratch;
+  p.counters = counters;
+  p.workers = workers;
+  int *arrival = reinterpret_cast<int *>(dsmem + DefaultCfg::SMEM);
+  constexpr bool kFast = M % kTile == 0 && N % kTile == 0 && K % DefaultCfg::BK == 0 &&
+                         M % 4 == 0;
+  constexpr int kVec = kFast || K % 8 == 0 ? 8 : 1;
+  if (kVec == 8 && !(aligned16(A) && aligned16(B)))
+    return;
+  if (kFast && !p.c_vec_ok)
+    return;
+  streamk_cta<kF16, kF16, true, !kFast, kVec>(p, blockIdx.x, dsmem, arrival);
+}
+#endif
+
+#ifdef WAVE_ABI_FA
+extern "C" __global__ __launch_bounds__(512, 1) void flash_attention_bf16_gfx950(
+    const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint16_t *O) {
+  using namespace wave::attention;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t dsmem[];
+  constexpr int B = WAVE_ABI_FA_B, H = WAVE_ABI_FA_H, S = WAVE_ABI_FA_S;
+  static_assert(B > 0 && H > 0 && S > 0, "shape");
+  constexpr int kQBlocks = (S + 32 * kPPWaves - 1) / (32 * kPPWaves);
+  if (blockDim.x != 64 * kPPWaves || blockDim.y != 1 || blockDim.z != 1 ||
+      (int)(gridDim.x * gridDim.y) != kQBlocks * B * H || dynamic_lds_bytes() < (uint32_t)kPPSmem)
+    return;
+  Params p{};
+  p.Q = Q;
+  p.K = K;
+  p.V = V;
+  p.O = O;
+  p.batch = runtime_int(B);
+  p.q_heads = runtime_int(H);
+  p.kv_heads = p.q_heads;
+  p.seq_q = runtime_int(S);
+  p.seq_k = p.seq_q;
+  p.q_blocks = runtime_int(kQBlocks);
+  p.causal = runtime_int(0);
+  // 1/sqrt(128) * log2(e), in the same float operations as the host path.
+  p.scale_log2 = (1.0f / 11.313708498984761f) * kLog2e;
+  fwd_pp_cta<kBF16>(p, blockIdx.y * gridDim.x + blockIdx.x, dsmem);
+}
+#endif
+
+#ifdef WAVE_ABI_FA32
+extern "C" __global__ __launch_bounds__(1024) void flash_attention_f32(
+    const _Float16 *Q, const _Float16 *K, const _Float16 *V, float *O) {
+  constexpr int M = WAVE_ABI_FA32_M, N = WAVE_ABI_FA32_N, D = WAVE_ABI_FA32_D;
+  static_assert(M > 0 && N > 0 && D > 0 && N <= 16384, "shape");
+  __shared__ float weights[N];
+  __shared__ float red[1024];
+  if (blockDim.y != 1 || blockDim.z != 1)
+    return;
+  wave::attention::small_cta(Q, K, V, O, M, N, D, weights, red);
+}
+#endif

@@ -129,3 +129,81 @@ def test_product_does_not_import_oracle():
                 text = open(os.path.join(dirpath, f)).read()
                 assert not re.search(r"liboracle|import oracle|from oracle|oracle\.h|oracle/",
                                      text), f
+
+
+# Reference kernel symbol -> kernarg bytes of its bare-pointer argument list
+# (pointers 8 bytes, int32 4 bytes, before the hidden arguments).
+ABI_SYMBOLS = {
+    "gemm_": ("wmma_f16_matmul_tiled", 3 * 8 + 4),
+    "streamk_": ("gfx950_f16_streamk_gemm", 5 * 8 + 4),
+    "fa_bf16_": ("flash_attention_bf16_gfx950", 4 * 8),
+    "fa32_": ("flash_attention_f32", 4 * 8),
+}
+
+
+def test_code_objects_export_reference_symbols():
+    """Every built code object (7_amd/hsaco) is a plain gfx950 ELF whose one
+    kernel carries the reference's symbol name and explicit argument list."""
+    import glob
+    import os
+    import shutil
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    objs = sorted(glob.glob(os.path.join(root, "7_amd", "hsaco", "*.hsaco")))
+    assert objs, "code objects are built by make -C 7_amd/csrc (hsacos)"
+    readelf = shutil.which("llvm-readelf") or "/opt/rocm/llvm/bin/llvm-readelf"
+    if not os.path.exists(readelf):
+        pytest.skip("llvm-readelf not available")
+    for path in objs:
+        name = os.path.basename(path)
+        symbol, explicit = next(v for k, v in ABI_SYMBOLS.items() if name.startswith(k))
+        with open(path, "rb") as f:
+            assert f.read(4) == b"\x7fELF", name
+        notes = subprocess.run([readelf, "--notes", path], capture_output=True, text=True,
+                               check=True).stdout
+        assert "amdgcn-amd-amdhsa--gfx950" in notes, name
+        assert f".name:           {symbol}\n" in notes, name
+        assert ".vgpr_spill_count: 0" in notes or "bf16_cm" in name, name
+        # Explicit (non-hidden) kernel arguments end at `explicit` bytes.
+        args, cur = [], None
+        for line in notes.split(".args:")[1].split(".group_segment_fixed_size")[0].splitlines():
+            line = line.strip()
+            if line.startswith("- "):
+                cur = {}
+                args.append(cur)
+                line = line[2:]
+            if cur is not None and ":" in line:
+                key, val = (x.strip() for x in line.split(":", 1))
+                cur[key] = val
+        explicit_args = [a for a in args if not a[".value_kind"].startswith("hidden")]
+        end = max(int(a[".offset"]) + int(a[".size"]) for a in explicit_args)
+        assert end == explicit, (name, end)
+
+
+def test_kernel_abi_header_matches_code_objects(tmp_path):
+    """include/wave_kernel_abi.h's argument blocks end where the code
+    objects' explicit kernel arguments end (the kernarg layout the runners
+    fill through hipModuleLaunchKernel)."""
+    import os
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    src = tmp_path / "abi.c"
+    src.write_text(
+        '#include <stddef.h>\n#include <stdio.h>\n#include "wave_kernel_abi.h"\n'
+        "#define END(T, f) (unsigned)(offsetof(T, f) + sizeof(((T *)0)->f))\n"
+        "int main(void) {\n"
+        '  printf("%s %u\\n", WAVE_ABI_MATMUL_SYMBOL, END(wave_abi_matmul_args, trip));\n'
+        '  printf("%s %u\\n", WAVE_ABI_STREAMK_SYMBOL, END(wave_abi_streamk_args, workers));\n'
+        '  printf("%s %u\\n", WAVE_ABI_FA_SYMBOL, END(wave_abi_fa_args, O));\n'
+        '  printf("%s %u\\n", WAVE_ABI_FA32_SYMBOL, END(wave_abi_fa32_args, O));\n'
+        "  return 0;\n}\n")
+    exe = tmp_path / "abi"
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Werror", "-I", os.path.join(root, "include"),
+                    str(src), "-o", str(exe)], check=True)
+    out = dict(line.split() for line in subprocess.run(
+        [str(exe)], capture_output=True, text=True, check=True).stdout.splitlines())
+    assert {k: int(v) for k, v in out.items()} == {sym: end for sym, end in ABI_SYMBOLS.values()}

@@ -1,0 +1,203 @@
+"""The reference's device-side kernel ABI: code objects built from
+7_amd/csrc/ref_abi.hip, loaded with hipModuleLoad and launched with
+hipModuleLaunchKernel exactly as the reference's runners do (grid, block,
+dynamic LDS and bare-pointer arguments), checked against the oracle.
+
+* wmma_f16_matmul_tiled(A, B, C, trip): grid (M_blocks, N_blocks) of the
+  runner's tiling (wave-matmul-calibrate-runner.cpp:1114-1131, :1745-1762),
+  block 256, dynamic LDS 131072 (the reference's gfx950 4-wave profile).
+  Bucket inputs make every result bit-exact (wave_mfma_tiled.mlir:9).
+* gfx950_f16_streamk_gemm(A, B, C, scratch, counters, workers): grid
+  (workers), block 256; column-major C; counters back at zero afterwards
+  (runner.cpp:1718-1742).
+* flash_attention_bf16_gfx950(Q, K, V, O): grid (S/256, B*H), block 512,
+  dynamic LDS 136192 (wave-fa-gfx950-runner.cpp:396-428); tolerance 2e-2.
+* flash_attention_f32(Q, K, V, O): grid 1, the runner's --threads
+  (wave-fa-calibrate-runner.cpp:346-361); tolerance 3e-3 (:263).
+"""
+
+import importlib
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import to_bits, to_dev
+
+pytestmark = pytest.mark.gpu
+
+GEMM_LDS = 131072
+FA_LDS = 136192
+
+
+@pytest.fixture(scope="module")
+def co():
+    return importlib.import_module("7_amd.code_object")
+
+
+def bucket_gemm(oracle, dev, M, N, K, dt, seed):
+    a = oracle.gemm_inputs(M, K, dt, seed, 0)
+    b = oracle.gemm_inputs(N, K, dt, seed, 1)
+    tdt = {1: torch.float16, 2: torch.bfloat16}[dt]
+    return a, b, to_dev(a, tdt, dev), to_dev(b, tdt, dev)
+
+
+def launch_tiled(co, name, grid, A, B, C, block=256, trip=0):
+    with co.CodeObject(name) as mod:
+        mod.kernel("wmma_f16_matmul_tiled").launch(grid, (block,), [A, B, C, trip],
+                                                   dynamic_lds=GEMM_LDS)
+        torch.cuda.synchronize()
+
+
+def test_tiled_config1_bit_exact(co, oracle, dev):
+    """32x32x64 f16 -> f32 row-major, seed 7, BM=BN=2 wmt=wnt=1: grid (1,1)."""
+    a, b, A, B = bucket_gemm(oracle, dev, 32, 32, 64, 1, 7)
+    C = torch.zeros((32, 32), dtype=torch.float32, device=dev)
+    launch_tiled(co, "gemm_f16_f32_rm_32x32x64", (1, 1), A, B, C)
+    assert np.array_equal(C.cpu().numpy(), oracle.gemm_nt(a, b, 1))
+
+
+def test_tiled_64x96x64_runner_grid(co, oracle, dev):
+    """wave_mfma_tiled.mlir:3-9 (seed 37, max_abs_diff 0.0) with the runner's
+    grid for 32x32 CTA blocks: 2 x 3 CTAs over one 256x256 tile."""
+    a, b, A, B = bucket_gemm(oracle, dev, 64, 96, 64, 1, 37)
+    C = torch.full((64, 96), float("nan"), dtype=torch.float32, device=dev)
+    launch_tiled(co, "gemm_f16_f32_rm_64x96x64", (2, 3), A, B, C)
+    assert np.array_equal(C.cpu().numpy(), oracle.gemm_nt(a, b, 1))
+
+
+@pytest.mark.parametrize("grid", [(2, 2), (1, 1), (3, 1), (16, 16)])
+def test_tiled_512_any_grid(co, oracle, dev, grid):
+    """512^3 f16 -> f16: the runner's 256x256 grid (2,2), fewer CTAs than
+    tiles (grid-stride loop) and more (the extra CTAs exit)."""
+    a, b, A, B = bucket_gemm(oracle, dev, 512, 512, 512, 1, 11)
+    C = torch.zeros((512, 512), dtype=torch.float16, device=dev)
+    launch_tiled(co, "gemm_f16_f16_rm_512x512x512", grid, A, B, C)
+    exp = oracle.round_output(oracle.gemm_nt(a, b, 1), 1)
+    assert np.array_equal(to_bits(C), exp)
+
+
+def test_tiled_ragged_bf16_column_major(co, oracle, dev):
+    """300x200x100 bf16 -> bf16, column-major C (masked load path)."""
+    a, b, A, B = bucket_gemm(oracle, dev, 300, 200, 100, 2, 5)
+    C = torch.zeros((200, 300), dtype=torch.bfloat16, device=dev)  # C^T row-major
+    launch_tiled(co, "gemm_bf16_bf16_cm_300x200x100", (2, 1), A, B, C)
+    exp = oracle.round_output(oracle.gemm_nt(a, b, 2), 2)
+    assert np.array_equal(to_bits(C).T, exp)
+
+
+def test_tiled_8192_matches_c_abi(co, wave, dev):
+    """The 8192^3 code object computes what wave_gemm_launch computes, bit
+    for bit (same tiles, same kernel body), on uniform [-1, 1) inputs."""
+    g = torch.Generator(device="cpu").manual_seed(7)
+    A = (torch.rand((8192, 8192), generator=g) * 2 - 1).to(torch.float16).to(dev)
+    B = (torch.rand((8192, 8192), generator=g) * 2 - 1).to(torch.float16).to(dev)
+    C = torch.empty((8192, 8192), dtype=torch.float16, device=dev)
+    launch_tiled(co, "gemm_f16_f16_rm_8192x8192x8192", (32, 32), A, B, C)
+    ref = wave.gemm(A, B, out_dtype=torch.float16)
+    torch.cuda.synchronize()
+    assert torch.equal(C, ref)
+
+
+def test_tiled_wrong_block_writes_nothing(co, oracle, dev):
+    """A launch with a block size the code object is not built for returns
+    without touching C."""
+    _, _, A, B = bucket_gemm(oracle, dev, 32, 32, 64, 1, 7)
+    C = torch.full((32, 32), 3.0, dtype=torch.float32, device=dev)
+    launch_tiled(co, "gemm_f16_f32_rm_32x32x64", (1, 1), A, B, C, block=128)
+    assert bool((C == 3.0).all())
+
+
+def test_tiled_too_little_lds_writes_nothing(co, oracle, dev):
+    """Less dynamic LDS than the 4-stage ring needs: the kernel reads the
+    launch's size (hidden_dynamic_lds_size) and returns."""
+    _, _, A, B = bucket_gemm(oracle, dev, 32, 32, 64, 1, 7)
+    C = torch.full((32, 32), 3.0, dtype=torch.float32, device=dev)
+    with co.CodeObject("gemm_f16_f32_rm_32x32x64") as mod:
+        mod.kernel("wmma_f16_matmul_tiled").launch((1, 1), (256,), [A, B, C, 0],
+                                                   dynamic_lds=GEMM_LDS - 1024)
+        torch.cuda.synchronize()
+    assert bool((C == 3.0).all())
+
+
+@pytest.mark.parametrize("workers", [6, 7, 13, 64])
+def test_streamk_runner_launch(co, wave, oracle, dev, workers):
+    """512x768x1024 f16, column-major f16 C: 6 tiles x 16 K units; 6 workers
+    is the aligned case, the others split tiles across workers."""
+    M, N, K = 512, 768, 1024
+    a, b, A, B = bucket_gemm(oracle, dev, M, N, K, 1, 3)
+    sb, cb = wave.streamk_workspace_bytes(M, N, workers)
+    scratch = torch.empty(sb // 4, dtype=torch.float32, device=dev)
+    counters = torch.zeros(cb // 4, dtype=torch.int32, device=dev)
+    C = torch.zeros((N, M), dtype=torch.float16, device=dev)  # column-major M x N
+    with co.CodeObject("streamk_f16_512x768x1024") as mod:
+        mod.kernel("gfx950_f16_streamk_gemm").launch(
+            (workers,), (256,), [A, B, C, scratch, counters, workers],
+            dynamic_lds=GEMM_LDS + 4)
+        torch.cuda.synchronize()
+    exp = oracle.round_output(oracle.gemm_nt(a, b, 1), 1)
+    assert np.array_equal(to_bits(C).T, exp)
+    assert int(counters.count_nonzero()) == 0
+
+
+def test_fa_bf16_runner_launch(co, wave, oracle, dev):
+    """B1 H2 S512 bf16 with the reference's bucket inputs (runner :194-202),
+    grid (S/256, B*H) = (2, 2), block 512, dynamic LDS 136192: every row
+    within 2e-2 of the double-precision reference, and bit-identical to
+    wave_fa_fwd_launch."""
+    Bt, H, S, D = 1, 2, 512, 128
+    q, k, v = oracle.fa_gfx950_inputs(Bt * H * S * D, 3, 1)
+    Q, Kt, V = (to_dev(x, torch.bfloat16, dev).view(Bt, H, S, D) for x in (q, k, v))
+    O = torch.zeros_like(Q)
+    with co.CodeObject("fa_bf16_b1_h2_s512") as mod:
+        mod.kernel("flash_attention_bf16_gfx950").launch(
+            (S // 256, Bt * H), (512,), [Q, Kt, V, O], dynamic_lds=FA_LDS)
+        torch.cuda.synchronize()
+    got = oracle.bits_to_f32(to_bits(O).reshape(Bt * H, S, D), 2)
+    hh, rr = np.meshgrid(np.arange(H), np.arange(S), indexing="ij")
+    ref = oracle.attention_rows(q, k, v, dtype=2, batch=Bt, q_heads=H, kv_heads=H, seq_q=S,
+                                seq_k=S, head_dim=D, causal=False, scale=1.0 / math.sqrt(D),
+                                heads=hh.ravel(), rows=rr.ravel())
+    assert float(np.abs(got[hh.ravel(), rr.ravel()] - ref).max()) <= 2e-2
+    assert torch.equal(O, wave.flash_attention(Q, Kt, V))
+
+
+@pytest.mark.parametrize("lds", [68096, 102400 - 16])
+def test_fa_bf16_too_little_lds_writes_nothing(co, oracle, dev, lds):
+    """The runner's 4-wave default --dynamic-lds (68096) is too small for the
+    8-wave kernel (102400): it returns without writing O."""
+    Bt, H, S, D = 1, 2, 512, 128
+    q, k, v = oracle.fa_gfx950_inputs(Bt * H * S * D, 3, 1)
+    Q, Kt, V = (to_dev(x, torch.bfloat16, dev).view(Bt, H, S, D) for x in (q, k, v))
+    O = torch.full_like(Q, 5.0)
+    with co.CodeObject("fa_bf16_b1_h2_s512") as mod:
+        mod.kernel("flash_attention_bf16_gfx950").launch(
+            (S // 256, Bt * H), (512,), [Q, Kt, V, O], dynamic_lds=lds)
+        torch.cuda.synchronize()
+    assert bool((O == 5.0).all())
+
+
+def test_fa_bf16_exact_lds_minimum(co, wave, oracle, dev):
+    """102400 bytes (the kernel's K and V^T rings) is enough."""
+    Bt, H, S, D = 1, 2, 512, 128
+    q, k, v = oracle.fa_gfx950_inputs(Bt * H * S * D, 4, 1)
+    Q, Kt, V = (to_dev(x, torch.bfloat16, dev).view(Bt, H, S, D) for x in (q, k, v))
+    O = torch.zeros_like(Q)
+    with co.CodeObject("fa_bf16_b1_h2_s512") as mod:
+        mod.kernel("flash_attention_bf16_gfx950").launch(
+            (S // 256, Bt * H), (512,), [Q, Kt, V, O], dynamic_lds=102400)
+        torch.cuda.synchronize()
+    assert torch.equal(O, wave.flash_attention(Q, Kt, V))
+
+
+@pytest.mark.parametrize("threads", [64, 32, 256])
+def test_fa_f32_runner_launch(co, oracle, dev, threads):
+    """block_m 16, seq_n 256, head_dim 64, grid 1, the runner's --threads."""
+    q, k, v = oracle.fa_f32_inputs(16, 256, 64, 9)
+    Q, Kt, V = (to_dev(x, torch.float16, dev) for x in (q, k, v))
+    O = torch.zeros((16, 64), dtype=torch.float32, device=dev)
+    with co.CodeObject("fa32_m16_n256_d64") as mod:
+        mod.kernel("flash_attention_f32").launch((1,), (threads,), [Q, Kt, V, O])
+        torch.cuda.synchronize()
+    assert float(np.abs(O.cpu().numpy() - oracle.fa_f32_reference(q, k, v)).max()) <= 3e-3
