@@ -9,13 +9,23 @@
 //   wave-bench gemm [--m M] [--n N] [--k K] [--input-type f16|bf16]
 //                   [--c-type f32|f16|bf16] [--output-layout row-major|column-major]
 //                   [--streamk-workers W] [--iters N] [--warmup N] [--repeats R]
-//                   [--seed S]
+//                   [--seed S] [--input-mode uniform|normal|bucket|rand-int|hpl|all-ones]
+//                   [--rand-int] [--hpl] [--all-ones] [--check]
 //   wave-bench fa   [--batch B] [--heads H] [--kv-heads H] [--sequence S]
 //                   [--dtype f16|bf16] [--causal] [--iters N] [--warmup N]
-//                   [--repeats R] [--seed S]
+//                   [--repeats R] [--seed S] [--check]
 //
-// Parity is checked by the test suite, not here.
-// Exit codes follow the runners: 2 for bad arguments, 1 for HIP failures.
+// Input modes: uniform [-1, 1) and N(0,1)/sqrt(K)
+// (config 3) from a seeded std::mt19937_64; bucket, rand-int, hpl and
+// all-ones restate the reference runner's generators (runner.cpp:681-716,
+// :1143-1186), e.g. for comparison with its rand_int profile numbers.
+// --check samples outputs against a host fp32 (GEMM) or double (FA)
+// reference with the runner's tolerances (1e-2 + 1e-3*|expected|,
+// runner.cpp:942, plus one ulp of a 16-bit output; 3e-2 for FA,
+// wave-fa-gfx950-runner.cpp:388) and prints the runner's `output_check:`
+// line; the full parity suite is tests/.
+// Exit codes follow the runners: 2 for bad arguments, 1 for HIP failures or
+// a failed check.
 #include "../../include/wave_runtime.h"
 
 #include <hip/hip_runtime.h>
@@ -88,6 +98,18 @@ int dtype_of(const std::string &s) {
   die("unknown dtype " + s);
 }
 
+float from_bits(uint16_t b, int dtype) {
+  if (dtype == WAVE_F16) {
+    _Float16 h;
+    std::memcpy(&h, &b, 2);
+    return (float)h;
+  }
+  uint32_t u = (uint32_t)b << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
 uint16_t to_bits(float v, int dtype) {
   if (dtype == WAVE_F16) {
     _Float16 h = (_Float16)v;
@@ -101,15 +123,69 @@ uint16_t to_bits(float v, int dtype) {
   return (uint16_t)(u >> 16);
 }
 
-// Uniform [-1, 1) or N(0, 1) * scale values, 16-bit storage.
-std::vector<uint16_t> synth(size_t n, int dtype, uint64_t seed, bool normal, float scale) {
+enum class Mode { Uniform, Normal, Bucket, RandInt, Hpl, AllOnes };
+
+Mode mode_of(const std::string &s) {
+  if (s == "uniform") return Mode::Uniform;
+  if (s == "normal") return Mode::Normal;
+  if (s == "bucket") return Mode::Bucket;
+  if (s == "rand-int") return Mode::RandInt;
+  if (s == "hpl") return Mode::Hpl;
+  if (s == "all-ones") return Mode::AllOnes;
+  die("unknown --input-mode " + s);
+}
+
+// The reference runner's index hash (runner.cpp:700-716).
+uint32_t index_hash(size_t index) {
+  uint64_t s = (uint64_t)index * 1664525ull + 1013904223ull;
+  for (int r = 0; r < 3; ++r)
+    s = s ^ (s << 13) ^ (s >> 17) ^ (s << 5);
+  return (uint32_t)s;
+}
+
+// `rows` x `k` values of operand `stream` (0 = A, 1 = B), 16-bit storage.
+std::vector<uint16_t> synth(size_t rows, size_t k, int dtype, uint64_t seed, int stream, Mode mode,
+                            float scale) {
+  const size_t n = rows * k;
   std::vector<uint16_t> out(n);
-  std::mt19937_64 rng(seed);
+  std::mt19937_64 rng(seed + (uint64_t)stream);
   std::uniform_real_distribution<float> uni(-1.f, 1.f);
   std::normal_distribution<float> nor(0.f, 1.f);
-  for (auto &v : out)
-    v = to_bits((normal ? nor(rng) : uni(rng)) * scale, dtype);
+  // Bucket LCG: seed ^ ((stream+1) * golden), values (bucket - 8) / 4.
+  uint32_t state = (uint32_t)seed ^ ((uint32_t)(stream + 1) * 0x9E3779B9u);
+  for (size_t i = 0; i < n; ++i) {
+    float v = 0.f;
+    switch (mode) {
+    case Mode::Uniform: v = uni(rng) * scale; break;
+    case Mode::Normal: v = nor(rng) * scale; break;
+    case Mode::Bucket:
+      state = 1664525u * state + 1013904223u;
+      v = (float)((int)((state >> 24) % 17u) - 8) * 0.25f;
+      break;
+    case Mode::RandInt: {
+      v = (float)(index_hash(i) % 5u) - 2.0f;
+      const size_t r = i / k, c = i % k;
+      if (stream == 1 && ((r ^ c) & 1u) == 0)
+        v = -v;
+      break;
+    }
+    case Mode::Hpl: v = (float)((double)index_hash(i) / (double)UINT32_MAX - 0.5); break;
+    case Mode::AllOnes: v = 1.f; break;
+    }
+    out[i] = to_bits(v, dtype);
+  }
   return out;
+}
+
+// Deterministic sample of `count` indices in [0, n), always including the
+// first and last.
+std::vector<size_t> sample_indices(size_t n, int count, uint64_t seed) {
+  std::vector<size_t> idx = {0, n - 1};
+  std::mt19937_64 rng(seed * 7919u + 13u);
+  std::uniform_int_distribution<size_t> d(0, n - 1);
+  for (int i = 0; i < count; ++i)
+    idx.push_back(d(rng));
+  return idx;
 }
 
 void *upload(const std::vector<uint16_t> &h) {
@@ -143,6 +219,13 @@ template <typename F> double median_us(F launch, int iters, int warmup, int repe
   return us[us.size() / 2];
 }
 
+double clock_mhz() {
+  double tf = 0, mhz = 0;
+  int cus = 0;
+  check_wave(wave_device_mfma_peak(0, &tf, &mhz, &cus), "device");
+  return mhz;
+}
+
 void print_device() {
   double tf = 0, mhz = 0;
   int cus = 0;
@@ -167,10 +250,16 @@ int run_gemm(Opts &o) {
   const uint64_t seed = (uint64_t)o.num("--seed", 7);
   if (M <= 0 || N <= 0 || K <= 0 || iters <= 0 || warmup < 0 || repeats <= 0)
     die("invalid non-positive argument");
-  const bool normal = o.str("--input-mode", "uniform") == "normal";
-  const float scale = normal ? 1.0f / std::sqrt((float)K) : 1.0f;
-  void *A = upload(synth((size_t)M * K, in, seed, normal, scale));
-  void *B = upload(synth((size_t)N * K, in, seed + 1, normal, scale));
+  std::string mode_name = o.str("--input-mode", "uniform");
+  if (o.flag("--rand-int")) mode_name = "rand-int";
+  if (o.flag("--hpl")) mode_name = "hpl";
+  if (o.flag("--all-ones")) mode_name = "all-ones";
+  const Mode mode = mode_of(mode_name);
+  const float scale = mode == Mode::Normal ? 1.0f / std::sqrt((float)K) : 1.0f;
+  const std::vector<uint16_t> hA = synth(M, K, in, seed, 0, mode, scale);
+  const std::vector<uint16_t> hB = synth(N, K, in, seed, 1, mode, scale);
+  void *A = upload(hA);
+  void *B = upload(hB);
   void *C = nullptr;
   check_hip(hipMalloc(&C, (size_t)M * N * (out == WAVE_F32 ? 4 : 2)), "hipMalloc C");
   float *scratch = nullptr;
@@ -198,9 +287,58 @@ int run_gemm(Opts &o) {
               o.str("--input-type", "f16").c_str(), o.str("--c-type", "f16").c_str(), lay.c_str());
   if (workers > 0)
     std::printf("streamk_workers: %d\n", workers);
+  std::printf("input_mode: %s\n", mode_name.c_str());
   std::printf("iters: %d repeats: %d\n", iters, repeats);
   std::printf("per_launch_us: %.3f\n", us);
+  std::printf("median_per_launch_us: %.3f\n", us);
+  std::printf("  hw_cycles_wallclock: %.0f\n", us * clock_mhz());
   std::printf("tflops: %.3f\n", 2.0 * M * N * (double)K / us * 1e-6);
+  if (o.flag("--check")) {
+    // C from the last launch; sampled elements against an fp32 host dot
+    // product rounded like the output (runner.cpp:738-745, :925-955).
+    const size_t ob = out == WAVE_F32 ? 4 : 2;
+    std::vector<uint8_t> hC((size_t)M * N * ob);
+    check_hip(hipMemcpy(hC.data(), C, hC.size(), hipMemcpyDeviceToHost), "hipMemcpy C");
+    double worst = 0.0;
+    size_t worst_idx = 0;
+    for (size_t idx : sample_indices((size_t)M * N, 512, seed)) {
+      const int m = layout == WAVE_ROW_MAJOR ? (int)(idx / N) : (int)(idx % M);
+      const int n = layout == WAVE_ROW_MAJOR ? (int)(idx % N) : (int)(idx / M);
+      float acc = 0.f;
+      for (int kk = 0; kk < K; ++kk)
+        acc += from_bits(hA[(size_t)m * K + kk], in) * from_bits(hB[(size_t)n * K + kk], in);
+      double exp = acc, got;
+      if (out == WAVE_F32) {
+        float g;
+        std::memcpy(&g, &hC[idx * 4], 4);
+        got = g;
+      } else {
+        uint16_t g;
+        std::memcpy(&g, &hC[idx * 2], 2);
+        got = from_bits(g, out);
+        exp = from_bits(to_bits(acc, out), out);
+      }
+      const double diff = std::fabs(got - exp);
+      if (diff > worst) {
+        worst = diff;
+        worst_idx = idx;
+      }
+      // The runner's bound plus one unit in the last place of the output
+      // type: two valid fp32 summation orders can round a 16-bit output to
+      // neighbouring values (one bf16 ulp is 0.25 at |C| ~ 40).
+      const double ulp = out == WAVE_F32 ? 0.0
+                         : std::ldexp(std::fabs(exp) > 0 ? std::fabs(exp) : 1.0,
+                                      out == WAVE_BF16 ? -7 : -10);
+      if (!(diff <= 1.0e-2 + 1.0e-3 * std::fabs(exp) + ulp)) {
+        std::fprintf(stderr,
+                     "output_check: failed m=%d n=%d expected=%.6f got=%.6f abs_diff=%.6f\n", m,
+                     n, exp, got, diff);
+        return 1;
+      }
+    }
+    std::printf("output_check: passed mode=sampled elements=514 max_abs_diff=%.6f index=%zu\n",
+                worst, worst_idx);
+  }
   if (workers > 0) {
     int nz = wave_gemm_streamk_counters_check(counters, M, N, nullptr);
     if (nz != 0) {
@@ -229,9 +367,12 @@ int run_fa(Opts &o) {
   if (B <= 0 || H <= 0 || Hkv <= 0 || S <= 0 || iters <= 0 || repeats <= 0)
     die("invalid non-positive argument");
   const size_t nq = (size_t)B * H * S * D, nkv = (size_t)B * Hkv * S * D;
-  void *Q = upload(synth(nq, dt, seed, true, 1.f));
-  void *Kd = upload(synth(nkv, dt, seed + 1, true, 1.f));
-  void *V = upload(synth(nkv, dt, seed + 2, true, 1.f));
+  const std::vector<uint16_t> hQ = synth(nq / D, D, dt, seed, 0, Mode::Normal, 1.f);
+  const std::vector<uint16_t> hK = synth(nkv / D, D, dt, seed, 1, Mode::Normal, 1.f);
+  const std::vector<uint16_t> hV = synth(nkv / D, D, dt, seed, 2, Mode::Normal, 1.f);
+  void *Q = upload(hQ);
+  void *Kd = upload(hK);
+  void *V = upload(hV);
   void *O = nullptr;
   check_hip(hipMalloc(&O, nq * 2), "hipMalloc O");
   auto launch = [&]() {
@@ -247,7 +388,51 @@ int run_fa(Opts &o) {
   std::printf("shape: B=%d H=%d Hkv=%d N=%d D=%d dtype=%s causal=%d\n", B, H, Hkv, S, D,
               o.str("--dtype", "f16").c_str(), causal);
   std::printf("per_launch_us: %.3f\n", us);
+  std::printf("median_per_launch_us: %.3f\n", us);
+  std::printf("  hw_cycles_wallclock: %.0f\n", us * clock_mhz());
   std::printf("tflops: %.3f\n", flops / us * 1e-6);
+  if (o.flag("--check")) {
+    // The reference runner's sampled heads x rows (wave-fa-gfx950-runner.cpp
+    // :204-232), double-precision softmax, tolerance 3e-2 (:388).
+    std::vector<uint16_t> hO(nq);
+    check_hip(hipMemcpy(hO.data(), O, nq * 2, hipMemcpyDeviceToHost), "hipMemcpy O");
+    const int heads[3] = {0, (B * H) / 2, B * H - 1};
+    const int rows[7] = {0, 31, 32, 127, S / 2, S - 128, S - 1};
+    const double scale = 1.0 / std::sqrt((double)D);
+    double worst = 0.0;
+    for (int bh : heads)
+      for (int r : rows) {
+        if (r < 0 || r >= S)
+          continue;
+        const int b = bh / H, h = bh % H, hk = h / (H / Hkv);
+        const size_t qb = ((size_t)bh * S + r) * D, kb = ((size_t)(b * Hkv + hk) * S) * D;
+        const int kend = causal ? r + 1 : S;
+        std::vector<double> w(kend);
+        double mx = -1e300, sum = 0.0;
+        for (int j = 0; j < kend; ++j) {
+          double s = 0.0;
+          for (int d = 0; d < D; ++d)
+            s += (double)from_bits(hQ[qb + d], dt) * from_bits(hK[kb + (size_t)j * D + d], dt);
+          w[j] = s * scale;
+          mx = std::max(mx, w[j]);
+        }
+        for (int j = 0; j < kend; ++j)
+          sum += (w[j] = std::exp(w[j] - mx));
+        for (int d = 0; d < D; ++d) {
+          double acc = 0.0;
+          for (int j = 0; j < kend; ++j)
+            acc += w[j] * from_bits(hV[kb + (size_t)j * D + d], dt);
+          const double diff = std::fabs(acc / sum - from_bits(hO[qb + d], dt));
+          worst = std::max(worst, diff);
+          if (!(diff <= 3e-2)) {
+            std::fprintf(stderr, "output_check: failed head=%d row=%d d=%d abs_diff=%.6f\n", bh,
+                         r, d, diff);
+            return 1;
+          }
+        }
+      }
+    std::printf("output_check: passed max_abs_diff=%.8f\n", worst);
+  }
   (void)hipFree(Q);
   (void)hipFree(Kd);
   (void)hipFree(V);

@@ -13,6 +13,11 @@ multithreaded C++ GEMM timed on a bounded sample of output rows of the same
 workload on this host's cores.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-fa]
+                    [--no-ref-compare]
+
+Secondary lines also run the same kernels on the input mode and shape of the
+reference's own published figures (rand_int GEMM inputs; the B2 H64 S8192
+bf16 attention profile) next to those figures, for comparison.
 """
 
 from __future__ import annotations
@@ -126,6 +131,21 @@ def cpu_reference_path(M, N, K, budget_s):
                       f"computeExpectedElement, {dt:.1f} s excluding input generation"}
 
 
+def rand_int_operand(rows, k, stream, torch):
+    """The reference runner's rand_int inputs (hipBLASLt-style integers in
+    [-2, 2]; wave-matmul-calibrate-runner.cpp:700-706, sign flip of B on
+    even (row ^ col) :1176-1183), as an f16 tensor on the host."""
+    idx = np.arange(rows * k, dtype=np.uint64)
+    s = idx * np.uint64(1664525) + np.uint64(1013904223)
+    for _ in range(3):
+        s = s ^ (s << np.uint64(13)) ^ (s >> np.uint64(17)) ^ (s << np.uint64(5))
+    v = (s.astype(np.uint32) % np.uint32(5)).astype(np.float32) - 2.0
+    if stream == 1:
+        flip = ((idx // np.uint64(k)) ^ (idx % np.uint64(k))) & np.uint64(1) == 0
+        v[flip] = -v[flip]
+    return torch.from_numpy(v.reshape(rows, k)).to(torch.float16)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -134,6 +154,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fa", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--no-ref-compare", action="store_true",
+                    help="skip the runs on the reference's published input modes / shapes")
     ap.add_argument("--workload", choices=["all", "gemm", "fa", "copy"], default="all",
                     help="gemm / fa: run only that kernel (for profiler passes); copy: "
                          "a 1 GiB device copy used to calibrate rocprofv3 byte counters")
@@ -196,6 +218,45 @@ def main():
                           "value": round(fa_tf, 2), "unit": "TFLOP/s",
                           "ms_per_step": round(fa_ms, 4),
                           "frac_of_mfma_peak": round(fa_tf / MFMA_PEAK_TFLOPS, 4)})
+        del q, k, v, o
+
+    if args.workload == "all" and not args.no_ref_compare:
+        # The same kernels on the input mode / shape of the reference's own
+        # published figures: not the headline
+        # metric, which uses uniform inputs.
+        ra = rand_int_operand(M, K, 0, torch).to(dev)
+        rb = rand_int_operand(N, K, 1, torch).to(dev)
+        r_ms = time_launches(lambda: wave.gemm(ra, rb, out_dtype=torch.float16, out=c),
+                             max(10, args.steps // 2), 3, torch)
+        r_tf = flops / (r_ms * 1e-3) / 1e12
+        log(f"gemm f16 8192^3 rand_int inputs: {r_ms * 1e3:.1f} us/launch, {r_tf:.1f} TFLOP/s")
+        secondary.append({"workload": "gemm_f16_8192x8192x8192_rand_int_inputs",
+                          "value": round(r_tf, 2), "unit": "TFLOP/s",
+                          "ms_per_step": round(r_ms, 4),
+                          "frac_of_mfma_peak": round(r_tf / MFMA_PEAK_TFLOPS, 4),
+                          "reference_published": {
+                              "value": 1400.4, "unit": "TFLOP/s", "hardware": "MI350X",
+                              "kernel": "gfx950-f16-256x256-8wave, rand_int inputs",
+                              "source": "docs/PerfReferences/WaveGfx950F16Gemm4Wave.md:29-31"}})
+        del ra, rb
+        B, H, S, D = 2, 64, 8192, 128
+        gq = torch.Generator(device="cpu").manual_seed(12)
+        q = torch.randn((B, H, S, D), generator=gq).to(torch.bfloat16).to(dev)
+        k = torch.randn((B, H, S, D), generator=gq).to(torch.bfloat16).to(dev)
+        v = torch.randn((B, H, S, D), generator=gq).to(torch.bfloat16).to(dev)
+        o = torch.empty_like(q)
+        f_ms = time_launches(lambda: wave.flash_attention(q, k, v, out=o), 10, 2, torch)
+        f_tf = 4.0 * B * H * S * S * D / (f_ms * 1e-3) / 1e12
+        log(f"fa fwd bf16 B2 H64 S8192 D128: {f_ms * 1e3:.1f} us/launch, {f_tf:.1f} TFLOP/s")
+        secondary.append({"workload": "fa_fwd_bf16_b2_h64_s8192_d128_noncausal_online_softmax",
+                          "value": round(f_tf, 2), "unit": "TFLOP/s",
+                          "ms_per_step": round(f_ms, 4),
+                          "frac_of_mfma_peak": round(f_tf / MFMA_PEAK_TFLOPS, 4),
+                          "reference_published": {
+                              "value": 1111.1, "unit": "TFLOP/s", "hardware": "MI350X",
+                              "kernel": "flash_attention_bf16_gfx950 8-wave, fixed-max mode "
+                                        "(qk_max_abs=1, no online max)",
+                              "source": "docs/PerfReferences/WaveGfx950FlashAttention.md:5-21"}})
         del q, k, v, o
 
     cpu = None
