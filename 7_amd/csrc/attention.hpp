@@ -18,6 +18,7 @@ struct FwdArgs {
   int dtype = 1;            // wave::kF16 or wave::kBF16 (Q, K, V and O)
   int causal = 0;           // mask key > query (top-left aligned)
   float scale = 0.f;        // softmax scale; 0 selects 1/sqrt(head_dim)
+  float qk_max_abs = 0.f;   // > 0: |Q|, |K| <= qk_max_abs, fixed-max kernel
 };
 
 hipError_t launch_fwd(const FwdArgs &args, hipStream_t stream);

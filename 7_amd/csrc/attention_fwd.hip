@@ -22,12 +22,23 @@ hipError_t launch_fwd(const FwdArgs &a, hipStream_t stream) {
   p.causal = a.causal;
   const float scale = a.scale > 0.f ? a.scale : 1.0f / std::sqrt((float)a.head_dim);
   p.scale_log2 = scale * kLog2e;
+  // Fixed-max mode: |s * scale| <= head_dim * qk_max_abs^2 * scale, in log2
+  // units (wave_flash_attention.py:108-113 with scale = 1/sqrt(128)).
+  p.fixed_max = (float)((double)kLog2e * scale * a.head_dim * a.qk_max_abs * a.qk_max_abs);
   // 8 waves x 32 query rows per CTA, two ping-pong groups of 4 waves.
   const dim3 grid(p.q_blocks * a.batch * a.q_heads), block(64 * kPPWaves);
-  if (a.dtype == kF16)
-    hipLaunchKernelGGL((fwd_pp_kernel<kF16>), grid, block, 0, stream, p);
-  else
-    hipLaunchKernelGGL((fwd_pp_kernel<kBF16>), grid, block, 0, stream, p);
+  const bool fixed = a.qk_max_abs > 0.f;
+  if (a.dtype == kF16) {
+    if (fixed)
+      hipLaunchKernelGGL((fwd_pp_kernel<kF16, true>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((fwd_pp_kernel<kF16, false>), grid, block, 0, stream, p);
+  } else {
+    if (fixed)
+      hipLaunchKernelGGL((fwd_pp_kernel<kBF16, true>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((fwd_pp_kernel<kBF16, false>), grid, block, 0, stream, p);
+  }
   return hipGetLastError();
 }
 

@@ -63,6 +63,7 @@ struct Params {
   int q_blocks;   // ceil(seq_q / (32 * NW))
   int causal;
   float scale_log2;  // softmax scale * log2(e)
+  float fixed_max;   // fixed-max kernels: the row max of every row (log2 units)
 };
 
 // Linear CTA id -> (batch*head, query block).
@@ -148,8 +149,12 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
 constexpr int kPPSmem = kKRingPP * kKBytes + 2 * kVtBytes;
 
 // CTA `raw` of a grid of q_blocks * batch * q_heads CTAs of 512 threads.
-// smem: kPPSmem bytes of 1024-byte-aligned LDS.
-template <int DT>
+// smem: kPPSmem bytes of 1024-byte-aligned LDS.  FIXED: the caller bounds
+// |Q|, |K| so that every scaled score lies in [-fixed_max, fixed_max]; the
+// running max is then the constant fixed_max and the softmax segment skips
+// the row max and the rescale (the reference's qk_max_abs mode,
+// wave_flash_attention.py:63-75, :108-113, :586-622).
+template <int DT, bool FIXED = false>
 __device__ __forceinline__ void fwd_pp_cta(const Params &p, int raw, uint8_t *smem) {
   constexpr int kRows = 32 * kPPWaves;
   const uint32_t wave = uniform(threadIdx.x >> 6);
@@ -240,7 +245,7 @@ __device__ __forceinline__ void fwd_pp_cta(const Params &p, int raw, uint8_t *sm
   for (int i = 0; i < 4; ++i)
     o[i] = f32x16{};
   float lsum = 0.f;
-  float m = -__builtin_inff();
+  float m = FIXED ? p.fixed_max : -__builtin_inff();
   const float c = p.scale_log2;
   // pin(x): x must be computed before this point (keeps each segment's work
   // on its side of the barrier that follows).
@@ -346,13 +351,15 @@ __device__ __forceinline__ void fwd_pp_cta(const Params &p, int raw, uint8_t *sm
   // Softmax of tile t (scores in sc): max, rescale, P(t) -> pf, row sums.
   auto softmax = [&](f32x16 (&sc)[2], int t) {
     mask(sc, t);
-    float mx = sc[0][0];
+    if constexpr (!FIXED) {
+      float mx = sc[0][0];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        mx = fmaxf(mx, sc[j][r]);
-    update_max(fmaxf(mx, __shfl_xor(mx, 32)) * c);
+        for (int r = 0; r < 16; ++r)
+          mx = fmaxf(mx, sc[j][r]);
+      update_max(fmaxf(mx, __shfl_xor(mx, 32)) * c);
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -486,10 +493,10 @@ __device__ __forceinline__ void fwd_pp_cta(const Params &p, int raw, uint8_t *sm
   }
 }
 
-template <int DT>
+template <int DT, bool FIXED>
 __global__ __launch_bounds__(512, 1) void fwd_pp_kernel(Params p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kPPSmem];
-  fwd_pp_cta<DT>(p, blockIdx.x, smem);
+  fwd_pp_cta<DT, FIXED>(p, blockIdx.x, smem);
 }
 
 } // namespace attention

@@ -19,6 +19,7 @@
 //                               bf16* O)
 //     (wave_flash_attention.py:1723-1728; runner wave-fa-gfx950-runner.cpp
 //     :396-402).  -DWAVE_ABI_FA -DWAVE_ABI_FA_B= -DWAVE_ABI_FA_H= -DWAVE_ABI_FA_S=
+//     [-DWAVE_ABI_FA_QK_MAX_ABS=b: the fixed-max profile for |Q|, |K| <= b]
 //   flash_attention_f32(const f16* Q, const f16* K, const f16* V, f32* O)
 //     (wave_attention.py:1436-1441; runner wave-fa-calibrate-runner.cpp
 //     :346-361).  -DWAVE_ABI_FA32 -DWAVE_ABI_FA32_M= _N= _D=
@@ -173,7 +174,17 @@ extern "C" __global__ __launch_bounds__(512, 1) void flash_attention_bf16_gfx950
   p.causal = runtime_int(0);
   // 1/sqrt(128) * log2(e), in the same float operations as the host path.
   p.scale_log2 = (1.0f / 11.313708498984761f) * kLog2e;
+#ifdef WAVE_ABI_FA_QK_MAX_ABS
+  // The reference's qk_max_abs profile (wave_flash_attention.py:108-113):
+  // fixed row max log2(e) * sqrt(128) * qk_max_abs^2, no online max.
+  constexpr double kB = WAVE_ABI_FA_QK_MAX_ABS;
+  static_assert(kB > 0 && -2.0 * 1.4426950408889634 * 11.313708498984761 * kB * kB >= -126.0,
+                "qk_max_abs outside the bf16 range");
+  p.fixed_max = (float)(1.4426950408889634 * (1.0 / 11.313708498984761) * 128.0 * kB * kB);
+  fwd_pp_cta<kBF16, true>(p, blockIdx.y * gridDim.x + blockIdx.x, dsmem);
+#else
   fwd_pp_cta<kBF16>(p, blockIdx.y * gridDim.x + blockIdx.x, dsmem);
+#endif
 }
 #endif
 

@@ -32,6 +32,8 @@ _SIGNATURES = {
     "wave_gemm_streamk_workspace_reset": (_I, [_P, _I, _I, _P]),
     "wave_gemm_streamk_counters_check": (_I, [_P, _I, _I, _P]),
     "wave_fa_fwd_launch": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P]),
+    "wave_fa_fwd_bounded_launch": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _F,
+                                        _P]),
     "wave_fa_f32_launch": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     "wave_status_string": (ctypes.c_char_p, [_I]),
     "wave_last_error": (ctypes.c_char_p, []),

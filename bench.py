@@ -255,7 +255,25 @@ def main():
                           "reference_published": {
                               "value": 1111.1, "unit": "TFLOP/s", "hardware": "MI350X",
                               "kernel": "flash_attention_bf16_gfx950 8-wave, fixed-max mode "
-                                        "(qk_max_abs=1, no online max)",
+                                        "(qk_max_abs=1, no online max; this line runs the "
+                                        "online-softmax kernel)",
+                              "source": "docs/PerfReferences/WaveGfx950FlashAttention.md:5-21"}})
+        # The reference's fixed-max profile itself: |Q|, |K| <= 1 declared
+        # (qk_max_abs=1), Q and K uniform in [-1, 1).
+        q = (torch.rand((B, H, S, D), generator=gq) * 2 - 1).to(torch.bfloat16).to(dev)
+        k = (torch.rand((B, H, S, D), generator=gq) * 2 - 1).to(torch.bfloat16).to(dev)
+        x_ms = time_launches(lambda: wave.flash_attention(q, k, v, qk_max_abs=1.0, out=o), 10, 2,
+                             torch)
+        x_tf = 4.0 * B * H * S * S * D / (x_ms * 1e-3) / 1e12
+        log(f"fa fwd bf16 B2 H64 S8192 D128 fixed max (qk_max_abs=1): {x_ms * 1e3:.1f} us/launch, "
+            f"{x_tf:.1f} TFLOP/s")
+        secondary.append({"workload": "fa_fwd_bf16_b2_h64_s8192_d128_noncausal_qk_max_abs_1",
+                          "value": round(x_tf, 2), "unit": "TFLOP/s",
+                          "ms_per_step": round(x_ms, 4),
+                          "frac_of_mfma_peak": round(x_tf / MFMA_PEAK_TFLOPS, 4),
+                          "reference_published": {
+                              "value": 1111.1, "unit": "TFLOP/s", "hardware": "MI350X",
+                              "kernel": "flash_attention_bf16_gfx950 8-wave, qk_max_abs=1",
                               "source": "docs/PerfReferences/WaveGfx950FlashAttention.md:5-21"}})
         del q, k, v, o
 

@@ -108,6 +108,20 @@ int wave_fa_fwd_launch(const void *Q, const void *K, const void *V, void *O,
                        int head_dim, int dtype, int causal, float scale,
                        void *stream);
 
+/* Fixed-max variant: the caller guarantees |Q|, |K| <= qk_max_abs, so every
+ * scaled score lies within bound = log2(e) * scale * head_dim *
+ * qk_max_abs^2 (log2 units) and the kernel uses that bound as the row max of
+ * every row: no online max, no rescale.  Replaces the reference's
+ * `qk_max_abs` mode of `flash_attention_bf16_gfx950`
+ * (wave_flash_attention.py:63-75 validation, :108-113 bound, :586-622
+ * softmax).  Returns WAVE_ERR_INVALID when qk_max_abs is not finite and
+ * positive or when 2^(-2 * bound) is below the smallest normal of dtype
+ * (2^-126 for bf16, 2^-14 for f16), as the reference rejects it. */
+int wave_fa_fwd_bounded_launch(const void *Q, const void *K, const void *V, void *O,
+                               int batch, int q_heads, int kv_heads, int seq,
+                               int head_dim, int dtype, int causal, float scale,
+                               float qk_max_abs, void *stream);
+
 /* ---- flash_attention_f32 ------------------------------------------------
  * Replaces `flash_attention_f32(Q, K, V, O)` (wave_attention.py:1406-1441;
  * wave-fa-calibrate-runner.cpp:346-361): Q [block_m][head_dim] f16

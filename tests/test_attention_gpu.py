@@ -130,3 +130,44 @@ def test_flash_attention_f32_abi(wave, oracle, dev, bm, sn, hd, seed):
                                  to_dev(v, torch.float16, dev))
     ref = oracle.fa_f32_reference(q, k, v)
     assert float(np.abs(o.cpu().numpy() - ref).max()) <= 3e-3
+
+
+def uniform_bits(n, dt, seed, bound):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    t = ((torch.rand(n, generator=g) * 2 - 1) * bound).to(TDT[dt])
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("dt,bound", [(2, 1.0), (1, 0.5)])
+@pytest.mark.parametrize("B,Hq,Hkv,S,causal", [(1, 2, 2, 512, False), (2, 4, 2, 300, True),
+                                               (1, 1, 1, 64, False)])
+def test_fixed_max_mode(wave, oracle, dev, dt, bound, B, Hq, Hkv, S, causal):
+    """qk_max_abs mode (wave_flash_attention.py:63-75, :108-113): inputs
+    within the declared bound, every row against the double-precision
+    softmax at 2e-2."""
+    D = 128
+    q = uniform_bits(B * Hq * S * D, dt, 21, bound)
+    k = uniform_bits(B * Hkv * S * D, dt, 22, bound)
+    v = normal_bits(B * Hkv * S * D, dt, 23)
+    qt = to_dev(q, TDT[dt], dev).view(B, Hq, S, D)
+    kt = to_dev(k, TDT[dt], dev).view(B, Hkv, S, D)
+    vt = to_dev(v, TDT[dt], dev).view(B, Hkv, S, D)
+    o = wave.flash_attention(qt, kt, vt, causal=causal, qk_max_abs=bound)
+    torch.cuda.synchronize()
+    got = oracle.bits_to_f32(to_bits(o).reshape(B * Hq, S, D), dt)
+    hh, rr = np.meshgrid(np.arange(B * Hq), np.arange(S), indexing="ij")
+    ref = oracle.attention_rows(q, k, v, dtype=dt, batch=B, q_heads=Hq, kv_heads=Hkv,
+                                seq_q=S, seq_k=S, head_dim=D, causal=causal,
+                                scale=1.0 / math.sqrt(D), heads=hh.ravel(), rows=rr.ravel())
+    assert float(np.abs(got[hh.ravel(), rr.ravel()] - ref).max()) <= TOL
+
+
+def test_fixed_max_reference_inputs(wave, oracle, dev):
+    """The reference runner's bf16 inputs (|Q|, |K| <= 0.25) under its
+    qk_max_abs=1 profile agree with the adaptive kernel within 2e-2."""
+    S = 512
+    q, k, v = oracle.fa_gfx950_inputs(S * 128, 5, 1)
+    qt, kt, vt = (to_dev(x, torch.bfloat16, dev).view(1, 1, S, 128) for x in (q, k, v))
+    fixed = wave.flash_attention(qt, kt, vt, qk_max_abs=1.0).float()
+    adaptive = wave.flash_attention(qt, kt, vt).float()
+    assert float((fixed - adaptive).abs().max()) <= TOL

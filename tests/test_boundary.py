@@ -111,6 +111,18 @@ def test_fa_rejects_bad_arguments(wave, kw, status):
     assert _fa(L, **kw) == status
 
 
+@pytest.mark.parametrize("dtype,bound", [(2, 0.0), (2, -1.0), (2, float("inf")),
+                                         (2, float("nan")), (2, 2.0), (1, 1.0)])
+def test_fa_bounded_rejects_bad_bound(wave, dtype, bound):
+    """wave_flash_attention.py:63-75: qk_max_abs finite and positive, and
+    2^(-2 * bound) a normal number of the P type (bf16: b <= 1.96;
+    f16: b <= 0.65 at D = 128)."""
+    L = wave.runtime.lib()
+    assert L.wave_fa_fwd_bounded_launch(16, 32, 48, 64, 1, 1, 1, 256, 128, dtype, 0, 0.0,
+                                        bound, None) == -1
+    assert "qk_max_abs" in wave.runtime.lib().wave_last_error().decode()
+
+
 def test_fa_f32_rejects_bad_arguments(wave):
     L = wave.runtime.lib()
     assert L.wave_fa_f32_launch(None, 32, 48, 64, 16, 16, 32, None) == -1

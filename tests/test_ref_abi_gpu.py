@@ -201,3 +201,18 @@ def test_fa_f32_runner_launch(co, oracle, dev, threads):
         mod.kernel("flash_attention_f32").launch((1,), (threads,), [Q, Kt, V, O])
         torch.cuda.synchronize()
     assert float(np.abs(O.cpu().numpy() - oracle.fa_f32_reference(q, k, v)).max()) <= 3e-3
+
+
+def test_fa_bf16_fixed_max_code_object(co, wave, oracle, dev):
+    """The reference's qk_max_abs=1 profile as a code object
+    (-DWAVE_ABI_FA_QK_MAX_ABS=1.0): bit-identical to
+    wave_fa_fwd_bounded_launch with the same bound."""
+    Bt, H, S, D = 1, 2, 512, 128
+    q, k, v = oracle.fa_gfx950_inputs(Bt * H * S * D, 6, 1)
+    Q, Kt, V = (to_dev(x, torch.bfloat16, dev).view(Bt, H, S, D) for x in (q, k, v))
+    O = torch.zeros_like(Q)
+    with co.CodeObject("fa_bf16_b1_h2_s512_qk1") as mod:
+        mod.kernel("flash_attention_bf16_gfx950").launch(
+            (S // 256, Bt * H), (512,), [Q, Kt, V, O], dynamic_lds=FA_LDS)
+        torch.cuda.synchronize()
+    assert torch.equal(O, wave.flash_attention(Q, Kt, V, qk_max_abs=1.0))
