@@ -1,5 +1,5 @@
 """wave-mi355x: MI355X-native (gfx950) drop-in for the reference's GEMM,
-Stream-K GEMM and flash-attention forward kernels.
+Stream-K GEMM, MXFP4 scaled GEMM and flash-attention forward kernels.
 
 The package directory name starts with a digit, so import it with
 ``importlib.import_module("7_amd")``.  The compute lives in
@@ -11,10 +11,10 @@ the reference's kernel symbols, one shape each) with hipModuleLoad.
 
 from . import code_object, runtime
 from .ops import (StreamKWorkspace, flash_attention, flash_attention_f32, gemm,
-                  gemm_streamk, streamk_workspace_bytes)
+                  gemm_mxfp4, gemm_streamk, streamk_workspace_bytes)
 from .runtime import WaveError
 
 __all__ = [
-    "runtime", "code_object", "gemm", "gemm_streamk", "StreamKWorkspace", "streamk_workspace_bytes",
+    "runtime", "code_object", "gemm", "gemm_mxfp4", "gemm_streamk", "StreamKWorkspace", "streamk_workspace_bytes",
     "flash_attention", "flash_attention_f32", "WaveError",
 ]

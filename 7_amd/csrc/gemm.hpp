@@ -20,6 +20,10 @@ struct GemmArgs {
   void *counters = nullptr; // Stream-K per-tile arrival counters (zeroed)
   int workers = 0;          // > 0 selects the Stream-K kernel
   bool force_masked = false;
+  // MXFP4 (in_dtype kMXFP4): A [M][K/2], B [N][K/2] packed fp4; e8m0 scales
+  // group-major [K/32][M] and [K/32][N].
+  const void *a_scale = nullptr;
+  const void *b_scale = nullptr;
 };
 
 constexpr int kTileEdge = 256;
@@ -28,6 +32,8 @@ constexpr int kKStage = 64;
 int tiles_for(int extent);
 int k_iterations(int K);
 hipError_t launch(const GemmArgs &args, hipStream_t stream);
+// MXFP4 scaled GEMM (gemm_mxfp4.hip): M, N % 256 == 0, K % 128 == 0.
+hipError_t launch_mxfp4(const GemmArgs &args, hipStream_t stream);
 // Short-M kernel (gemm_skinny.hip): M <= 128, K % 64 == 0, aligned.
 bool skinny_supported(const GemmArgs &args);
 hipError_t launch_skinny(const GemmArgs &args, hipStream_t stream);

@@ -33,6 +33,8 @@
 #include "gemm.hpp"
 #include "wave_common.hpp"
 
+#include <type_traits>
+
 #ifndef WAVE_GEMM_BK
 #define WAVE_GEMM_BK 32
 #endif
@@ -53,8 +55,10 @@ constexpr int kSKUnit = 64;  // Stream-K work unit: 64 K elements of one tile
 // LDS ring geometry for BK elements of K per stage and NSTAGE stages, and
 // the wave grid: WAVES waves, WPN along P (the MFMA row / C-contiguous
 // dimension) x WQN along Q, each owning TP x TQ MFMA 32x32 tiles.
-template <int BK_, int NSTAGE_, int WAVES_> struct Cfg {
+// SCALE_: bytes per stage of MXFP4 e8m0 scales after the A and B tiles.
+template <int BK_, int NSTAGE_, int WAVES_, int SCALE_ = 0> struct Cfg {
   static constexpr int BK = BK_;
+  static constexpr int SCALE = SCALE_;
   static constexpr int NSTAGE = NSTAGE_;
   static constexpr int WAVES = WAVES_;
   static constexpr int THREADS = 64 * WAVES;
@@ -65,13 +69,18 @@ template <int BK_, int NSTAGE_, int WAVES_> struct Cfg {
   static constexpr int CPR = BK / 8;             // 16-byte chunks per row
   static constexpr int KS = BK / 16;             // MFMA K slices per stage
   static constexpr int OPB = kTile * RB;         // bytes per operand tile
-  static constexpr int STAGE = 2 * OPB;          // A + B
+  static constexpr int STAGE = 2 * OPB + SCALE;  // A + B (+ scales)
   static constexpr int SMEM = NSTAGE * STAGE;
   static constexpr int DMA = OPB / 1024 / WAVES; // DMA issues per wave per operand
   static_assert(OPB == 128 * 128 * (BK / 32), "super-row layout covers BK 32/64");
   static_assert(SMEM <= 160 * 1024, "LDS ring exceeds 160 KiB");
 };
 using DefaultCfg = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE, WAVE_GEMM_WAVES>;
+// MXFP4: the same ring with K counted in 16-bit units (one 64-byte row
+// chunk = 128 fp4 values per stage, one MFMA 32x32x64 per 32-byte slice)
+// and 2 KiB of scales per stage: four 32-value groups x (256 A + 256 B)
+// rows, laid out [group][A rows | B rows].
+using Fp4Cfg = Cfg<32, 4, 4, 4 * 512>;
 
 // LDS geometry of an operand tile.  The tile is stored as 128-byte
 // "super-rows" of eight 16-byte slots: with BK = 64 super-row R is tile row
@@ -108,7 +117,9 @@ struct Params {
   const uint16_t *A;
   const uint16_t *B;
   void *C;
-  int M, N, K;
+  int M, N, K;    // MXFP4: K counted in 16-bit units (fp4 K / 4)
+  // MXFP4 only: e8m0 scales, group-major [K/32][M] and [K/32][N]
+  const uint8_t *a_scale, *b_scale;
   int tiles_m, tiles_n;
   int group_m;
   int ldc;        // N for row-major C, M for column-major C
@@ -201,9 +212,23 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
     qswz[t] = swz8(qR) ^ Geo<C>::slot_base(qr) ^ (lane >> 5);
   }
 
-  // Fragments of one 16-wide K slice: TP P tiles + TQ Q tiles, 16 bytes each.
+  // MXFP4: offsets of this lane's P / Q tile rows in a stage's scale area
+  // ([group][A rows | B rows], 512 bytes per 32-value group).
+  uint32_t psc[TP], qsc[TQ];
+  if constexpr (IN_DT == kMXFP4) {
+#pragma unroll
+    for (int t = 0; t < TP; ++t)
+      psc[t] = 2 * C::OPB + (COL_MAJOR ? 0u : 256u) + wp * (TP * 32) + t * 32 + (lane & 31);
+#pragma unroll
+    for (int t = 0; t < TQ; ++t)
+      qsc[t] = 2 * C::OPB + (COL_MAJOR ? 256u : 0u) + wq * (TQ * 32) + t * 32 + (lane & 31);
+  }
+
+  // Fragments of one 16-wide K slice: TP P tiles + TQ Q tiles, 16 bytes each
+  // (MXFP4: 64 fp4 values per slice, plus each lane's e8m0 scale byte).
   struct Frag {
     u32x4 p[TP], q[TQ];
+    uint32_t sp[TP], sq[TQ];
   };
   // Fragment j of a slice: j < TQ -> Q tile j, else P tile j - TQ.
   auto read_one = [&](Frag &f, uint32_t stage, int kk, int j) {
@@ -214,6 +239,14 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
     else
       f.p[j - TQ] = *reinterpret_cast<const u32x4 *>(s + poff[j - TQ] +
                                                      ((x ^ pswz[j - TQ]) << 4));
+    if constexpr (IN_DT == kMXFP4) {
+      // Lane half h holds the slice's 32-value group 2*kk + h.
+      const uint8_t *sg = s + (x + (lane >> 5)) * 512u;
+      if (j < TQ)
+        f.sq[j] = sg[qsc[j]];
+      else
+        f.sp[j - TQ] = sg[psc[j - TQ]];
+    }
   };
   auto read_frags = [&](Frag &f, uint32_t stage, int kk) {
 #pragma unroll
@@ -236,8 +269,13 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
           read_one(nxt, nstage, nkk, j);
       }
 #pragma unroll
-      for (int tq = 0; tq < TQ; ++tq)
-        acc[tp][tq] = mfma32x32x16<IN_DT>(cur.p[tp], cur.q[tq], acc[tp][tq]);
+      for (int tq = 0; tq < TQ; ++tq) {
+        if constexpr (IN_DT == kMXFP4)
+          acc[tp][tq] = mfma_fp4_32x32x64(cur.p[tp], cur.q[tq], acc[tp][tq], cur.sp[tp],
+                                          cur.sq[tq]);
+        else
+          acc[tp][tq] = mfma32x32x16<IN_DT>(cur.p[tp], cur.q[tq], acc[tp][tq]);
+      }
       hook(tp);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -275,18 +313,35 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
     const char *b_tile =
         reinterpret_cast<const char *>(p.B) + (size_t)n0 * rowbytes;
     const uint32_t lds0 = lds_addr(smem) + wave * C::DMA * 1024;
-    // DMA d of one stage (0 <= d < 2*DMA): A chunks first, then B.
+    // MXFP4 scales: wave w copies group 4*kt + w of the A scales (lanes
+    // 0-15, 256 rows) and of the B scales (lanes 16-31) into its 512 bytes
+    // of the stage's scale area.
+    const uint32_t lds_sc = lds_addr(smem) + 2 * C::OPB + wave * 512;
+    const uint32_t a_sc = wave * (uint32_t)p.M + m0 + (lane & 15) * 16;
+    const uint32_t b_sc = wave * (uint32_t)p.N + n0 + (lane & 15) * 16;
+    // DMA d of one stage (0 <= d < 2*DMA): A chunks first, then B; MXFP4
+    // adds d = 2*DMA (A scales) and 2*DMA + 1 (B scales).
     auto issue_one = [&](uint32_t stage, int kt, int d) {
       const uint32_t l = lds0 + stage * C::STAGE;
-      if (d < C::DMA)
+      if (d < C::DMA) {
         dma16(l + d * 1024, a_tile + (size_t)kt * C::RB, goff[d]);
-      else
+      } else if (d < 2 * C::DMA) {
         dma16(l + C::OPB + (d - C::DMA) * 1024, b_tile + (size_t)kt * C::RB,
               goff[d - C::DMA]);
+      } else if constexpr (IN_DT == kMXFP4) {
+        const uint32_t g0 = (uint32_t)kt * 4u;
+        if (d == 2 * C::DMA) {
+          if (lane < 16)
+            dma16(lds_sc + stage * C::STAGE, p.a_scale, a_sc + g0 * (uint32_t)p.M);
+        } else if (lane - 16u < 16u) {
+          dma16(lds_sc + stage * C::STAGE, p.b_scale, b_sc + g0 * (uint32_t)p.N);
+        }
+      }
     };
+    constexpr int kDmaPerStage = 2 * C::DMA + (IN_DT == kMXFP4 ? 2 : 0);
     auto issue = [&](uint32_t stage, int kt) {
 #pragma unroll
-      for (int d = 0; d < 2 * C::DMA; ++d)
+      for (int d = 0; d < kDmaPerStage; ++d)
         issue_one(stage, kt, d);
     };
     // Steady-state DMA schedule: the D2 issues of the prefetched stage are
@@ -295,7 +350,7 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
     // group d*G/D2.  At the barrier of iteration i stage i+1 must be
     // complete; issued after it are stages i+2 .. i+NSTAGE-2 and the P
     // pre-barrier issues of stage i+NSTAGE-1, hence vmcnt(D2*(NSTAGE-3)+P).
-    constexpr int D2 = 2 * C::DMA;
+    constexpr int D2 = kDmaPerStage;
     constexpr int G1 = (C::KS - 1) * 4;
     constexpr int G2 = C::NSTAGE >= 3 ? 4 : 0;
     constexpr int G = G1 + G2;
@@ -448,9 +503,13 @@ __device__ __forceinline__ void store_tile(const Params &p, int m0, int n0,
 
 // One 256x256 output tile: CTA `raw` of a grid of tiles_m * tiles_n CTAs.
 // smem: DefaultCfg::SMEM bytes of 1024-byte-aligned LDS.
+template <int IN_DT>
+using CfgFor = std::conditional_t<IN_DT == kMXFP4, Fp4Cfg, DefaultCfg>;
+
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
 __device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *smem) {
-  using C = DefaultCfg;
+  using C = CfgFor<IN_DT>;
+  static_assert(IN_DT != kMXFP4 || !MASKED, "MXFP4 takes whole tiles only");
   int tm, tn;
   tile_coords(raw, p.tiles_m, p.tiles_n, p.group_m, true, tm, tn);
   const int m0 = tm * kTile, n0 = tn * kTile;
@@ -470,7 +529,7 @@ __device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *sme
 
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
 __global__ __launch_bounds__(DefaultCfg::THREADS, 1) void tiled_kernel(Params p) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[DefaultCfg::SMEM];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[CfgFor<IN_DT>::SMEM];
   tiled_cta<IN_DT, OUT_DT, COL_MAJOR, MASKED, VEC>(p, blockIdx.x, smem);
 }
 

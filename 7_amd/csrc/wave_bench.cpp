@@ -6,7 +6,7 @@
 // back-to-back launches between two hipEvents (median over `repeats`), and
 // print the runners' `key: value` lines (per_launch_us, tflops, ...).
 //
-//   wave-bench gemm [--m M] [--n N] [--k K] [--input-type f16|bf16]
+//   wave-bench gemm [--m M] [--n N] [--k K] [--input-type f16|bf16|mxfp4]
 //                   [--c-type f32|f16|bf16] [--output-layout row-major|column-major]
 //                   [--streamk-workers W] [--iters N] [--warmup N] [--repeats R]
 //                   [--seed S] [--input-mode uniform|normal|bucket|rand-int|hpl|all-ones]
@@ -19,6 +19,10 @@
 // (config 3) from a seeded std::mt19937_64; bucket, rand-int, hpl and
 // all-ones restate the reference runner's generators (runner.cpp:681-716,
 // :1143-1186), e.g. for comparison with its rand_int profile numbers.
+// MXFP4 (--input-type mxfp4) takes the runner's random e2m1 codes and e8m0
+// scales 124..127 (runner.cpp:1135-1150, :1208-1220) or, with --all-ones,
+// codes 0x22 and scales 0x7f; rand-int and hpl are refused as the runner
+// refuses them (runner.cpp:599-600).
 // --check samples outputs against a host fp32 (GEMM) or double (FA)
 // reference with the runner's tolerances (1e-2 + 1e-3*|expected|,
 // runner.cpp:942, plus one ulp of a 16-bit output; 3e-2 for FA,
@@ -236,8 +240,139 @@ void print_device() {
               p.gcnArchName, cus, mhz, tf);
 }
 
+// The runner's LCG (runner.cpp:681-689).
+uint32_t lcg_state(uint64_t seed, int stream) {
+  return (uint32_t)seed ^ ((uint32_t)(stream + 1) * 0x9E3779B9u);
+}
+uint32_t lcg_next(uint32_t &s) { return s = 1664525u * s + 1013904223u; }
+
+float fp4_value(unsigned code) {
+  static const float mag[8] = {0.f, 0.5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f};
+  return (code & 8u) ? -mag[code & 7u] : mag[code & 7u];
+}
+
+int run_gemm_mxfp4(Opts &o, int M, int N, int K, int out, int layout, const std::string &lay,
+                   int iters, int warmup, int repeats, uint64_t seed) {
+  std::string mode_name = o.str("--input-mode", "uniform");
+  if (o.flag("--rand-int")) mode_name = "rand-int";
+  if (o.flag("--hpl")) mode_name = "hpl";
+  if (o.flag("--all-ones")) mode_name = "all-ones";
+  if (mode_name == "rand-int" || mode_name == "hpl")
+    die("--rand-int and --hpl are dense-input modes; MXFP4 takes random or all-ones");
+  const bool ones = mode_name == "all-ones";
+  if (K % 32)
+    die("MXFP4 K must be a multiple of 32");
+  auto codes = [&](size_t rows, int stream) {
+    std::vector<uint8_t> v(rows * (size_t)K / 2, 0x22);
+    uint32_t st = lcg_state(seed, stream);
+    if (!ones)
+      for (auto &b : v) {
+        const unsigned lo = (lcg_next(st) >> 28) & 0xfu, hi = (lcg_next(st) >> 28) & 0xfu;
+        b = (uint8_t)(lo | (hi << 4));
+      }
+    return v;
+  };
+  auto scales = [&](size_t rows, int stream) {
+    std::vector<uint8_t> v(rows * (size_t)(K / 32), 0x7f);
+    uint32_t st = lcg_state(seed, stream);
+    if (!ones)
+      for (auto &b : v)
+        b = (uint8_t)(124u + ((lcg_next(st) >> 29) & 3u));
+    return v;
+  };
+  const std::vector<uint8_t> hA = codes(M, 0), hB = codes(N, 1);
+  const std::vector<uint8_t> hSA = scales(M, 2), hSB = scales(N, 3);
+  auto up8 = [](const std::vector<uint8_t> &h) {
+    void *d = nullptr;
+    check_hip(hipMalloc(&d, h.size()), "hipMalloc");
+    check_hip(hipMemcpy(d, h.data(), h.size(), hipMemcpyHostToDevice), "hipMemcpy");
+    return d;
+  };
+  void *A = up8(hA), *B = up8(hB), *SA = up8(hSA), *SB = up8(hSB);
+  void *C = nullptr;
+  check_hip(hipMalloc(&C, (size_t)M * N * (out == WAVE_F32 ? 4 : 2)), "hipMalloc C");
+  auto launch = [&]() {
+    check_wave(wave_gemm_mxfp4_launch(A, B, C, SA, SB, M, N, K, out, layout, nullptr),
+               "wave_gemm_mxfp4_launch");
+  };
+  const double us = median_us(launch, iters, warmup, repeats);
+  print_device();
+  std::printf("kernel: wmma_f16_matmul_tiled\n");
+  std::printf("shape: m=%d n=%d k=%d input_type=mxfp4 c_type=%s output_layout=%s\n", M, N, K,
+              o.str("--c-type", "f16").c_str(), lay.c_str());
+  std::printf("mxfp4_input_layout: canonical\n");
+  std::printf("input_mode: %s\n", ones ? "all-ones" : "random");
+  std::printf("iters: %d repeats: %d\n", iters, repeats);
+  std::printf("per_launch_us: %.3f\n", us);
+  std::printf("median_per_launch_us: %.3f\n", us);
+  std::printf("  hw_cycles_wallclock: %.0f\n", us * clock_mhz());
+  std::printf("tflops: %.3f\n", 2.0 * M * N * (double)K / us * 1e-6);
+  int rc = 0;
+  if (o.flag("--check")) {
+    // Sampled elements against the runner's float accumulation of decoded
+    // values (runner.cpp:1565-1597), its tolerance plus one output ulp.
+    const size_t ob = out == WAVE_F32 ? 4 : 2;
+    std::vector<uint8_t> hC((size_t)M * N * ob);
+    check_hip(hipMemcpy(hC.data(), C, hC.size(), hipMemcpyDeviceToHost), "hipMemcpy C");
+    auto val = [&](const std::vector<uint8_t> &x, const std::vector<uint8_t> &sx, int rows,
+                   int r, int kk) {
+      const uint8_t b = x[((size_t)r * K + kk) / 2];
+      return fp4_value((kk & 1) ? (b >> 4) : (b & 0xfu)) *
+             std::ldexp(1.0f, (int)sx[(size_t)(kk / 32) * rows + r] - 127);
+    };
+    double worst = 0.0;
+    for (size_t idx : sample_indices((size_t)M * N, 512, seed)) {
+      const int m = layout == WAVE_ROW_MAJOR ? (int)(idx / N) : (int)(idx % M);
+      const int n = layout == WAVE_ROW_MAJOR ? (int)(idx % N) : (int)(idx / M);
+      float acc = 0.f;
+      for (int kk = 0; kk < K; ++kk)
+        acc += val(hA, hSA, M, m, kk) * val(hB, hSB, N, n, kk);
+      double exp = acc, got;
+      if (out == WAVE_F32) {
+        float g;
+        std::memcpy(&g, &hC[idx * 4], 4);
+        got = g;
+      } else {
+        uint16_t g;
+        std::memcpy(&g, &hC[idx * 2], 2);
+        got = from_bits(g, out);
+        exp = from_bits(to_bits(acc, out), out);
+      }
+      const double diff = std::fabs(got - exp);
+      worst = std::max(worst, diff);
+      const double ulp = out == WAVE_F32 ? 0.0
+                         : std::ldexp(std::fabs(exp) > 0 ? std::fabs(exp) : 1.0,
+                                      out == WAVE_BF16 ? -7 : -10);
+      if (!(diff <= 1.0e-2 + 1.0e-3 * std::fabs(exp) + ulp)) {
+        std::fprintf(stderr,
+                     "output_check: failed m=%d n=%d expected=%.6f got=%.6f abs_diff=%.6f\n", m,
+                     n, exp, got, diff);
+        rc = 1;
+        break;
+      }
+    }
+    if (rc == 0)
+      std::printf("output_check: passed mode=sampled elements=514 max_abs_diff=%.6f\n", worst);
+  }
+  for (void *p : {A, B, SA, SB, C})
+    (void)hipFree(p);
+  return rc;
+}
+
 int run_gemm(Opts &o) {
   const int M = (int)o.num("--m", 8192), N = (int)o.num("--n", 8192), K = (int)o.num("--k", 8192);
+  if (o.str("--input-type", "f16") == "mxfp4") {
+    const std::string lay = o.str("--output-layout", "row-major");
+    if (lay != "row-major" && lay != "column-major")
+      die("--output-layout must be row-major or column-major");
+    const int iters = (int)o.num("--iters", 100), warmup = (int)o.num("--warmup", 10);
+    const int repeats = (int)o.num("--repeats", 3);
+    if (M <= 0 || N <= 0 || K <= 0 || iters <= 0 || warmup < 0 || repeats <= 0)
+      die("invalid non-positive argument");
+    return run_gemm_mxfp4(o, M, N, K, dtype_of(o.str("--c-type", "f16")),
+                          lay == "row-major" ? WAVE_ROW_MAJOR : WAVE_COL_MAJOR, lay, iters,
+                          warmup, repeats, (uint64_t)o.num("--seed", 7));
+  }
   const int in = dtype_of(o.str("--input-type", "f16"));
   const int out = dtype_of(o.str("--c-type", "f16"));
   const std::string lay = o.str("--output-layout", "row-major");

@@ -18,7 +18,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Element type codes of the C ABI (include/wave_runtime.h).
-enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2, kMXFP4 = 3 };
 
 // v_mfma_f32_32x32x16_{f16,bf16}: D[32x32] += A[32x16] * B[16x32].
 // Lane l supplies A[l%32][8*(l/32) .. +8] and B[8*(l/32) .. +8][l%32] as
@@ -33,6 +33,21 @@ __device__ __forceinline__ f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
         __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
         0);
+}
+
+// v_mfma_scale_f32_32x32x64_f8f6f4 with fp4 (e2m1) A and B: D[32x32] +=
+// (A * sa)[32x64] * (B * sb)[64x32].  Lane l supplies 32 fp4 values (16
+// bytes, two per byte, low nibble first) of row l%32 (A) / column l%32 (B)
+// at K offset 32*(l/32), and in byte 0 of sa / sb the e8m0 scale
+// 2^(raw-127) of exactly those 32 values; the accumulator layout is that of
+// the 16-bit 32x32 MFMA above (layout checked by the MXFP4 parity tests).
+__device__ __forceinline__ f32x16 mfma_fp4_32x32x64(u32x4 a, u32x4 b, f32x16 c, uint32_t sa,
+                                                    uint32_t sb) {
+  typedef int i32x8 __attribute__((ext_vector_type(8)));
+  const i32x8 av = {(int)a[0], (int)a[1], (int)a[2], (int)a[3], 0, 0, 0, 0};
+  const i32x8 bv = {(int)b[0], (int)b[1], (int)b[2], (int)b[3], 0, 0, 0, 0};
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 4, 4, 0, (int)sa, 0,
+                                                         (int)sb);
 }
 
 // 32-bit LDS byte address of a __shared__ object (address space 3).

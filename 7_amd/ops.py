@@ -61,6 +61,39 @@ def gemm(a: torch.Tensor, b: torch.Tensor, *, out_dtype="f16",
     return out
 
 
+def gemm_mxfp4(a: torch.Tensor, b: torch.Tensor, a_scale: torch.Tensor,
+               b_scale: torch.Tensor, *, out_dtype="f32", layout: str = "row",
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """MXFP4 scaled GEMM (the reference's ``mxfp4`` input type,
+    wave_matmul.py:996-1022): A [M, K/2] and B [N, K/2] uint8, two e2m1
+    values per byte (low nibble = even k); a_scale [K/32, M] and b_scale
+    [K/32, N] uint8 e8m0.  C[m, n] = sum_k a[m, k] 2^(sa[k/32, m]-127) *
+    b[n, k] 2^(sb[k/32, n]-127), fp32 accumulate.  layout as in gemm().
+    """
+    for t, name in ((a, "a"), (b, "b"), (a_scale, "a_scale"), (b_scale, "b_scale")):
+        _need(t, name)
+        if t.dtype != torch.uint8 or t.dim() != 2:
+            raise ValueError(f"{name} must be a 2-D uint8 tensor")
+    M, KB = a.shape
+    N = b.shape[0]
+    K = 2 * KB
+    if b.shape[1] != KB:
+        raise ValueError("a must be [M, K/2] and b [N, K/2]")
+    if K % 32 or tuple(a_scale.shape) != (K // 32, M) or tuple(b_scale.shape) != (K // 32, N):
+        raise ValueError("scales must be [K/32, M] and [K/32, N]")
+    odt = _dtype(out_dtype)
+    shape = (M, N) if layout == "row" else (N, M)
+    if out is None:
+        out = torch.empty(shape, dtype=odt, device=a.device)
+    elif tuple(out.shape) != shape or out.dtype != odt:
+        raise ValueError("out has the wrong shape or dtype")
+    _need(out, "out")
+    rt.check(rt.lib().wave_gemm_mxfp4_launch(
+        a.data_ptr(), b.data_ptr(), out.data_ptr(), a_scale.data_ptr(), b_scale.data_ptr(),
+        M, N, K, _DT[odt], rt.ROW_MAJOR if layout == "row" else rt.COL_MAJOR, _stream(a)))
+    return out
+
+
 def streamk_workspace_bytes(M: int, N: int, workers: int) -> tuple[int, int]:
     s, c = ctypes.c_size_t(), ctypes.c_size_t()
     rt.check(rt.lib().wave_gemm_streamk_workspace_bytes(M, N, workers, ctypes.byref(s),

@@ -94,6 +94,25 @@ int wave_gemm_streamk_workspace_reset(uint32_t *counters, int M, int N,
 int wave_gemm_streamk_counters_check(const uint32_t *counters, int M, int N,
                                      void *stream);
 
+/* ---- MXFP4 scaled GEMM ----------------------------------------------------
+ * C[m][n] = sum_k (a[m][k] * 2^(sa[k/32][m] - 127)) * (b[n][k] * 2^(sb[k/32][n] - 127))
+ * with fp32 accumulation and one RNE rounding to out_dtype.  A [M][K/2] and
+ * B [N][K/2] bytes, two OCP e2m1 (fp4) values per byte, low nibble = even k;
+ * A_scale [K/32][M] and B_scale [K/32][N] e8m0 bytes, group-major (the
+ * reference's canonical layout).  Replaces the `mxfp4` input type of
+ * `wmma_f16_matmul_tiled(A, B, C, A_scale, B_scale, trip)`
+ * (python/mlir/dialects/wave_matmul.py:187-206 `mfma.scale.f32.16x16x128.f4`,
+ * :996-1022 reference math, :6965-6975 argument list; runner
+ * wave-matmul-calibrate-runner.cpp:1565-1595 decode and expected value,
+ * :1792-1794 argument block).  Requires M, N % 256 == 0, K % 128 == 0 (the
+ * reference's MXFP4 K tile, runner.cpp:1098-1100), A, B and both scale
+ * arrays 16-byte aligned, C aligned to 4 elements, and
+ * (K/32) * max(M, N) < 2^32. */
+int wave_gemm_mxfp4_launch(const void *A, const void *B, void *C,
+                           const void *A_scale, const void *B_scale, int M,
+                           int N, int K, int out_dtype, int c_layout,
+                           void *stream);
+
 /* ---- flash-attention forward --------------------------------------------
  * O = softmax(Q K^T * scale) V.  Q, O: [batch][q_heads][seq][head_dim];
  * K, V: [batch][kv_heads][seq][head_dim]; dtype f16 or bf16 for all four;

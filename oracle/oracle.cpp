@@ -295,29 +295,25 @@ float oracle_gemm_element(const uint16_t *a, const uint16_t *b, int k,
   return acc;
 }
 
-// Rows [m0, m1) of C = A * B^T with A [M x K] and B [N x K] row-major, the
-// runner's per-element float accumulation in ascending k (runner.cpp:1586),
-// blocked over (n, k) so each C element is still summed strictly in k order.
-// This is also the multithreaded CPU baseline that bench.py times.
-void oracle_gemm_nt_rows(const uint16_t *a, const uint16_t *b, float *c,
-                         int m0, int m1, int n, int k, int dtype, int threads) {
+} // extern "C"
+
+namespace {
+
+// Rows [m0, m1) of C = A * B^T from decoded operands: `arow(r, dst)` writes
+// row r of A (K floats) and bt is B^T [K][N].  Each C element is the
+// runner's float accumulation in ascending k (runner.cpp:1586-1597), blocked
+// over (n, k) so every element is still summed strictly in k order.
+template <typename ARow>
+void gemmFloatRows(ARow arowOf, const std::vector<float> &bt, float *c, int m0,
+                   int m1, int n, int k, int threads) {
   constexpr int NB = 128, KB = 256, MB = 32;
-  // B^T as float, [K][N], shared by all threads.
-  std::vector<float> bt(static_cast<size_t>(k) * n);
-  parallelFor(0, n, threads, [&](int col) {
-    for (int i = 0; i < k; ++i)
-      bt[static_cast<size_t>(i) * n + col] =
-          toFloat(b[static_cast<size_t>(col) * k + i], dtype);
-  });
   int mBlocks = (m1 - m0 + MB - 1) / MB;
   parallelFor(0, mBlocks, threads, [&](int mb) {
     int rb = m0 + mb * MB;
     int re = std::min(rb + MB, m1);
     std::vector<float> arow(static_cast<size_t>(MB) * k);
     for (int r = rb; r < re; ++r)
-      for (int i = 0; i < k; ++i)
-        arow[static_cast<size_t>(r - rb) * k + i] =
-            toFloat(a[static_cast<size_t>(r) * k + i], dtype);
+      arowOf(r, arow.data() + static_cast<size_t>(r - rb) * k);
     std::vector<float> acc(static_cast<size_t>(MB) * NB);
     for (int nb = 0; nb < n; nb += NB) {
       int nw = std::min(NB, n - nb);
@@ -341,6 +337,29 @@ void oracle_gemm_nt_rows(const uint16_t *a, const uint16_t *b, float *c,
                     sizeof(float) * nw);
     }
   });
+}
+
+} // namespace
+
+extern "C" {
+
+// Rows [m0, m1) of C = A * B^T with A [M x K] and B [N x K] row-major (f16 or
+// bf16).  This is also the multithreaded CPU baseline that bench.py times.
+void oracle_gemm_nt_rows(const uint16_t *a, const uint16_t *b, float *c,
+                         int m0, int m1, int n, int k, int dtype, int threads) {
+  // B^T as float, [K][N], shared by all threads.
+  std::vector<float> bt(static_cast<size_t>(k) * n);
+  parallelFor(0, n, threads, [&](int col) {
+    for (int i = 0; i < k; ++i)
+      bt[static_cast<size_t>(i) * n + col] =
+          toFloat(b[static_cast<size_t>(col) * k + i], dtype);
+  });
+  gemmFloatRows(
+      [&](int r, float *dst) {
+        for (int i = 0; i < k; ++i)
+          dst[i] = toFloat(a[static_cast<size_t>(r) * k + i], dtype);
+      },
+      bt, c, m0, m1, n, k, threads);
 }
 
 void oracle_gemm_nt(const uint16_t *a, const uint16_t *b, float *c, int m,
@@ -573,6 +592,162 @@ int oracle_streamk_segments(int tile_count, int k_iterations, int workers,
 int oracle_hardware_threads(void) {
   unsigned n = std::thread::hardware_concurrency();
   return n ? static_cast<int>(n) : 1;
+}
+
+// ---- MXFP4 ---------------------------------------------------------------
+
+// OCP e2m1 decode: magnitude table {0, .5, 1, 1.5, 2, 3, 4, 6}, sign bit 3
+// (runner.cpp:722-727).  The table follows from e2m1 (1 sign, 2 exponent
+// bits with bias 1, 1 mantissa bit, subnormal at exponent 0).
+float oracle_mxfp4_code_value(int code) {
+  int e = (code >> 1) & 3, m = code & 1;
+  float mag = e == 0 ? 0.5f * m : std::ldexp(1.0f + 0.5f * m, e - 1);
+  return (code & 8) ? -mag : mag;
+}
+
+// e8m0 scale: 2^(raw - 127) (runner.cpp:729-731; wave_matmul.py:854-855).
+float oracle_e8m0_value(int raw) {
+  return static_cast<float>(std::ldexp(1.0, raw - 127));
+}
+
+// Packed codes for a `rows` x `k` operand, two per byte, low nibble = even
+// element (runner.cpp:1135-1150; wave_matmul.py:883-888).  Modes:
+//   RANDOM     runner: code = (nextRand >> 28) & 0xf on randState(seed, stream)
+//   ALL_ONES   runner --all-ones: 0x22 (1.0, 1.0)
+//   HALVES     Python non-random inputs: first half of the elements 1.0
+//              (code 0x2), the rest 2.0 (code 0x4) (wave_matmul.py:985-989)
+//   PY_RANDOM  Python random inputs: code 0x2 if bit 31 of the LCG state is
+//              set, else 0x4 (wave_matmul.py:858-866)
+void oracle_mxfp4_inputs(uint8_t *out, int rows, int k, int seed, int stream,
+                         int mode) {
+  size_t elements = static_cast<size_t>(rows) * static_cast<size_t>(k);
+  uint32_t st = oracle_rand_state(seed, stream);
+  size_t half = elements / 2;
+  for (size_t i = 0; i < elements; i += 2) {
+    uint8_t code[2];
+    for (int h = 0; h < 2; ++h) {
+      switch (mode) {
+      case ORACLE_MODE_ALL_ONES:
+        code[h] = 0x2;
+        break;
+      case ORACLE_MODE_HALVES:
+        code[h] = i + h < half ? 0x2 : 0x4;
+        break;
+      case ORACLE_MODE_PY_RANDOM:
+        code[h] = (oracle_next_rand(&st) >> 31) ? 0x2 : 0x4;
+        break;
+      default:
+        code[h] = static_cast<uint8_t>((oracle_next_rand(&st) >> 28) & 0xfu);
+        break;
+      }
+    }
+    out[i / 2] = static_cast<uint8_t>(code[0] | (code[1] << 4));
+  }
+}
+
+// Group-major [k/32][rows] e8m0 scales.  RANDOM: 124 + ((nextRand >> 29) & 3)
+// on randState(seed, stream) (runner.cpp:1208-1220); ALL_ONES: 0x7f;
+// HALVES / PY_RANDOM (the Python path, seed-independent,
+// wave_matmul.py:937-950): (0x7f for the first rows/2 rows, else `low`) -
+// group, with low 0x7e for A (stream 2) and 0x7d for B (stream 3).
+void oracle_mxfp4_scales(uint8_t *out, int rows, int k, int seed, int stream,
+                         int mode) {
+  int groups = k / 32;
+  size_t n = static_cast<size_t>(rows) * groups;
+  if (mode == ORACLE_MODE_ALL_ONES) {
+    std::memset(out, 0x7f, n);
+    return;
+  }
+  if (mode == ORACLE_MODE_HALVES || mode == ORACLE_MODE_PY_RANDOM) {
+    int low = stream == 3 ? 0x7d : 0x7e;
+    for (int g = 0; g < groups; ++g)
+      for (int r = 0; r < rows; ++r)
+        out[static_cast<size_t>(g) * rows + r] =
+            static_cast<uint8_t>((r < rows / 2 ? 0x7f : low) - g);
+    return;
+  }
+  uint32_t st = oracle_rand_state(seed, stream);
+  for (size_t i = 0; i < n; ++i)
+    out[i] = static_cast<uint8_t>(124u + ((oracle_next_rand(&st) >> 29) & 3u));
+}
+
+} // extern "C"
+
+namespace {
+// Element (row, kk) of a packed operand times its group scale
+// (runner.cpp:1565-1584 readMXFP4Input * e8m0ToFloat).
+inline float mxfp4Scaled(const uint8_t *x, const uint8_t *sx, int rows, int k,
+                         int64_t row, int kk) {
+  uint8_t packed = x[(static_cast<size_t>(row) * k + kk) / 2];
+  int code = (kk & 1) ? (packed >> 4) : (packed & 0xf);
+  return oracle_mxfp4_code_value(code) *
+         oracle_e8m0_value(sx[static_cast<size_t>(kk / 32) * rows + row]);
+}
+} // namespace
+
+extern "C" {
+
+// One C element, the runner's float accumulation (runner.cpp:1586-1597).
+float oracle_gemm_mxfp4_element(const uint8_t *a, const uint8_t *b,
+                                const uint8_t *sa, const uint8_t *sb, int m,
+                                int n, int k, int64_t row, int64_t col) {
+  float acc = 0.0f;
+  for (int i = 0; i < k; ++i)
+    acc += mxfp4Scaled(a, sa, m, k, row, i) * mxfp4Scaled(b, sb, n, k, col, i);
+  return acc;
+}
+
+// Rows [m0, m1) of C [M][N] row-major, same float accumulation order.
+void oracle_gemm_mxfp4_rows(const uint8_t *a, const uint8_t *b,
+                            const uint8_t *sa, const uint8_t *sb, float *c,
+                            int m0, int m1, int m, int n, int k, int threads) {
+  std::vector<float> bt(static_cast<size_t>(k) * n);
+  parallelFor(0, n, threads, [&](int col) {
+    for (int i = 0; i < k; ++i)
+      bt[static_cast<size_t>(i) * n + col] = mxfp4Scaled(b, sb, n, k, col, i);
+  });
+  gemmFloatRows(
+      [&](int r, float *dst) {
+        for (int i = 0; i < k; ++i)
+          dst[i] = mxfp4Scaled(a, sa, m, k, r, i);
+      },
+      bt, c, m0, m1, n, k, threads);
+}
+
+// AITER B layout (runner.cpp:1223-1246; wave_matmul.py:891-910): byte
+// (row, kb) of the [N][K/2] operand goes to
+// (((row/16 * K/64 + kb/32) * 2 + kb%32/16) * 16 + row%16) * 16 + kb%16.
+void oracle_mxfp4_aiter_b(const uint8_t *in, uint8_t *out, int n, int k) {
+  int storageK = k / 2, kBlocks = storageK / 32;
+  for (int row = 0; row < n; ++row)
+    for (int kb = 0; kb < storageK; ++kb) {
+      size_t dst = ((((static_cast<size_t>(row / 16) * kBlocks + kb / 32) * 2 +
+                      (kb % 32) / 16) * 16 + row % 16) * 16) + kb % 16;
+      out[dst] = in[static_cast<size_t>(row) * storageK + kb];
+    }
+}
+
+// AITER scale layout (runner.cpp:1248-1283; wave_matmul.py:913-935): rows
+// padded to 256, groups to 8, pad bytes 0x7f; scale (group g, row r) goes to
+// (r/32 * G8 + g/8) * 256 + (g%4) * 64 + (r%16) * 4 + (g%8/4) * 2 + r%32/16,
+// G8 = padded groups / 8.  Returns the padded size; out may be NULL.
+size_t oracle_mxfp4_aiter_scales(const uint8_t *in, uint8_t *out, int rows,
+                                 int k) {
+  int groups = k / 32;
+  size_t paddedRows = (static_cast<size_t>(rows) + 255) / 256 * 256;
+  size_t paddedGroups = (static_cast<size_t>(groups) + 7) / 8 * 8;
+  size_t total = paddedRows * paddedGroups;
+  if (!out)
+    return total;
+  std::memset(out, 0x7f, total);
+  size_t g8 = paddedGroups / 8;
+  for (int r = 0; r < rows; ++r)
+    for (int g = 0; g < groups; ++g) {
+      size_t dst = (static_cast<size_t>(r / 32) * g8 + g / 8) * 256 +
+                   (g % 4) * 64 + (r % 16) * 4 + ((g % 8) / 4) * 2 + (r % 32) / 16;
+      out[dst] = in[static_cast<size_t>(g) * rows + r];
+    }
+  return total;
 }
 
 } // extern "C"

@@ -32,7 +32,8 @@ enum {
   ORACLE_MODE_ALL_ONES = 1,  /* --all-ones                                  */
   ORACLE_MODE_RAND_INT = 2,  /* --rand-int (hipBLASLt rand_int)             */
   ORACLE_MODE_HPL = 3,       /* --hpl                                       */
-  ORACLE_MODE_HALVES = 4     /* python non-random: first half 1, rest 2     */
+  ORACLE_MODE_HALVES = 4,    /* python non-random: first half 1, rest 2     */
+  ORACLE_MODE_PY_RANDOM = 5  /* python MXFP4 random codes (0x2 / 0x4)       */
 };
 
 /* ---- scalar generators and rounding ---------------------------------- */
@@ -57,6 +58,24 @@ void oracle_gemm_nt_rows(const uint16_t *a, const uint16_t *b, float *c,
 float oracle_gemm_element(const uint16_t *a, const uint16_t *b, int k,
                           int dtype, int64_t row, int64_t col);
 void oracle_round_output(const float *in, void *out, size_t n, int out_dtype);
+
+/* ---- MXFP4 scaled GEMM (runner.cpp:718-732, :1135-1150, :1208-1283,
+ *      :1565-1597; wave_matmul.py:854-950, :996-1022) ------------------- */
+float oracle_mxfp4_code_value(int code);
+float oracle_e8m0_value(int raw);
+void oracle_mxfp4_inputs(uint8_t *out, int rows, int k, int seed, int stream,
+                         int mode);
+void oracle_mxfp4_scales(uint8_t *out, int rows, int k, int seed, int stream,
+                         int mode);
+float oracle_gemm_mxfp4_element(const uint8_t *a, const uint8_t *b,
+                                const uint8_t *sa, const uint8_t *sb, int m,
+                                int n, int k, int64_t row, int64_t col);
+void oracle_gemm_mxfp4_rows(const uint8_t *a, const uint8_t *b,
+                            const uint8_t *sa, const uint8_t *sb, float *c,
+                            int m0, int m1, int m, int n, int k, int threads);
+void oracle_mxfp4_aiter_b(const uint8_t *in, uint8_t *out, int n, int k);
+size_t oracle_mxfp4_aiter_scales(const uint8_t *in, uint8_t *out, int rows,
+                                 int k);
 
 /* ---- flash attention ---------------------------------------------------- */
 void oracle_fa_f32_inputs(uint16_t *q, uint16_t *k, uint16_t *v, int block_m,

@@ -21,6 +21,7 @@ _lib = None
 
 F32, F16, BF16 = 0, 1, 2
 MODE_RANDOM, MODE_ALL_ONES, MODE_RAND_INT, MODE_HPL, MODE_HALVES = 0, 1, 2, 3, 4
+MODE_PY_RANDOM = 5
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -55,6 +56,15 @@ def lib() -> ctypes.CDLL:
             "oracle_gemm_nt_rows": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _I]),
             "oracle_gemm_element": (ctypes.c_float, [_P, _P, _I, _I, _I64, _I64]),
             "oracle_round_output": (None, [_P, _P, _SZ, _I]),
+            "oracle_mxfp4_code_value": (ctypes.c_float, [_I]),
+            "oracle_e8m0_value": (ctypes.c_float, [_I]),
+            "oracle_mxfp4_inputs": (None, [_P, _I, _I, _I, _I, _I]),
+            "oracle_mxfp4_scales": (None, [_P, _I, _I, _I, _I, _I]),
+            "oracle_gemm_mxfp4_element": (ctypes.c_float, [_P, _P, _P, _P, _I, _I, _I, _I64,
+                                                           _I64]),
+            "oracle_gemm_mxfp4_rows": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I]),
+            "oracle_mxfp4_aiter_b": (None, [_P, _P, _I, _I]),
+            "oracle_mxfp4_aiter_scales": (_SZ, [_P, _P, _I, _I]),
             "oracle_fa_f32_inputs": (None, [_P, _P, _P, _I, _I, _I, _I]),
             "oracle_fa_f32_reference": (None, [_P, _P, _P, _P, _I, _I, _I]),
             "oracle_fa_gfx950_inputs": (None, [_P, _P, _P, _SZ, _I, _I, _I]),
@@ -148,6 +158,68 @@ def gemm_elements(a: np.ndarray, b: np.ndarray, rows, cols, dtype: int = F16) ->
     L = lib()
     return np.array([L.oracle_gemm_element(_ptr(a), _ptr(b), k, dtype, int(r), int(c))
                      for r, c in zip(rows, cols)], dtype=np.float32)
+
+
+# ---- MXFP4 ------------------------------------------------------------------------
+def mxfp4_inputs(rows: int, k: int, seed: int = 0, stream: int = 0,
+                 mode: int = MODE_RANDOM) -> np.ndarray:
+    """Packed e2m1 codes [rows, k/2] (low nibble = even k)."""
+    out = np.empty(rows * k // 2, dtype=np.uint8)
+    lib().oracle_mxfp4_inputs(_ptr(out), rows, k, seed, stream, mode)
+    return out.reshape(rows, k // 2)
+
+
+def mxfp4_scales(rows: int, k: int, seed: int = 0, stream: int = 2,
+                 mode: int = MODE_RANDOM) -> np.ndarray:
+    """Group-major e8m0 scales [k/32, rows] (stream 2 = A, 3 = B)."""
+    out = np.empty(rows * (k // 32), dtype=np.uint8)
+    lib().oracle_mxfp4_scales(_ptr(out), rows, k, seed, stream, mode)
+    return out.reshape(k // 32, rows)
+
+
+def mxfp4_operands(m: int, n: int, k: int, seed: int = 0, mode: int = MODE_RANDOM):
+    """(A, B, A_scale, B_scale) as the runner (RANDOM / ALL_ONES) or the
+    Python builder (HALVES / PY_RANDOM) makes them."""
+    return (mxfp4_inputs(m, k, seed, 0, mode), mxfp4_inputs(n, k, seed, 1, mode),
+            mxfp4_scales(m, k, seed, 2, mode), mxfp4_scales(n, k, seed, 3, mode))
+
+
+def gemm_mxfp4_rows(a, b, sa, sb, m0: int, m1: int, threads: int | None = None) -> np.ndarray:
+    """Rows [m0, m1) of the MXFP4 product, the runner's float accumulation."""
+    a, b, sa, sb = (np.ascontiguousarray(x, dtype=np.uint8) for x in (a, b, sa, sb))
+    m, n, k = a.shape[0], b.shape[0], 2 * a.shape[1]
+    c = np.zeros((m, n), dtype=np.float32)
+    lib().oracle_gemm_mxfp4_rows(_ptr(a), _ptr(b), _ptr(sa), _ptr(sb), _ptr(c), m0, m1, m, n,
+                                 k, threads or hardware_threads())
+    return c[m0:m1]
+
+
+def gemm_mxfp4(a, b, sa, sb, threads: int | None = None) -> np.ndarray:
+    return gemm_mxfp4_rows(a, b, sa, sb, 0, a.shape[0], threads)
+
+
+def gemm_mxfp4_elements(a, b, sa, sb, rows, cols) -> np.ndarray:
+    a, b, sa, sb = (np.ascontiguousarray(x, dtype=np.uint8) for x in (a, b, sa, sb))
+    m, n, k = a.shape[0], b.shape[0], 2 * a.shape[1]
+    L = lib()
+    return np.array([L.oracle_gemm_mxfp4_element(_ptr(a), _ptr(b), _ptr(sa), _ptr(sb), m, n,
+                                                 k, int(r), int(c))
+                     for r, c in zip(rows, cols)], dtype=np.float32)
+
+
+def mxfp4_aiter_b(b: np.ndarray, n: int, k: int) -> np.ndarray:
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    out = np.empty(b.size, dtype=np.uint8)
+    lib().oracle_mxfp4_aiter_b(_ptr(b), _ptr(out), n, k)
+    return out
+
+
+def mxfp4_aiter_scales(s: np.ndarray, rows: int, k: int) -> np.ndarray:
+    s = np.ascontiguousarray(s, dtype=np.uint8)
+    size = lib().oracle_mxfp4_aiter_scales(_ptr(s), None, rows, k)
+    out = np.empty(size, dtype=np.uint8)
+    lib().oracle_mxfp4_aiter_scales(_ptr(s), _ptr(out), rows, k)
+    return out
 
 
 # ---- flash attention ----------------------------------------------------------

@@ -89,4 +89,59 @@ void ref_streamk_workspace(int m, int n, int k, int workers, uint64_t *scratch,
   *block = l.blockThreads;
 }
 
+// MXFP4 generators (runner.cpp:1135-1150, :1208-1220): packed e2m1 codes and
+// group-major e8m0 scales for `rows` x `k`.
+void ref_mxfp4_input_bytes(int rows, int k, int seed, int stream, int all_ones,
+                           uint8_t *out) {
+  std::vector<uint8_t> b = makeMXFP4InputBytes(
+      static_cast<size_t>(rows) * k, seed, stream, all_ones != 0);
+  std::memcpy(out, b.data(), b.size());
+}
+void ref_mxfp4_scale_bytes(int rows, int k, int seed, int stream, int all_ones,
+                           uint8_t *out) {
+  std::vector<uint8_t> b = makeMXFP4ScaleBytes(rows, k, seed, stream, all_ones != 0);
+  std::memcpy(out, b.data(), b.size());
+}
+float ref_mxfp4_code_to_float(int code) { return mxfp4CodeToFloat(static_cast<uint8_t>(code)); }
+float ref_e8m0_to_float(int raw) { return e8m0ToFloat(static_cast<uint8_t>(raw)); }
+
+// The runner's MXFP4 expected output: makeHostInputs + computeExpectedElement
+// + roundExpectedOutput (runner.cpp:1436-1456, :1565-1597).
+void ref_gemm_mxfp4_expected(int m, int n, int k, int seed, int all_ones,
+                             int out_type, double *out) {
+  Args a;
+  a.m = m;
+  a.n = n;
+  a.k = k;
+  a.inputType = InputType::MXFP4;
+  a.waveSize = 64;
+  a.seed = seed;
+  a.allOnes = all_ones != 0;
+  a.cType = out_type == 1 ? CType::F16 : out_type == 2 ? CType::BF16 : CType::F32;
+  HostInputs in = makeHostInputs(a);
+  for (int i = 0; i < m; ++i)
+    for (int j = 0; j < n; ++j)
+      out[static_cast<size_t>(i) * n + j] =
+          roundExpectedOutput(computeExpectedElement(in, a, i, j), a.cType);
+}
+
+// AITER layouts (runner.cpp:1223-1283): shuffled B bytes and scale bytes.
+void ref_mxfp4_aiter_b(const uint8_t *in, int n, int k, uint8_t *out) {
+  Args a;
+  a.n = n;
+  a.k = k;
+  std::vector<uint8_t> c(in, in + static_cast<size_t>(n) * (k / 2));
+  std::vector<uint8_t> s = makeAITERBBytes(c, a);
+  std::memcpy(out, s.data(), s.size());
+}
+size_t ref_mxfp4_aiter_scales(const uint8_t *in, int rows, int k, uint8_t *out) {
+  Args a;
+  a.k = k;
+  std::vector<uint8_t> c(in, in + static_cast<size_t>(rows) * (k / 32));
+  std::vector<uint8_t> s = makeAITERScaleBytes(c, rows, a);
+  if (out)
+    std::memcpy(out, s.data(), s.size());
+  return s.size();
+}
+
 } // extern "C"

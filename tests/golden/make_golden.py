@@ -145,6 +145,59 @@ def matmul_vectors() -> dict:
     return out
 
 
+def mxfp4_vectors() -> dict:
+    """The runner's MXFP4 generators, expected outputs and AITER shuffles
+    (runner.cpp:1135-1150, :1208-1283, :1436-1456, :1565-1597)."""
+    L = load("libref_matmul.so")
+    L.ref_mxfp4_input_bytes.argtypes = [ctypes.c_int] * 5 + [P]
+    L.ref_mxfp4_scale_bytes.argtypes = [ctypes.c_int] * 5 + [P]
+    L.ref_mxfp4_code_to_float.restype = ctypes.c_float
+    L.ref_mxfp4_code_to_float.argtypes = [ctypes.c_int]
+    L.ref_e8m0_to_float.restype = ctypes.c_float
+    L.ref_e8m0_to_float.argtypes = [ctypes.c_int]
+    L.ref_gemm_mxfp4_expected.argtypes = [ctypes.c_int] * 6 + [P]
+    L.ref_mxfp4_aiter_b.argtypes = [P, ctypes.c_int, ctypes.c_int, P]
+    L.ref_mxfp4_aiter_scales.restype = ctypes.c_size_t
+    L.ref_mxfp4_aiter_scales.argtypes = [P, ctypes.c_int, ctypes.c_int, P]
+
+    out: dict = {}
+    out["code_to_float"] = [L.ref_mxfp4_code_to_float(c) for c in range(16)]
+    out["e8m0_to_float"] = [L.ref_e8m0_to_float(r) for r in range(100, 140)]
+    inputs, scales = {}, {}
+    for seed in (0, 7):
+        for ones in (0, 1):
+            for (rows, k) in ((4, 64), (16, 128)):
+                for stream in (0, 1):
+                    buf = np.zeros(rows * k // 2, np.uint8)
+                    L.ref_mxfp4_input_bytes(rows, k, seed, stream, ones, ptr(buf))
+                    inputs[f"{seed}:{ones}:{rows}x{k}:{stream}"] = buf.tolist()
+                for stream in (2, 3):
+                    buf = np.zeros(rows * k // 32, np.uint8)
+                    L.ref_mxfp4_scale_bytes(rows, k, seed, stream, ones, ptr(buf))
+                    scales[f"{seed}:{ones}:{rows}x{k}:{stream}"] = buf.tolist()
+    out["inputs"] = inputs
+    out["scales"] = scales
+    gemms = {}
+    for (m, n, k, seed, ones, ot) in ((16, 16, 128, 7, 0, 0), (32, 16, 256, 0, 0, 0),
+                                      (16, 32, 128, 7, 0, 1), (16, 16, 128, 3, 0, 2),
+                                      (16, 16, 256, 7, 1, 0)):
+        buf = np.zeros(m * n, np.float64)
+        L.ref_gemm_mxfp4_expected(m, n, k, seed, ones, ot, ptr(buf))
+        gemms[f"{m}x{n}x{k}:{seed}:{ones}:{ot}"] = buf.tolist()
+    out["gemm_expected"] = gemms
+    rng = np.random.default_rng(5)
+    b = rng.integers(0, 256, 32 * 64, dtype=np.uint8)
+    sb = np.zeros(32 * 64, np.uint8)
+    L.ref_mxfp4_aiter_b(ptr(b), 32, 128, ptr(sb))
+    out["aiter_b"] = {"n": 32, "k": 128, "in": b.tolist(), "out": sb.tolist()}
+    s = rng.integers(0, 256, 40 * 12, dtype=np.uint8)  # 40 rows, K = 384 (12 groups)
+    size = L.ref_mxfp4_aiter_scales(ptr(s), 40, 384, None)
+    ss = np.zeros(size, np.uint8)
+    L.ref_mxfp4_aiter_scales(ptr(s), 40, 384, ptr(ss))
+    out["aiter_scales"] = {"rows": 40, "k": 384, "in": s.tolist(), "out": ss.tolist()}
+    return out
+
+
 def fa_vectors() -> dict:
     out: dict = {}
     L32 = load("libref_fa_f32.so")
@@ -196,6 +249,8 @@ def fa_vectors() -> dict:
 def main() -> None:
     with open(os.path.join(HERE, "matmul_runner_vectors.json"), "w") as f:
         json.dump(matmul_vectors(), f, separators=(",", ":"))
+    with open(os.path.join(HERE, "mxfp4_runner_vectors.json"), "w") as f:
+        json.dump(mxfp4_vectors(), f, separators=(",", ":"))
     with open(os.path.join(HERE, "fa_runner_vectors.json"), "w") as f:
         json.dump(fa_vectors(), f, separators=(",", ":"))
     print("golden fixtures written to", HERE)

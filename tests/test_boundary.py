@@ -65,6 +65,27 @@ def test_gemm_rejects_bad_arguments(wave, kw, status):
     assert L.wave_last_error()
 
 
+def _mxfp4(L, **kw):
+    a = dict(A=256, B=512, C=1024, SA=2048, SB=4096, M=256, N=256, K=256, o=0, lay=0)
+    a.update(kw)
+    return L.wave_gemm_mxfp4_launch(a["A"], a["B"], a["C"], a["SA"], a["SB"], a["M"], a["N"],
+                                    a["K"], a["o"], a["lay"], None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(A=None), -1), (dict(SA=None), -1), (dict(SB=None), -1), (dict(M=0), -1),
+    (dict(K=-128), -1), (dict(K=64), -1), (dict(K=200), -1), (dict(o=3), -1),
+    (dict(lay=2), -1), (dict(M=384), -2), (dict(N=100), -2), (dict(A=264), -2),
+    (dict(SB=4100), -2), (dict(C=1032), -2), (dict(K=1 << 30, M=1 << 15), -2),
+])
+def test_mxfp4_rejects_bad_arguments(wave, kw, status):
+    """The reference's MXFP4 contract: K a multiple of the 128-wide MFMA K
+    tile (runner.cpp:1098-1100), packed rows and scales 16-byte aligned."""
+    L = wave.runtime.lib()
+    assert _mxfp4(L, **kw) == status
+    assert L.wave_last_error()
+
+
 def test_streamk_workspace_sizes(wave):
     # runner.cpp:393-412 and rand_int_test.cpp:216-227: 5 workers ->
     # 5*2*256*256*4 bytes of scratch; 512x768 -> 6 counters
