@@ -79,8 +79,12 @@ using DefaultCfg = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE, WAVE_GEMM_WAVES>;
 // MXFP4: the same ring with K counted in 16-bit units (one 64-byte row
 // chunk = 128 fp4 values per stage, one MFMA 32x32x64 per 32-byte slice)
 // and 2 KiB of scales per stage: four 32-value groups x (256 A + 256 B)
-// rows, laid out [group][A rows | B rows].
-using Fp4Cfg = Cfg<32, 4, 4, 4 * 512>;
+// rows, laid out [group][A rows | B rows].  8 waves (two per SIMD, 128x64
+// outputs each) measured 2-8 % faster than 4 for these short-latency MFMAs.
+#ifndef WAVE_FP4_WAVES
+#define WAVE_FP4_WAVES 8
+#endif
+using Fp4Cfg = Cfg<32, 4, WAVE_FP4_WAVES, 4 * 512>;
 
 // LDS geometry of an operand tile.  The tile is stored as 128-byte
 // "super-rows" of eight 16-byte slots: with BK = 64 super-row R is tile row
@@ -313,12 +317,21 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
     const char *b_tile =
         reinterpret_cast<const char *>(p.B) + (size_t)n0 * rowbytes;
     const uint32_t lds0 = lds_addr(smem) + wave * C::DMA * 1024;
-    // MXFP4 scales: wave w copies group 4*kt + w of the A scales (lanes
-    // 0-15, 256 rows) and of the B scales (lanes 16-31) into its 512 bytes
-    // of the stage's scale area.
-    const uint32_t lds_sc = lds_addr(smem) + 2 * C::OPB + wave * 512;
-    const uint32_t a_sc = wave * (uint32_t)p.M + m0 + (lane & 15) * 16;
-    const uint32_t b_sc = wave * (uint32_t)p.N + n0 + (lane & 15) * 16;
+    // MXFP4 scales: a stage has 8 scale jobs, (group j/2 of the stage) x
+    // (A if j is even, else B), 256 rows = 4 bytes a lane each; wave w runs
+    // jobs w*SJ .. w*SJ+SJ-1 into [group][A rows | B rows] of the stage's
+    // scale area.  All 64 lanes take part, so the loop body stays one basic
+    // block and its explicit instruction order holds.
+    constexpr int SJ = IN_DT == kMXFP4 ? 8 / C::WAVES : 0;
+    uint32_t lds_sc[SJ > 0 ? SJ : 1], g_sc[SJ > 0 ? SJ : 1];
+    if constexpr (SJ > 0) {
+#pragma unroll
+      for (int s = 0; s < SJ; ++s) {
+        const uint32_t j = wave * SJ + s, grp = j >> 1;
+        lds_sc[s] = lds_addr(smem) + 2 * C::OPB + grp * 512 + (j & 1) * 256;
+        g_sc[s] = grp * (uint32_t)((j & 1) ? p.N : p.M) + ((j & 1) ? n0 : m0) + lane * 4;
+      }
+    }
     // DMA d of one stage (0 <= d < 2*DMA): A chunks first, then B; MXFP4
     // adds d = 2*DMA (A scales) and 2*DMA + 1 (B scales).
     auto issue_one = [&](uint32_t stage, int kt, int d) {
@@ -329,16 +342,14 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
         dma16(l + C::OPB + (d - C::DMA) * 1024, b_tile + (size_t)kt * C::RB,
               goff[d - C::DMA]);
       } else if constexpr (IN_DT == kMXFP4) {
-        const uint32_t g0 = (uint32_t)kt * 4u;
-        if (d == 2 * C::DMA) {
-          if (lane < 16)
-            dma16(lds_sc + stage * C::STAGE, p.a_scale, a_sc + g0 * (uint32_t)p.M);
-        } else if (lane - 16u < 16u) {
-          dma16(lds_sc + stage * C::STAGE, p.b_scale, b_sc + g0 * (uint32_t)p.N);
-        }
+        const int s = d - 2 * C::DMA;
+        const bool is_b = ((wave * SJ + s) & 1) != 0;
+        const uint32_t g0 = (uint32_t)kt * 4u * (uint32_t)(is_b ? p.N : p.M);
+        dma4(lds_sc[s] + stage * C::STAGE, is_b ? (const void *)p.b_scale : p.a_scale,
+             g_sc[s] + g0);
       }
     };
-    constexpr int kDmaPerStage = 2 * C::DMA + (IN_DT == kMXFP4 ? 2 : 0);
+    constexpr int kDmaPerStage = 2 * C::DMA + SJ;
     auto issue = [&](uint32_t stage, int kt) {
 #pragma unroll
       for (int d = 0; d < kDmaPerStage; ++d)
@@ -501,6 +512,70 @@ __device__ __forceinline__ void store_tile(const Params &p, int m0, int n0,
   }
 }
 
+// Whole-tile store through LDS.  The MFMA layout leaves each lane 4
+// consecutive P values of one Q line, so a direct store instruction writes 8
+// or 16 bytes into each of 32 lines; here the tile is first transposed into
+// LDS lines (128 KiB: all 256 Q lines of 16-bit output, or 128 at a time of
+// f32) and then written as whole 512- or 1024-byte line runs, 16 bytes a
+// lane.  The 16-byte chunks of LDS line r sit at chunk ^ (r mod chunks), so
+// both the scattered writes and the line reads spread over all banks.
+// Needs: the mainloop's LDS reads and DMA finished, a whole tile, C 16-byte
+// aligned and ldc * 2 a multiple of 16 bytes.
+template <class C, int OUT_DT, bool COL_MAJOR, typename Get>
+__device__ __forceinline__ void store_tile_lds(const Params &p, int m0, int n0, uint8_t *smem,
+                                               Get get) {
+  constexpr int OB = OUT_DT == kF32 ? 4 : 2;
+  constexpr int LINE = 256 * OB;             // bytes of one 256-wide line
+  constexpr int CH = LINE / 16;              // 16-byte chunks per line
+  constexpr int ROWS = 131072 / LINE;        // lines per pass (256 or 128)
+  constexpr int PASSES = 256 / ROWS;
+  static_assert(C::SMEM >= 131072, "LDS ring smaller than one output pass");
+  const uint32_t tid = threadIdx.x;
+  const uint32_t wave = tid >> 6, lane = tid & 63;
+  const int wp = wave % C::WPN, wq = wave / C::WPN;
+  const int P0 = COL_MAJOR ? m0 : n0, Q0 = COL_MAJOR ? n0 : m0;
+  const int wq0 = wq * (C::TQ * 32);
+  char *out = reinterpret_cast<char *>(p.C);
+#pragma unroll
+  for (int pass = 0; pass < PASSES; ++pass) {
+    if (wq0 / ROWS == pass) {
+#pragma unroll
+      for (int tq = 0; tq < C::TQ; ++tq) {
+        const uint32_t r = (uint32_t)(wq0 % ROWS + tq * 32) + (lane & 31);
+#pragma unroll
+        for (int tp = 0; tp < C::TP; ++tp) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            // Element p = wp*TP*32 + tp*32 + 8g + 4*(lane/32) of line r.
+            const uint32_t e = wp * (C::TP * 32) + tp * 32 + 8 * g + 4 * (lane >> 5);
+            const uint32_t c = e * OB / 16, within = (e * OB) % 16;
+            uint8_t *dst = smem + r * LINE + ((c ^ (r % CH)) * 16) + within;
+            const f32x4 v = get(tp, tq, g);
+            if constexpr (OUT_DT == kF32)
+              *reinterpret_cast<f32x4 *>(dst) = v;
+            else
+              *reinterpret_cast<u32x2 *>(dst) =
+                  u32x2{pack2<OUT_DT>(v[0], v[1]), pack2<OUT_DT>(v[2], v[3])};
+          }
+        }
+      }
+    }
+    lds_barrier();
+    constexpr int PER = ROWS * CH / C::THREADS;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const uint32_t flat = i * C::THREADS + tid;
+      const uint32_t r = flat / CH, c = flat % CH;
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(smem + r * LINE + ((c ^ (r % CH)) * 16));
+      const size_t q = (size_t)(Q0 + pass * ROWS + (int)r);
+      *reinterpret_cast<u32x4 *>(out + (q * p.ldc + P0) * OB + c * 16) = v;
+    }
+    // Every wave's line reads are done before LDS is written again (next
+    // pass, or the next tile's DMA ring in a grid-stride caller).
+    lds_barrier();
+  }
+}
+
 // One 256x256 output tile: CTA `raw` of a grid of tiles_m * tiles_n CTAs.
 // smem: DefaultCfg::SMEM bytes of 1024-byte-aligned LDS.
 template <int IN_DT>
@@ -512,7 +587,10 @@ __device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *sme
   static_assert(IN_DT != kMXFP4 || !MASKED, "MXFP4 takes whole tiles only");
   int tm, tn;
   tile_coords(raw, p.tiles_m, p.tiles_n, p.group_m, true, tm, tn);
-  const int m0 = tm * kTile, n0 = tn * kTile;
+  // The tile origin is uniform; readfirstlane keeps it (and the DMA bases
+  // derived from it) in SGPRs, as the DMA's scalar base operand requires.
+  const int m0 = __builtin_amdgcn_readfirstlane(tm * kTile);
+  const int n0 = __builtin_amdgcn_readfirstlane(tn * kTile);
   f32x16 acc[C::TP][C::TQ];
 #pragma unroll
   for (int i = 0; i < C::TP; ++i)
@@ -521,14 +599,20 @@ __device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *sme
       acc[i][j] = f32x16{};
   const int kt_n = (p.K + C::BK - 1) / C::BK;
   mainloop<C, IN_DT, COL_MAJOR, MASKED, VEC>(p, m0, n0, 0, kt_n, smem, acc);
-  store_tile<C, OUT_DT, COL_MAJOR, MASKED>(p, m0, n0, [&](int tp, int tq, int g) {
+  auto get = [&](int tp, int tq, int g) {
     return f32x4{acc[tp][tq][4 * g], acc[tp][tq][4 * g + 1],
                  acc[tp][tq][4 * g + 2], acc[tp][tq][4 * g + 3]};
-  });
+  };
+  // 16-bit output goes through LDS; f32 output, twice the bytes, is bound by
+  // HBM writes either way and is stored directly (measured faster).
+  if (!MASKED && OUT_DT != kF32 && (((uintptr_t)p.C | (uintptr_t)p.ldc * 2) & 15) == 0)
+    store_tile_lds<C, OUT_DT, COL_MAJOR>(p, m0, n0, smem, get);
+  else
+    store_tile<C, OUT_DT, COL_MAJOR, MASKED>(p, m0, n0, get);
 }
 
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
-__global__ __launch_bounds__(DefaultCfg::THREADS, 1) void tiled_kernel(Params p) {
+__global__ __launch_bounds__(CfgFor<IN_DT>::THREADS, 1) void tiled_kernel(Params p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[CfgFor<IN_DT>::SMEM];
   tiled_cta<IN_DT, OUT_DT, COL_MAJOR, MASKED, VEC>(p, blockIdx.x, smem);
 }

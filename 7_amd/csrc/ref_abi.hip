@@ -11,6 +11,12 @@
 //     (wave_matmul.py:11415-11427, :6954-6982; runner.cpp:1790-1791).
 //     -DWAVE_ABI_GEMM -DWAVE_ABI_M= -DWAVE_ABI_N= -DWAVE_ABI_K=
 //     -DWAVE_ABI_IN=kF16|kBF16 -DWAVE_ABI_OUT=kF32|kF16|kBF16 -DWAVE_ABI_CM=0|1
+//   wmma_f16_matmul_tiled(const u8* A, const u8* B, C_t* C, const u8* A_scale,
+//                         const u8* B_scale, int32 trip)
+//     the reference's mxfp4 input type (wave_matmul.py:6965-6975; runner.cpp
+//     :1792-1794): packed e2m1 A [M][K/2], B [N][K/2], e8m0 scales
+//     [K/32][M], [K/32][N].  -DWAVE_ABI_MXFP4 -DWAVE_ABI_M= -DWAVE_ABI_N=
+//     -DWAVE_ABI_K= -DWAVE_ABI_OUT=kF32|kF16|kBF16 -DWAVE_ABI_CM=0|1
 //   gfx950_f16_streamk_gemm(const f16* A, const f16* B, f16* C, f32* scratch,
 //                           u32* counters, int32 workers)
 //     (wave_matmul.py:11556-11567; runner.cpp:1811-1816; column-major C,
@@ -30,6 +36,10 @@
 //    Block 256 threads and >= 131072 bytes of dynamic LDS (the reference's
 //    gfx950 4-wave profile passes exactly that).  `trip` is accepted and
 //    unused: the K loop length follows from the baked K.
+//  * MXFP4 wmma_f16_matmul_tiled: any grid (grid-stride over the tiles),
+//    block 512 (8 waves, the reference's gfx950-mxfp4-256x256-8wave block)
+//    and >= 139264 bytes of dynamic LDS; M, N % 256 == 0 and K % 128 == 0
+//    at build time; A, B and both scale arrays 16-byte aligned.
 //  * gfx950_f16_streamk_gemm: grid (workers), block 256, >= 131076 bytes of
 //    dynamic LDS; workspace as wave_gemm_streamk_workspace_bytes.
 //  * flash_attention_bf16_gfx950: grid (S/256, B*H), block 512, >= 102400
@@ -108,6 +118,46 @@ extern "C" __global__ __launch_bounds__(256, 1) void wmma_f16_matmul_tiled(
   const int ctas = gridDim.x * gridDim.y;
   for (int raw = blockIdx.y * gridDim.x + blockIdx.x; raw < tiles; raw += ctas)
     tiled_cta<WAVE_ABI_IN, WAVE_ABI_OUT, CM, !kFast, kVec>(p, raw, dsmem);
+}
+#endif
+
+#ifdef WAVE_ABI_MXFP4
+extern "C" __global__ __launch_bounds__(wave::gemm::Fp4Cfg::THREADS, 1) void wmma_f16_matmul_tiled(
+    const uint8_t *A, const uint8_t *B, void *C, const uint8_t *A_scale, const uint8_t *B_scale,
+    int trip) {
+  using namespace wave::gemm;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t dsmem[];
+  (void)trip;
+  if (blockDim.x != Fp4Cfg::THREADS || blockDim.y != 1 || blockDim.z != 1 ||
+      dynamic_lds_bytes() < (uint32_t)Fp4Cfg::SMEM)
+    return;
+  constexpr int M = WAVE_ABI_M, N = WAVE_ABI_N, K = WAVE_ABI_K;
+  static_assert(M > 0 && N > 0 && M % kTile == 0 && N % kTile == 0 && K > 0 && K % 128 == 0,
+                "MXFP4 code objects take whole 256x256 tiles and K % 128 == 0");
+  static_assert((uint64_t)(K / 32) * (M > N ? M : N) < (1ull << 32), "scale offsets");
+  constexpr bool CM = WAVE_ABI_CM != 0;
+  constexpr int OUT_BYTES = WAVE_ABI_OUT == kF32 ? 4 : 2;
+  if (!(aligned16(A) && aligned16(B) && aligned16(A_scale) && aligned16(B_scale)) ||
+      ((uintptr_t)C % (4 * OUT_BYTES)) != 0)
+    return;
+  Params p{};
+  p.A = reinterpret_cast<const uint16_t *>(A);
+  p.B = reinterpret_cast<const uint16_t *>(B);
+  p.C = C;
+  p.a_scale = A_scale;
+  p.b_scale = B_scale;
+  p.M = runtime_int(M);
+  p.N = runtime_int(N);
+  p.K = runtime_int(K / 4);  // 16-bit units
+  p.tiles_m = p.M / kTile;
+  p.tiles_n = p.N / kTile;
+  p.group_m = min(4, p.tiles_m);
+  p.ldc = CM ? p.M : p.N;
+  p.c_vec_ok = 1;
+  const int tiles = p.tiles_m * p.tiles_n;
+  const int ctas = gridDim.x * gridDim.y;
+  for (int raw = blockIdx.y * gridDim.x + blockIdx.x; raw < tiles; raw += ctas)
+    tiled_cta<kMXFP4, WAVE_ABI_OUT, CM, false, 8>(p, raw, dsmem);
 }
 #endif
 

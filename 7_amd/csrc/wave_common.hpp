@@ -74,6 +74,16 @@ __device__ __forceinline__ void dma16(uint32_t lds, const void *base,
                : "s"(lds), "v"(voff), "s"(base));
 }
 
+// The same with 4 bytes per lane: 64 lanes fill 256 bytes of LDS at
+// lds + 4 * lane.
+__device__ __forceinline__ void dma4(uint32_t lds, const void *base, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\t"
+               "s_nop 0\n\t"
+               "global_load_lds_dword %1, %2"
+               :
+               : "s"(lds), "v"(voff), "s"(base));
+}
+
 // Wait until this wave's outstanding vector-memory operations (including the
 // LDS DMA above) have completed, then join the workgroup barrier.  The asm
 // memory clobber also stops the compiler moving LDS accesses across it.

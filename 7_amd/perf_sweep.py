@@ -7,6 +7,8 @@ Kernel matrix (the reference's defaults, :32-42, :150-326, :876-877):
 * ``f16``         tiled GEMM, M = N = 4096, K in 512 .. 16384.
 * ``f16-streamk`` the same shapes through Stream-K, 256 workers.
 * ``bf16``        tiled GEMM with bf16 in/out (not in the reference).
+* ``mxfp4``       MXFP4 scaled GEMM, f16 column-major C, K in 1024 .. 32768
+                  (the reference's MXFP4_DOC_K_VALUES, :33, :189-197).
 * ``fa``          flash-attention forward, B2 H64 S8192 D128 bf16.
 
 Each run is one ``7_amd/wave-bench`` process with ``--check``; its
@@ -29,11 +31,13 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 BENCH = os.path.join(HERE, "wave-bench")
 
 F16_K_VALUES = (512, 1024, 2048, 3072, 4096, 8192, 16384)
+MXFP4_K_VALUES = (1024, 2048, 3072, 4096, 8192, 16384, 32768)
 FA_SHAPE = dict(batch=2, heads=64, sequence=8192, head_dim=128, xcds=8, waves=8)
 PROFILES = {
     "f16": "wave-mi355x-f16-256x256-4wave",
     "f16-streamk": "wave-mi355x-f16-256x256-4wave-streamk",
     "bf16": "wave-mi355x-bf16-256x256-4wave",
+    "mxfp4": "wave-mi355x-mxfp4-256x256-8wave",
     "fa": "wave-mi355x-fa-8wave-pingpong",
 }
 COLUMNS = ["kernel", "profile", "m", "n", "k", "variants", "iters", "warmup", "repeats", "us",
@@ -50,9 +54,15 @@ def runs(args):
             flops = 4 * s["batch"] * s["heads"] * s["sequence"] ** 2 * s["head_dim"]
             yield kernel, None, cmd, flops
             continue
-        for k in args.k:
+        ks = args.k
+        if kernel == "mxfp4" and not args.k_given:
+            ks = MXFP4_K_VALUES
+        for k in ks:
             cmd = [BENCH, "gemm", "--m", str(args.m), "--n", str(args.n), "--k", str(k),
                    "--input-mode", args.input_mode]
+            if kernel == "mxfp4":
+                cmd += ["--input-type", "mxfp4", "--c-type", "f16", "--output-layout",
+                        "column-major"]
             if kernel == "bf16":
                 cmd += ["--input-type", "bf16", "--c-type", "bf16"]
             if kernel == "f16-streamk":
@@ -74,8 +84,7 @@ def main(argv=None):
                     type=lambda s: [k for k in s.split(",") if k])
     ap.add_argument("--m", type=int, default=4096)
     ap.add_argument("--n", type=int, default=4096)
-    ap.add_argument("--k", default=",".join(map(str, F16_K_VALUES)),
-                    type=lambda s: [int(x) for x in s.split(",") if x])
+    ap.add_argument("--k", default=None, type=lambda s: [int(x) for x in s.split(",") if x])
     ap.add_argument("--input-mode", default="uniform")
     ap.add_argument("--streamk-workers", type=int, default=256)
     ap.add_argument("--iters", type=int, default=100)
@@ -85,6 +94,9 @@ def main(argv=None):
     ap.add_argument("--csv", default=None)
     ap.add_argument("--keep-going", action="store_true")
     args = ap.parse_args(argv)
+    args.k_given = args.k is not None
+    if args.k is None:
+        args.k = list(F16_K_VALUES)
     unknown = set(args.kernels) - set(PROFILES)
     if unknown:
         ap.error(f"unknown kernels {sorted(unknown)}; choose from {sorted(PROFILES)}")

@@ -17,7 +17,8 @@ workload on this host's cores.
 
 Secondary lines also run the same kernels on the input mode and shape of the
 reference's own published figures (rand_int GEMM inputs; the B2 H64 S8192
-bf16 attention profile) next to those figures, for comparison.
+bf16 attention profile; the 4096x4096x32768 MXFP4 profile) next to those
+figures, for comparison.
 """
 
 from __future__ import annotations
@@ -36,6 +37,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 MFMA_PEAK_TFLOPS = 2516.6   # MI355X dense f16/bf16: 256 CU x 2.4 GHz x 4096
+FP4_PEAK_TFLOPS = 10066.3  # MI355X dense fp4 MFMA: 256 CU x 2.4 GHz x 16384
 HBM_PEAK_GBS = 8000.0
 PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "gemm_f16_8192_traffic.txt")
 
@@ -276,6 +278,33 @@ def main():
                               "kernel": "flash_attention_bf16_gfx950 8-wave, qk_max_abs=1",
                               "source": "docs/PerfReferences/WaveGfx950FlashAttention.md:5-21"}})
         del q, k, v, o
+        # MXFP4 scaled GEMM at the reference's MXFP4 profile shape
+        # (4096 x 4096 x 32768, f16 column-major C): random e2m1 codes (every
+        # nibble uniform over the 16 codes) and e8m0 scales uniform over
+        # 124..127, the distribution of the runner's generator.
+        Mx, Nx, Kx = 4096, 4096, 32768
+        gx = torch.Generator(device=dev).manual_seed(13)
+        xa = torch.randint(0, 256, (Mx, Kx // 2), generator=gx, device=dev, dtype=torch.uint8)
+        xb = torch.randint(0, 256, (Nx, Kx // 2), generator=gx, device=dev, dtype=torch.uint8)
+        xsa = torch.randint(124, 128, (Kx // 32, Mx), generator=gx, device=dev,
+                            dtype=torch.uint8)
+        xsb = torch.randint(124, 128, (Kx // 32, Nx), generator=gx, device=dev,
+                            dtype=torch.uint8)
+        xc = torch.empty((Nx, Mx), dtype=torch.float16, device=dev)
+        m_ms = time_launches(lambda: wave.gemm_mxfp4(xa, xb, xsa, xsb, out_dtype=torch.float16,
+                                                     layout="col", out=xc), 20, 3, torch)
+        m_tf = 2.0 * Mx * Nx * Kx / (m_ms * 1e-3) / 1e12
+        log(f"gemm mxfp4 4096x4096x32768: {m_ms * 1e3:.1f} us/launch, {m_tf:.1f} TFLOP/s "
+            f"({100 * m_tf / FP4_PEAK_TFLOPS:.1f}% of {FP4_PEAK_TFLOPS})")
+        secondary.append({"workload": "gemm_mxfp4_4096x4096x32768_f16_col_random",
+                          "value": round(m_tf, 2), "unit": "TFLOP/s",
+                          "ms_per_step": round(m_ms, 4),
+                          "frac_of_fp4_peak": round(m_tf / FP4_PEAK_TFLOPS, 4),
+                          "reference_published": {
+                              "value": 4460.0, "unit": "TFLOP/s", "hardware": "gfx950",
+                              "kernel": "gfx950-mxfp4-256x256-8wave, random inputs",
+                              "source": "docs/Gfx950MatmulProfiles.md:57-68"}})
+        del xa, xb, xsa, xsb, xc
 
     cpu = None
     ref_cpu = None

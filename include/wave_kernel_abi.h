@@ -47,6 +47,31 @@ typedef struct {
   int32_t trip;
 } wave_abi_matmul_args;
 
+/* wmma_f16_matmul_tiled(const u8* A, const u8* B, C_t* C, const u8* A_scale,
+ *                       const u8* B_scale, int32 trip), the mxfp4 input type
+ * Replaces: the same kernel built with input_type="mxfp4"
+ *   (python/mlir/dialects/wave_matmul.py:6965-6975 argument list, :187-206
+ *   MFMA; runner wave-matmul-calibrate-runner.cpp:1792-1794 argument block).
+ * A [M][K/2], B [N][K/2] packed e2m1 (low nibble = even k); A_scale
+ * [K/32][M], B_scale [K/32][N] e8m0 (canonical layout); C as above.
+ * Built with: make hsaco NAME=mxfp4_<...> DEFS="-DWAVE_ABI_MXFP4 -DWAVE_ABI_M=..
+ *   -DWAVE_ABI_N=.. -DWAVE_ABI_K=.. -DWAVE_ABI_OUT=kF32|kF16|kBF16 -DWAVE_ABI_CM=0|1"
+ *   (M, N % 256 == 0, K % 128 == 0).
+ * Launch: any grid (grid-stride over the 256x256 tiles), block 512 (the
+ *   reference's 8-wave MXFP4 block), dynamic LDS >= 139264 bytes; A, B and
+ *   the scales 16-byte aligned.  `trip` is accepted and unused. */
+#define WAVE_ABI_MXFP4_SYMBOL "wmma_f16_matmul_tiled"
+#define WAVE_ABI_MXFP4_BLOCK 512
+#define WAVE_ABI_MXFP4_MIN_LDS 139264
+typedef struct {
+  const void *A;
+  const void *B;
+  void *C;
+  const void *A_scale;
+  const void *B_scale;
+  int32_t trip;
+} wave_abi_mxfp4_args;
+
 /* gfx950_f16_streamk_gemm(const f16* A, const f16* B, f16* C, f32* scratch,
  *                         u32* counters, int32 workers)
  * Replaces: python/mlir/dialects/wave_matmul.py:11556-11567, launched by

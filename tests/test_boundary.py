@@ -166,11 +166,14 @@ def test_product_does_not_import_oracle():
 
 # Reference kernel symbol -> kernarg bytes of its bare-pointer argument list
 # (pointers 8 bytes, int32 4 bytes, before the hidden arguments).
+# Keyed by code-object name prefix; the third field names the argument block
+# in include/wave_kernel_abi.h.
 ABI_SYMBOLS = {
-    "gemm_": ("wmma_f16_matmul_tiled", 3 * 8 + 4),
-    "streamk_": ("gfx950_f16_streamk_gemm", 5 * 8 + 4),
-    "fa_bf16_": ("flash_attention_bf16_gfx950", 4 * 8),
-    "fa32_": ("flash_attention_f32", 4 * 8),
+    "gemm_": ("wmma_f16_matmul_tiled", 3 * 8 + 4, "matmul"),
+    "mxfp4_": ("wmma_f16_matmul_tiled", 5 * 8 + 4, "mxfp4"),
+    "streamk_": ("gfx950_f16_streamk_gemm", 5 * 8 + 4, "streamk"),
+    "fa_bf16_": ("flash_attention_bf16_gfx950", 4 * 8, "fa"),
+    "fa32_": ("flash_attention_f32", 4 * 8, "fa32"),
 }
 
 
@@ -189,7 +192,7 @@ def test_code_objects_export_reference_symbols():
         pytest.skip("llvm-readelf not available")
     for path in objs:
         name = os.path.basename(path)
-        symbol, explicit = next(v for k, v in ABI_SYMBOLS.items() if name.startswith(k))
+        symbol, explicit, _ = next(v for k, v in ABI_SYMBOLS.items() if name.startswith(k))
         with open(path, "rb") as f:
             assert f.read(4) == b"\x7fELF", name
         notes = subprocess.run([readelf, "--notes", path], capture_output=True, text=True,
@@ -229,14 +232,16 @@ def test_kernel_abi_header_matches_code_objects(tmp_path):
         '#include <stddef.h>\n#include <stdio.h>\n#include "wave_kernel_abi.h"\n'
         "#define END(T, f) (unsigned)(offsetof(T, f) + sizeof(((T *)0)->f))\n"
         "int main(void) {\n"
-        '  printf("%s %u\\n", WAVE_ABI_MATMUL_SYMBOL, END(wave_abi_matmul_args, trip));\n'
-        '  printf("%s %u\\n", WAVE_ABI_STREAMK_SYMBOL, END(wave_abi_streamk_args, workers));\n'
-        '  printf("%s %u\\n", WAVE_ABI_FA_SYMBOL, END(wave_abi_fa_args, O));\n'
-        '  printf("%s %u\\n", WAVE_ABI_FA32_SYMBOL, END(wave_abi_fa32_args, O));\n'
+        '  printf("matmul %s %u\\n", WAVE_ABI_MATMUL_SYMBOL, END(wave_abi_matmul_args, trip));\n'
+        '  printf("mxfp4 %s %u\\n", WAVE_ABI_MXFP4_SYMBOL, END(wave_abi_mxfp4_args, trip));\n'
+        '  printf("streamk %s %u\\n", WAVE_ABI_STREAMK_SYMBOL, END(wave_abi_streamk_args, workers));\n'
+        '  printf("fa %s %u\\n", WAVE_ABI_FA_SYMBOL, END(wave_abi_fa_args, O));\n'
+        '  printf("fa32 %s %u\\n", WAVE_ABI_FA32_SYMBOL, END(wave_abi_fa32_args, O));\n'
         "  return 0;\n}\n")
     exe = tmp_path / "abi"
     subprocess.run([gcc, "-std=c99", "-Wall", "-Werror", "-I", os.path.join(root, "include"),
                     str(src), "-o", str(exe)], check=True)
-    out = dict(line.split() for line in subprocess.run(
-        [str(exe)], capture_output=True, text=True, check=True).stdout.splitlines())
-    assert {k: int(v) for k, v in out.items()} == {sym: end for sym, end in ABI_SYMBOLS.values()}
+    rows = [line.split() for line in subprocess.run(
+        [str(exe)], capture_output=True, text=True, check=True).stdout.splitlines()]
+    got = {block: (sym, int(end)) for block, sym, end in rows}
+    assert got == {block: (sym, end) for sym, end, block in ABI_SYMBOLS.values()}

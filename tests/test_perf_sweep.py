@@ -25,10 +25,15 @@ def test_parse_wave_bench_lines():
 
 def test_default_matrix_follows_reference_defaults():
     sweep = importlib.import_module("7_amd.perf_sweep")
-    ns = type("A", (), dict(kernels=["f16", "fa"], m=4096, n=4096, k=list(sweep.F16_K_VALUES),
+    ns = type("A", (), dict(kernels=["f16", "fa", "mxfp4"], m=4096, n=4096,
+                            k=list(sweep.F16_K_VALUES), k_given=False,
                             input_mode="uniform", streamk_workers=256))
     runs = list(sweep.runs(ns))
     gemm = [r for r in runs if r[0] == "f16"]
     assert [r[1][2] for r in gemm] == [512, 1024, 2048, 3072, 4096, 8192, 16384]
     fa = [r for r in runs if r[0] == "fa"][0]
     assert fa[3] == 4 * 2 * 64 * 8192 ** 2 * 128
+    # MXFP4 rows: the reference's MXFP4_DOC_K_VALUES (wave-matmul-perf-sweep.py:33)
+    mx = [r for r in runs if r[0] == "mxfp4"]
+    assert [r[1][2] for r in mx] == [1024, 2048, 3072, 4096, 8192, 16384, 32768]
+    assert "--input-type" in mx[0][2] and "mxfp4" in mx[0][2]

@@ -7,6 +7,9 @@ dynamic LDS and bare-pointer arguments), checked against the oracle.
   runner's tiling (wave-matmul-calibrate-runner.cpp:1114-1131, :1745-1762),
   block 256, dynamic LDS 131072 (the reference's gfx950 4-wave profile).
   Bucket inputs make every result bit-exact (wave_mfma_tiled.mlir:9).
+* wmma_f16_matmul_tiled(A, B, C, A_scale, B_scale, trip), mxfp4 input type
+  (runner.cpp:1792-1794): block 512, dynamic LDS 139264; the runner's
+  random codes and scales are exact at K = 512.
 * gfx950_f16_streamk_gemm(A, B, C, scratch, counters, workers): grid
   (workers), block 256; column-major C; counters back at zero afterwards
   (runner.cpp:1718-1742).
@@ -119,6 +122,60 @@ def test_tiled_too_little_lds_writes_nothing(co, oracle, dev):
                                                    dynamic_lds=GEMM_LDS - 1024)
         torch.cuda.synchronize()
     assert bool((C == 3.0).all())
+
+
+MXFP4_LDS = 139264
+
+
+def up8(x, dev):
+    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.uint8)).to(dev)
+
+
+@pytest.mark.parametrize("grid", [(1, 2), (2, 1), (1, 1), (8, 8)])
+def test_mxfp4_runner_launch(co, oracle, dev, grid):
+    """wmma_f16_matmul_tiled(A, B, C, A_scale, B_scale, trip), mxfp4 input
+    type (runner.cpp:1792-1794): block 512, the runner's random codes and
+    scales (exact at K = 512), any grid."""
+    M, N, K = 256, 512, 512
+    a, b, sa, sb = oracle.mxfp4_operands(M, N, K, 7)
+    C = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+    with co.CodeObject("mxfp4_f32_rm_256x512x512") as mod:
+        mod.kernel("wmma_f16_matmul_tiled").launch(
+            grid, (512,), [up8(a, dev), up8(b, dev), C, up8(sa, dev), up8(sb, dev), 3],
+            dynamic_lds=MXFP4_LDS)
+        torch.cuda.synchronize()
+    assert np.array_equal(C.cpu().numpy(), oracle.gemm_mxfp4(a, b, sa, sb))
+
+
+@pytest.mark.parametrize("block,lds", [(256, MXFP4_LDS), (512, MXFP4_LDS - 2048)])
+def test_mxfp4_outside_contract_writes_nothing(co, oracle, dev, block, lds):
+    a, b, sa, sb = oracle.mxfp4_operands(256, 512, 512, 7)
+    C = torch.full((256, 512), 3.0, dtype=torch.float32, device=dev)
+    with co.CodeObject("mxfp4_f32_rm_256x512x512") as mod:
+        mod.kernel("wmma_f16_matmul_tiled").launch(
+            (2, 1), (block,), [up8(a, dev), up8(b, dev), C, up8(sa, dev), up8(sb, dev), 0],
+            dynamic_lds=lds)
+        torch.cuda.synchronize()
+    assert bool((C == 3.0).all())
+
+
+def test_mxfp4_4096_matches_c_abi(co, wave, dev):
+    """The 4096x4096x8192 f16 column-major code object (the reference's MXFP4
+    profile layout) computes what wave_gemm_mxfp4_launch computes, bit for
+    bit."""
+    g = torch.Generator(device=dev).manual_seed(3)
+    M, N, K = 4096, 4096, 8192
+    A = torch.randint(0, 256, (M, K // 2), generator=g, device=dev, dtype=torch.uint8)
+    B = torch.randint(0, 256, (N, K // 2), generator=g, device=dev, dtype=torch.uint8)
+    SA = torch.randint(124, 128, (K // 32, M), generator=g, device=dev, dtype=torch.uint8)
+    SB = torch.randint(124, 128, (K // 32, N), generator=g, device=dev, dtype=torch.uint8)
+    C = torch.empty((N, M), dtype=torch.float16, device=dev)
+    with co.CodeObject("mxfp4_f16_cm_4096x4096x8192") as mod:
+        mod.kernel("wmma_f16_matmul_tiled").launch((256,), (512,), [A, B, C, SA, SB, 0],
+                                                   dynamic_lds=MXFP4_LDS)
+    ref = wave.gemm_mxfp4(A, B, SA, SB, out_dtype=torch.float16, layout="col")
+    torch.cuda.synchronize()
+    assert torch.equal(C, ref)
 
 
 @pytest.mark.parametrize("workers", [6, 7, 13, 64])
