@@ -512,68 +512,58 @@ __device__ __forceinline__ void store_tile(const Params &p, int m0, int n0,
   }
 }
 
-// Whole-tile store through LDS.  The MFMA layout leaves each lane 4
-// consecutive P values of one Q line, so a direct store instruction writes 8
-// or 16 bytes into each of 32 lines; here the tile is first transposed into
-// LDS lines (128 KiB: all 256 Q lines of 16-bit output, or 128 at a time of
-// f32) and then written as whole 512- or 1024-byte line runs, 16 bytes a
-// lane.  The 16-byte chunks of LDS line r sit at chunk ^ (r mod chunks), so
-// both the scattered writes and the line reads spread over all banks.
+// Whole-tile store of a 16-bit output through LDS.  The MFMA layout leaves
+// each lane 4 consecutive P values of one Q line, so a direct store
+// instruction writes 8 bytes into each of 32 lines; here the tile is first
+// transposed into 256 LDS lines of 512 bytes (128 KiB) and then written as
+// whole 512-byte line runs, 16 bytes a lane.  In LDS line r, 16-byte chunk c
+// sits at c ^ (r mod 32) and its two 8-byte halves are swapped when bit 4
+// of r is set: the 32 lanes of one scattered write (32 lines, one chunk
+// half each) then cover all 64 banks, and the line reads are contiguous.
 // Needs: the mainloop's LDS reads and DMA finished, a whole tile, C 16-byte
 // aligned and ldc * 2 a multiple of 16 bytes.
 template <class C, int OUT_DT, bool COL_MAJOR, typename Get>
 __device__ __forceinline__ void store_tile_lds(const Params &p, int m0, int n0, uint8_t *smem,
                                                Get get) {
-  constexpr int OB = OUT_DT == kF32 ? 4 : 2;
-  constexpr int LINE = 256 * OB;             // bytes of one 256-wide line
-  constexpr int CH = LINE / 16;              // 16-byte chunks per line
-  constexpr int ROWS = 131072 / LINE;        // lines per pass (256 or 128)
-  constexpr int PASSES = 256 / ROWS;
-  static_assert(C::SMEM >= 131072, "LDS ring smaller than one output pass");
+  static_assert(OUT_DT != kF32, "16-bit outputs only");
+  constexpr int LINE = 512, CH = 32;
+  static_assert(C::SMEM >= 256 * LINE, "LDS ring smaller than the output tile");
   const uint32_t tid = threadIdx.x;
   const uint32_t wave = tid >> 6, lane = tid & 63;
   const int wp = wave % C::WPN, wq = wave / C::WPN;
   const int P0 = COL_MAJOR ? m0 : n0, Q0 = COL_MAJOR ? n0 : m0;
-  const int wq0 = wq * (C::TQ * 32);
   char *out = reinterpret_cast<char *>(p.C);
 #pragma unroll
-  for (int pass = 0; pass < PASSES; ++pass) {
-    if (wq0 / ROWS == pass) {
+  for (int tq = 0; tq < C::TQ; ++tq) {
+    const uint32_t r = (uint32_t)(wq * (C::TQ * 32) + tq * 32) + (lane & 31);
+    const uint32_t half = ((lane >> 5) ^ (r >> 4)) & 1u;
 #pragma unroll
-      for (int tq = 0; tq < C::TQ; ++tq) {
-        const uint32_t r = (uint32_t)(wq0 % ROWS + tq * 32) + (lane & 31);
+    for (int tp = 0; tp < C::TP; ++tp) {
 #pragma unroll
-        for (int tp = 0; tp < C::TP; ++tp) {
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            // Element p = wp*TP*32 + tp*32 + 8g + 4*(lane/32) of line r.
-            const uint32_t e = wp * (C::TP * 32) + tp * 32 + 8 * g + 4 * (lane >> 5);
-            const uint32_t c = e * OB / 16, within = (e * OB) % 16;
-            uint8_t *dst = smem + r * LINE + ((c ^ (r % CH)) * 16) + within;
-            const f32x4 v = get(tp, tq, g);
-            if constexpr (OUT_DT == kF32)
-              *reinterpret_cast<f32x4 *>(dst) = v;
-            else
-              *reinterpret_cast<u32x2 *>(dst) =
-                  u32x2{pack2<OUT_DT>(v[0], v[1]), pack2<OUT_DT>(v[2], v[3])};
-          }
-        }
+      for (int g = 0; g < 4; ++g) {
+        // Elements wp*TP*32 + tp*32 + 8g + 4*(lane/32) .. +3 of line r.
+        const uint32_t c = wp * (C::TP * 4) + tp * 4 + g;
+        const f32x4 v = get(tp, tq, g);
+        *reinterpret_cast<u32x2 *>(smem + r * LINE + ((c ^ (r % CH)) * 16) + half * 8) =
+            u32x2{pack2<OUT_DT>(v[0], v[1]), pack2<OUT_DT>(v[2], v[3])};
       }
     }
-    lds_barrier();
-    constexpr int PER = ROWS * CH / C::THREADS;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const uint32_t flat = i * C::THREADS + tid;
-      const uint32_t r = flat / CH, c = flat % CH;
-      const u32x4 v = *reinterpret_cast<const u32x4 *>(smem + r * LINE + ((c ^ (r % CH)) * 16));
-      const size_t q = (size_t)(Q0 + pass * ROWS + (int)r);
-      *reinterpret_cast<u32x4 *>(out + (q * p.ldc + P0) * OB + c * 16) = v;
-    }
-    // Every wave's line reads are done before LDS is written again (next
-    // pass, or the next tile's DMA ring in a grid-stride caller).
-    lds_barrier();
   }
+  lds_barrier();
+  constexpr int PER = 256 * CH / C::THREADS;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const uint32_t flat = i * C::THREADS + tid;
+    const uint32_t r = flat / CH, c = flat % CH;
+    u32x4 v = *reinterpret_cast<const u32x4 *>(smem + r * LINE + ((c ^ (r % CH)) * 16));
+    if ((r >> 4) & 1u)
+      v = u32x4{v[2], v[3], v[0], v[1]};
+    const size_t q = (size_t)(Q0 + (int)r);
+    *reinterpret_cast<u32x4 *>(out + (q * p.ldc + P0) * 2 + c * 16) = v;
+  }
+  // Every wave's line reads are done before LDS is written again (the next
+  // tile's DMA ring in a grid-stride caller).
+  lds_barrier();
 }
 
 // One 256x256 output tile: CTA `raw` of a grid of tiles_m * tiles_n CTAs.
@@ -605,10 +595,13 @@ __device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *sme
   };
   // 16-bit output goes through LDS; f32 output, twice the bytes, is bound by
   // HBM writes either way and is stored directly (measured faster).
-  if (!MASKED && OUT_DT != kF32 && (((uintptr_t)p.C | (uintptr_t)p.ldc * 2) & 15) == 0)
-    store_tile_lds<C, OUT_DT, COL_MAJOR>(p, m0, n0, smem, get);
-  else
-    store_tile<C, OUT_DT, COL_MAJOR, MASKED>(p, m0, n0, get);
+  if constexpr (!MASKED && OUT_DT != kF32) {
+    if ((((uintptr_t)p.C | (uintptr_t)p.ldc * 2) & 15) == 0) {
+      store_tile_lds<C, OUT_DT, COL_MAJOR>(p, m0, n0, smem, get);
+      return;
+    }
+  }
+  store_tile<C, OUT_DT, COL_MAJOR, MASKED>(p, m0, n0, get);
 }
 
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>

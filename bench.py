@@ -148,6 +148,33 @@ def rand_int_operand(rows, k, stream, torch):
     return torch.from_numpy(v.reshape(rows, k)).to(torch.float16)
 
 
+def mxfp4_line(wave, torch, dev, steps, warmup):
+    """MXFP4 scaled GEMM at the reference's MXFP4 profile shape (4096 x 4096
+    x 32768, f16 column-major C): random e2m1 codes (every nibble uniform
+    over the 16 codes) and e8m0 scales uniform over 124..127, the
+    distribution of the runner's generator (runner.cpp:1135-1150,
+    :1208-1220)."""
+    Mx, Nx, Kx = 4096, 4096, 32768
+    gx = torch.Generator(device=dev).manual_seed(13)
+    xa = torch.randint(0, 256, (Mx, Kx // 2), generator=gx, device=dev, dtype=torch.uint8)
+    xb = torch.randint(0, 256, (Nx, Kx // 2), generator=gx, device=dev, dtype=torch.uint8)
+    xsa = torch.randint(124, 128, (Kx // 32, Mx), generator=gx, device=dev, dtype=torch.uint8)
+    xsb = torch.randint(124, 128, (Kx // 32, Nx), generator=gx, device=dev, dtype=torch.uint8)
+    xc = torch.empty((Nx, Mx), dtype=torch.float16, device=dev)
+    m_ms = time_launches(lambda: wave.gemm_mxfp4(xa, xb, xsa, xsb, out_dtype=torch.float16,
+                                                 layout="col", out=xc), steps, warmup, torch)
+    m_tf = 2.0 * Mx * Nx * Kx / (m_ms * 1e-3) / 1e12
+    log(f"gemm mxfp4 4096x4096x32768: {m_ms * 1e3:.1f} us/launch, {m_tf:.1f} TFLOP/s "
+        f"({100 * m_tf / FP4_PEAK_TFLOPS:.1f}% of {FP4_PEAK_TFLOPS})")
+    return {"workload": "gemm_mxfp4_4096x4096x32768_f16_col_random",
+            "value": round(m_tf, 2), "unit": "TFLOP/s", "ms_per_step": round(m_ms, 4),
+            "frac_of_fp4_peak": round(m_tf / FP4_PEAK_TFLOPS, 4),
+            "reference_published": {
+                "value": 4460.0, "unit": "TFLOP/s", "hardware": "gfx950",
+                "kernel": "gfx950-mxfp4-256x256-8wave, random inputs",
+                "source": "docs/Gfx950MatmulProfiles.md:57-68"}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -158,8 +185,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-ref-compare", action="store_true",
                     help="skip the runs on the reference's published input modes / shapes")
-    ap.add_argument("--workload", choices=["all", "gemm", "fa", "copy"], default="all",
-                    help="gemm / fa: run only that kernel (for profiler passes); copy: "
+    ap.add_argument("--workload", choices=["all", "gemm", "fa", "mxfp4", "copy"], default="all",
+                    help="gemm / fa / mxfp4: run only that kernel (for profiler passes); copy: "
                          "a 1 GiB device copy used to calibrate rocprofv3 byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -181,8 +208,12 @@ def main():
         ms = time_launches(lambda: dst.copy_(src), args.steps, args.warmup, torch)
         log(f"copy 1 GiB: {ms:.3f} ms, {2 * 4 * src.numel() / (ms * 1e-3) / 1e9:.0f} GB/s")
         return
-    if args.workload == "fa":
+    if args.workload in ("fa", "mxfp4"):
         args.no_cpu = True
+    if args.workload == "mxfp4":
+        m = mxfp4_line(wave, torch, dev, args.steps, args.warmup)
+        print(json.dumps(m), flush=True)
+        return
 
     M = N = K = 8192
     g = torch.Generator(device="cpu").manual_seed(7)
@@ -278,33 +309,7 @@ def main():
                               "kernel": "flash_attention_bf16_gfx950 8-wave, qk_max_abs=1",
                               "source": "docs/PerfReferences/WaveGfx950FlashAttention.md:5-21"}})
         del q, k, v, o
-        # MXFP4 scaled GEMM at the reference's MXFP4 profile shape
-        # (4096 x 4096 x 32768, f16 column-major C): random e2m1 codes (every
-        # nibble uniform over the 16 codes) and e8m0 scales uniform over
-        # 124..127, the distribution of the runner's generator.
-        Mx, Nx, Kx = 4096, 4096, 32768
-        gx = torch.Generator(device=dev).manual_seed(13)
-        xa = torch.randint(0, 256, (Mx, Kx // 2), generator=gx, device=dev, dtype=torch.uint8)
-        xb = torch.randint(0, 256, (Nx, Kx // 2), generator=gx, device=dev, dtype=torch.uint8)
-        xsa = torch.randint(124, 128, (Kx // 32, Mx), generator=gx, device=dev,
-                            dtype=torch.uint8)
-        xsb = torch.randint(124, 128, (Kx // 32, Nx), generator=gx, device=dev,
-                            dtype=torch.uint8)
-        xc = torch.empty((Nx, Mx), dtype=torch.float16, device=dev)
-        m_ms = time_launches(lambda: wave.gemm_mxfp4(xa, xb, xsa, xsb, out_dtype=torch.float16,
-                                                     layout="col", out=xc), 20, 3, torch)
-        m_tf = 2.0 * Mx * Nx * Kx / (m_ms * 1e-3) / 1e12
-        log(f"gemm mxfp4 4096x4096x32768: {m_ms * 1e3:.1f} us/launch, {m_tf:.1f} TFLOP/s "
-            f"({100 * m_tf / FP4_PEAK_TFLOPS:.1f}% of {FP4_PEAK_TFLOPS})")
-        secondary.append({"workload": "gemm_mxfp4_4096x4096x32768_f16_col_random",
-                          "value": round(m_tf, 2), "unit": "TFLOP/s",
-                          "ms_per_step": round(m_ms, 4),
-                          "frac_of_fp4_peak": round(m_tf / FP4_PEAK_TFLOPS, 4),
-                          "reference_published": {
-                              "value": 4460.0, "unit": "TFLOP/s", "hardware": "gfx950",
-                              "kernel": "gfx950-mxfp4-256x256-8wave, random inputs",
-                              "source": "docs/Gfx950MatmulProfiles.md:57-68"}})
-        del xa, xb, xsa, xsb, xc
+        secondary.append(mxfp4_line(wave, torch, dev, 20, 3))
 
     cpu = None
     ref_cpu = None
