@@ -1,5 +1,7 @@
 // attention_fwd.hip -- instantiation and host launch of the gfx950
-// flash-attention forward kernel (attention_kernels.hpp).
+// flash-attention forward kernels: the 8-wave ping-pong kernel
+// (attention_kernels.hpp) and the 4-wave kernel (attention_fwd4.hpp).
+#include "attention_fwd4.hpp"
 #include "attention_kernels.hpp"
 
 #include <cmath>
@@ -25,9 +27,25 @@ hipError_t launch_fwd(const FwdArgs &a, hipStream_t stream) {
   // Fixed-max mode: |s * scale| <= head_dim * qk_max_abs^2 * scale, in log2
   // units (wave_flash_attention.py:108-113 with scale = 1/sqrt(128)).
   p.fixed_max = (float)((double)kLog2e * scale * a.head_dim * a.qk_max_abs * a.qk_max_abs);
+  const bool fixed = a.qk_max_abs > 0.f;
+  if (a.waves == kF4Waves) {
+    // 4 waves x 64 query rows per CTA (the same 256-row blocks).
+    const dim3 grid(p.q_blocks * a.batch * a.q_heads), block(64 * kF4Waves);
+    if (a.dtype == kF16) {
+      if (fixed)
+        hipLaunchKernelGGL((fwd4_kernel<kF16, true>), grid, block, 0, stream, p);
+      else
+        hipLaunchKernelGGL((fwd4_kernel<kF16, false>), grid, block, 0, stream, p);
+    } else {
+      if (fixed)
+        hipLaunchKernelGGL((fwd4_kernel<kBF16, true>), grid, block, 0, stream, p);
+      else
+        hipLaunchKernelGGL((fwd4_kernel<kBF16, false>), grid, block, 0, stream, p);
+    }
+    return hipGetLastError();
+  }
   // 8 waves x 32 query rows per CTA, two ping-pong groups of 4 waves.
   const dim3 grid(p.q_blocks * a.batch * a.q_heads), block(64 * kPPWaves);
-  const bool fixed = a.qk_max_abs > 0.f;
   if (a.dtype == kF16) {
     if (fixed)
       hipLaunchKernelGGL((fwd_pp_kernel<kF16, true>), grid, block, 0, stream, p);

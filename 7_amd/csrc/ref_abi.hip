@@ -26,6 +26,7 @@
 //     (wave_flash_attention.py:1723-1728; runner wave-fa-gfx950-runner.cpp
 //     :396-402).  -DWAVE_ABI_FA -DWAVE_ABI_FA_B= -DWAVE_ABI_FA_H= -DWAVE_ABI_FA_S=
 //     [-DWAVE_ABI_FA_QK_MAX_ABS=b: the fixed-max profile for |Q|, |K| <= b]
+//     [-DWAVE_ABI_FA_WAVES=4: the reference's 4-wave configuration]
 //   flash_attention_f32(const f16* Q, const f16* K, const f16* V, f32* O)
 //     (wave_attention.py:1436-1441; runner wave-fa-calibrate-runner.cpp
 //     :346-361).  -DWAVE_ABI_FA32 -DWAVE_ABI_FA32_M= _N= _D=
@@ -43,7 +44,9 @@
 //  * gfx950_f16_streamk_gemm: grid (workers), block 256, >= 131076 bytes of
 //    dynamic LDS; workspace as wave_gemm_streamk_workspace_bytes.
 //  * flash_attention_bf16_gfx950: grid (S/256, B*H), block 512, >= 102400
-//    bytes of dynamic LDS (the reference's 8-wave profile passes 136192).
+//    bytes of dynamic LDS (the reference's 8-wave profile passes 136192);
+//    built with WAVE_ABI_FA_WAVES=4: block 256, >= 45056 bytes (the
+//    runner's 4-wave default --threads 256 --dynamic-lds 68096).
 //    Non-causal, one KV head per query head, scale 1/sqrt(128).
 //  * flash_attention_f32: grid (1,1,1), any block size up to 1024; LDS is
 //    static.
@@ -51,8 +54,9 @@
 // less dynamic LDS than stated, returns without writing anything; so does a
 // GEMM launch whose A/B (16 bytes) or C (4 elements) lack the alignment its
 // load path needs (hipMalloc'd buffers always have it).  The FA runner's
-// default --dynamic-lds (68096, its 4-wave setting) is too small for this
-// 8-wave kernel: pass --threads 512 --dynamic-lds 136192.
+// default (--threads 256 --dynamic-lds 68096, its 4-wave setting) takes the
+// 4-wave code objects; the 8-wave ones need --threads 512 --dynamic-lds 136192.
+#include "attention_fwd4.hpp"
 #include "attention_kernels.hpp"
 #include "fa_small.hpp"
 #include "gemm_kernels.hpp"
@@ -200,15 +204,23 @@ extern "C" __global__ __launch_bounds__(256, 1) void gfx950_f16_streamk_gemm(
 #endif
 
 #ifdef WAVE_ABI_FA
-extern "C" __global__ __launch_bounds__(512, 1) void flash_attention_bf16_gfx950(
+#ifndef WAVE_ABI_FA_WAVES
+#define WAVE_ABI_FA_WAVES 8
+#endif
+static_assert(WAVE_ABI_FA_WAVES == 4 || WAVE_ABI_FA_WAVES == 8, "waves must be 4 or 8");
+// The 4-wave kernel is built for two CTAs per CU (64 KiB of LDS each).
+extern "C" __global__ __launch_bounds__(64 * WAVE_ABI_FA_WAVES, WAVE_ABI_FA_WAVES == 4 ? 2 : 1)
+void flash_attention_bf16_gfx950(
     const uint16_t *Q, const uint16_t *K, const uint16_t *V, uint16_t *O) {
   using namespace wave::attention;
   extern __shared__ __attribute__((aligned(1024))) uint8_t dsmem[];
   constexpr int B = WAVE_ABI_FA_B, H = WAVE_ABI_FA_H, S = WAVE_ABI_FA_S;
   static_assert(B > 0 && H > 0 && S > 0, "shape");
-  constexpr int kQBlocks = (S + 32 * kPPWaves - 1) / (32 * kPPWaves);
-  if (blockDim.x != 64 * kPPWaves || blockDim.y != 1 || blockDim.z != 1 ||
-      (int)(gridDim.x * gridDim.y) != kQBlocks * B * H || dynamic_lds_bytes() < (uint32_t)kPPSmem)
+  // Both wave counts take 256 query rows per CTA (wave_flash_attention.py:23, :93).
+  constexpr int kQBlocks = (S + 255) / 256;
+  constexpr int kSmem = WAVE_ABI_FA_WAVES == 4 ? kF4Smem : kPPSmem;
+  if (blockDim.x != 64 * WAVE_ABI_FA_WAVES || blockDim.y != 1 || blockDim.z != 1 ||
+      (int)(gridDim.x * gridDim.y) != kQBlocks * B * H || dynamic_lds_bytes() < (uint32_t)kSmem)
     return;
   Params p{};
   p.Q = Q;
@@ -231,10 +243,15 @@ extern "C" __global__ __launch_bounds__(512, 1) void flash_attention_bf16_gfx950
   static_assert(kB > 0 && -2.0 * 1.4426950408889634 * 11.313708498984761 * kB * kB >= -126.0,
                 "qk_max_abs outside the bf16 range");
   p.fixed_max = (float)(1.4426950408889634 * (1.0 / 11.313708498984761) * 128.0 * kB * kB);
-  fwd_pp_cta<kBF16, true>(p, blockIdx.y * gridDim.x + blockIdx.x, dsmem);
+  constexpr bool kFixed = true;
 #else
-  fwd_pp_cta<kBF16>(p, blockIdx.y * gridDim.x + blockIdx.x, dsmem);
+  constexpr bool kFixed = false;
 #endif
+  const int raw = blockIdx.y * gridDim.x + blockIdx.x;
+  if constexpr (WAVE_ABI_FA_WAVES == 4)
+    fwd4_cta<kBF16, kFixed>(p, raw, dsmem);
+  else
+    fwd_pp_cta<kBF16, kFixed>(p, raw, dsmem);
 }
 #endif
 

@@ -239,9 +239,27 @@ int wave_gemm_streamk_counters_check(const uint32_t *counters, int M, int N,
 
 namespace {
 // Shared by the adaptive (qk_max_abs == 0) and fixed-max entry points.
+// wave_flash_attention.py:63-75: qk_max_abs finite and positive, and the
+// smallest probability 2^(-2 * bound) a normal number of the P type.
+int check_qk_bound(float qk_max_abs, float scale, int head_dim, int dtype) {
+  if (!(qk_max_abs > 0.f) || !std::isfinite(qk_max_abs))
+    return fail(WAVE_ERR_INVALID, "fa: qk_max_abs must be finite and positive");
+  const double s = scale > 0.f ? (double)scale : 1.0 / std::sqrt((double)head_dim);
+  const double bound = 1.4426950408889634 * s * head_dim * (double)qk_max_abs * qk_max_abs;
+  const double min_normal_log2 = dtype == WAVE_F16 ? -14.0 : -126.0;
+  if (-2.0 * bound < min_normal_log2)
+    return fail(WAVE_ERR_INVALID,
+                "fa: qk_max_abs=%g fixed reference %.3g exceeds the %s range; use "
+                "wave_fa_fwd_launch", (double)qk_max_abs, bound,
+                dtype == WAVE_F16 ? "f16" : "bf16");
+  return WAVE_OK;
+}
+
 int fa_fwd(const void *Q, const void *K, const void *V, void *O, int batch, int q_heads,
            int kv_heads, int seq, int head_dim, int dtype, int causal, float scale,
-           float qk_max_abs, void *stream, const char *name) {
+           float qk_max_abs, int waves, void *stream, const char *name) {
+  if (waves != 4 && waves != 8)
+    return fail(WAVE_ERR_INVALID, "fa: waves=%d must be 4 or 8", waves);
   if (!Q || !K || !V || !O)
     return fail(WAVE_ERR_INVALID, "fa: null Q, K, V or O");
   if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || seq <= 0)
@@ -279,6 +297,7 @@ int fa_fwd(const void *Q, const void *K, const void *V, void *O, int batch, int 
   a.causal = causal;
   a.scale = scale;
   a.qk_max_abs = qk_max_abs;
+  a.waves = waves;
   return hip_status(wave::attention::launch_fwd(a, static_cast<hipStream_t>(stream)), name);
 }
 } // namespace
@@ -288,27 +307,31 @@ int wave_fa_fwd_launch(const void *Q, const void *K, const void *V, void *O,
                        int head_dim, int dtype, int causal, float scale,
                        void *stream) {
   return fa_fwd(Q, K, V, O, batch, q_heads, kv_heads, seq, head_dim, dtype, causal, scale, 0.f,
-                stream, "wave_fa_fwd_launch");
+                8, stream, "wave_fa_fwd_launch");
 }
 
 int wave_fa_fwd_bounded_launch(const void *Q, const void *K, const void *V, void *O,
                                int batch, int q_heads, int kv_heads, int seq,
                                int head_dim, int dtype, int causal, float scale,
                                float qk_max_abs, void *stream) {
-  // wave_flash_attention.py:63-75: finite and positive, and the smallest
-  // probability 2^(-2 * bound) must stay a normal number of the P type.
-  if (!(qk_max_abs > 0.f) || !std::isfinite(qk_max_abs))
-    return fail(WAVE_ERR_INVALID, "fa: qk_max_abs must be finite and positive");
-  const double s = scale > 0.f ? (double)scale : 1.0 / std::sqrt((double)head_dim);
-  const double bound = 1.4426950408889634 * s * head_dim * (double)qk_max_abs * qk_max_abs;
-  const double min_normal_log2 = dtype == WAVE_F16 ? -14.0 : -126.0;
-  if (-2.0 * bound < min_normal_log2)
-    return fail(WAVE_ERR_INVALID,
-                "fa: qk_max_abs=%g fixed reference %.3g exceeds the %s range; use "
-                "wave_fa_fwd_launch", (double)qk_max_abs, bound,
-                dtype == WAVE_F16 ? "f16" : "bf16");
+  const int st = check_qk_bound(qk_max_abs, scale, head_dim, dtype);
+  if (st != WAVE_OK)
+    return st;
   return fa_fwd(Q, K, V, O, batch, q_heads, kv_heads, seq, head_dim, dtype, causal, scale,
-                qk_max_abs, stream, "wave_fa_fwd_bounded_launch");
+                qk_max_abs, 8, stream, "wave_fa_fwd_bounded_launch");
+}
+
+int wave_fa_fwd_config_launch(const void *Q, const void *K, const void *V, void *O,
+                              int batch, int q_heads, int kv_heads, int seq, int head_dim,
+                              int dtype, int causal, float scale, float qk_max_abs, int waves,
+                              void *stream) {
+  if (qk_max_abs != 0.f) {
+    const int st = check_qk_bound(qk_max_abs, scale, head_dim, dtype);
+    if (st != WAVE_OK)
+      return st;
+  }
+  return fa_fwd(Q, K, V, O, batch, q_heads, kv_heads, seq, head_dim, dtype, causal, scale,
+                qk_max_abs, waves, stream, "wave_fa_fwd_config_launch");
 }
 
 int wave_fa_f32_launch(const void *Q, const void *K, const void *V, float *O,

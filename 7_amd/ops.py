@@ -150,12 +150,14 @@ def gemm_streamk(a: torch.Tensor, b: torch.Tensor, workers: int, *,
 
 def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
                     causal: bool = False, scale: float | None = None,
-                    qk_max_abs: float | None = None,
+                    qk_max_abs: float | None = None, waves: int = 8,
                     out: torch.Tensor | None = None) -> torch.Tensor:
     """softmax(Q K^T * scale) V for q [B, Hq, S, D], k/v [B, Hkv, S, D].
 
     qk_max_abs: the caller's bound on |Q| and |K|; selects the fixed-max
-    kernel (no online max; wave_fa_fwd_bounded_launch)."""
+    kernel (no online max; wave_fa_fwd_bounded_launch).  waves: 8 (the
+    ping-pong kernel) or 4 (the reference's 4-wave configuration;
+    wave_fa_fwd_config_launch)."""
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
         _need(t, n)
         if t.dim() != 4:
@@ -171,7 +173,11 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     _need(out, "out")
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, Hq, Hkv, S, D,
             _DT[q.dtype], int(causal), float(scale or 0.0))
-    if qk_max_abs is None:
+    if waves != 8:
+        rt.check(rt.lib().wave_fa_fwd_config_launch(
+            *args, 0.0 if qk_max_abs is None else float(qk_max_abs), int(waves),
+            _stream(q)))
+    elif qk_max_abs is None:
         rt.check(rt.lib().wave_fa_fwd_launch(*args, _stream(q)))
     else:
         rt.check(rt.lib().wave_fa_fwd_bounded_launch(*args, float(qk_max_abs), _stream(q)))

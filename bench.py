@@ -308,6 +308,21 @@ def main():
                               "value": 1111.1, "unit": "TFLOP/s", "hardware": "MI350X",
                               "kernel": "flash_attention_bf16_gfx950 8-wave, qk_max_abs=1",
                               "source": "docs/PerfReferences/WaveGfx950FlashAttention.md:5-21"}})
+        # The reference's 4-wave configuration (block 256) on the same shape.
+        q = torch.randn((B, H, S, D), generator=gq).to(torch.bfloat16).to(dev)
+        k = torch.randn((B, H, S, D), generator=gq).to(torch.bfloat16).to(dev)
+        w_ms = time_launches(lambda: wave.flash_attention(q, k, v, waves=4, out=o), 10, 2, torch)
+        w_tf = 4.0 * B * H * S * S * D / (w_ms * 1e-3) / 1e12
+        log(f"fa fwd bf16 B2 H64 S8192 D128 4-wave: {w_ms * 1e3:.1f} us/launch, {w_tf:.1f} TFLOP/s")
+        secondary.append({"workload": "fa_fwd_bf16_b2_h64_s8192_d128_noncausal_4wave",
+                          "value": round(w_tf, 2), "unit": "TFLOP/s",
+                          "ms_per_step": round(w_ms, 4),
+                          "frac_of_mfma_peak": round(w_tf / MFMA_PEAK_TFLOPS, 4),
+                          "reference_published": {
+                              "value": 984.0, "unit": "TFLOP/s", "hardware": "gfx950",
+                              "kernel": "four-wave BM=128 branch experiment (upper end of "
+                                        "978-984)",
+                              "source": "docs/PerfReferences/WaveGfx950FlashAttention.md:67"}})
         del q, k, v, o
         secondary.append(mxfp4_line(wave, torch, dev, 20, 3))
 

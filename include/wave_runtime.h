@@ -141,6 +141,19 @@ int wave_fa_fwd_bounded_launch(const void *Q, const void *K, const void *V, void
                                int head_dim, int dtype, int causal, float scale,
                                float qk_max_abs, void *stream);
 
+/* Both knobs of the reference's Gfx950FlashAttentionConfig
+ * (wave_flash_attention.py:44-93, :114-135) in one call: waves = 8 runs the
+ * kernel of wave_fa_fwd_launch; waves = 4 runs the reference's 4-wave
+ * configuration (256 threads, 64 query rows per wave, the same 256-row
+ * blocks and grid).  qk_max_abs = 0 selects the online softmax; > 0 the
+ * fixed-max mode, validated as in wave_fa_fwd_bounded_launch.  Other
+ * arguments as wave_fa_fwd_launch.  Returns WAVE_ERR_INVALID for waves
+ * other than 4 or 8. */
+int wave_fa_fwd_config_launch(const void *Q, const void *K, const void *V, void *O,
+                              int batch, int q_heads, int kv_heads, int seq,
+                              int head_dim, int dtype, int causal, float scale,
+                              float qk_max_abs, int waves, void *stream);
+
 /* ---- flash_attention_f32 ------------------------------------------------
  * Replaces `flash_attention_f32(Q, K, V, O)` (wave_attention.py:1406-1441;
  * wave-fa-calibrate-runner.cpp:346-361): Q [block_m][head_dim] f16

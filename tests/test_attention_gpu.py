@@ -9,6 +9,9 @@
   large ones (runner :204-232), and --zero-qk (every row = mean of V).
 * wave_fa_f32_launch vs oracle.fa_f32_reference at the runner tolerance
   3e-3 (wave-fa-calibrate-runner.cpp:251-273).
+* Every forward case runs on both kernels: waves=8 (wave_fa_fwd_launch) and
+  the reference's 4-wave configuration (wave_fa_fwd_config_launch, waves=4;
+  wave_flash_attention.py:44-93).
 """
 
 import math
@@ -25,13 +28,16 @@ TOL = 2e-2
 TDT = {1: torch.float16, 2: torch.bfloat16}
 
 
-def run_fa(wave, oracle, dev, q, k, v, dt, B, Hq, Hkv, S, causal, heads, rows):
+WAVES = pytest.mark.parametrize("waves", [8, 4])
+
+
+def run_fa(wave, oracle, dev, q, k, v, dt, B, Hq, Hkv, S, causal, heads, rows, waves=8):
     """q, k, v: uint16 bit arrays [B*H*S*D]; checks (head, row) pairs."""
     D = 128
     qt = to_dev(q, TDT[dt], dev).view(B, Hq, S, D)
     kt = to_dev(k, TDT[dt], dev).view(B, Hkv, S, D)
     vt = to_dev(v, TDT[dt], dev).view(B, Hkv, S, D)
-    o = wave.flash_attention(qt, kt, vt, causal=causal)
+    o = wave.flash_attention(qt, kt, vt, causal=causal, waves=waves)
     torch.cuda.synchronize()
     got = oracle.bits_to_f32(to_bits(o).reshape(B * Hq, S, D), dt)
     hh, rr = np.meshgrid(np.asarray(heads), np.asarray(rows), indexing="ij")
@@ -50,14 +56,15 @@ def normal_bits(n, dt, seed):
     return t.view(torch.int16).numpy().view(np.uint16)
 
 
+@WAVES
 @pytest.mark.parametrize("seq", [256, 512])
 @pytest.mark.parametrize("iscale", [1, 4])
-def test_reference_inputs_all_rows(wave, oracle, dev, seq, iscale):
+def test_reference_inputs_all_rows(wave, oracle, dev, seq, iscale, waves):
     """wave_flash_attention_gfx950_runtime.mlir:3-38: B1 H1 S256, adaptive
     input scale 4; bf16 bucket inputs, every row checked."""
     n = seq * 128
     q, k, v = oracle.fa_gfx950_inputs(n, 0, iscale)
-    err = run_fa(wave, oracle, dev, q, k, v, 2, 1, 1, 1, seq, False, [0], range(seq))
+    err = run_fa(wave, oracle, dev, q, k, v, 2, 1, 1, 1, seq, False, [0], range(seq), waves)
     assert err <= TOL, err
 
 
@@ -72,31 +79,35 @@ def test_zero_qk_rows_are_mean_v(wave, oracle, dev):
     assert float((o - mean).abs().max()) <= 1e-2
 
 
+@WAVES
 @pytest.mark.parametrize("dt", [1, 2])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("B,Hq,Hkv,S", [(1, 2, 2, 128), (2, 4, 2, 320), (1, 8, 1, 200),
                                         (1, 1, 1, 64), (1, 2, 1, 1000), (1, 1, 1, 7)])
-def test_small_problems_all_rows(wave, oracle, dev, dt, causal, B, Hq, Hkv, S):
+def test_small_problems_all_rows(wave, oracle, dev, dt, causal, B, Hq, Hkv, S, waves):
     q = normal_bits(B * Hq * S * 128, dt, 1)
     k = normal_bits(B * Hkv * S * 128, dt, 2)
     v = normal_bits(B * Hkv * S * 128, dt, 3)
     err = run_fa(wave, oracle, dev, q, k, v, dt, B, Hq, Hkv, S, causal,
-                 range(B * Hq), range(S))
+                 range(B * Hq), range(S), waves)
     assert err <= TOL, err
 
 
-def test_config4_f16_b4_h32_s4096(wave, oracle, dev):
+@WAVES
+def test_config4_f16_b4_h32_s4096(wave, oracle, dev, waves):
     """non-causal f16, N(0,1), sampled heads and rows."""
     B, H, S = 4, 32, 4096
     n = B * H * S * 128
     q, k, v = (normal_bits(n, 1, s) for s in (11, 12, 13))
     heads = oracle.fa_reference_heads(B * H)
     rows = oracle.fa_reference_rows(S) + [1, 255, 256, 1000, 4000]
-    err = run_fa(wave, oracle, dev, q, k, v, 1, B, H, H, S, False, heads, sorted(set(rows)))
+    err = run_fa(wave, oracle, dev, q, k, v, 1, B, H, H, S, False, heads, sorted(set(rows)),
+                 waves)
     assert err <= TOL, err
 
 
-def test_config5_causal_gqa_bf16_s8192(wave, oracle, dev):
+@WAVES
+def test_config5_causal_gqa_bf16_s8192(wave, oracle, dev, waves):
     """causal, 64 query heads over 8 KV heads, S=8192."""
     B, Hq, Hkv, S = 1, 64, 8, 8192
     q = normal_bits(B * Hq * S * 128, 2, 21)
@@ -104,7 +115,7 @@ def test_config5_causal_gqa_bf16_s8192(wave, oracle, dev):
     v = normal_bits(B * Hkv * S * 128, 2, 23)
     heads = [0, 7, 8, 31, 63]
     rows = sorted(set(oracle.fa_reference_rows(S) + [1, 63, 64, 4097, 8191]))
-    err = run_fa(wave, oracle, dev, q, k, v, 2, B, Hq, Hkv, S, True, heads, rows)
+    err = run_fa(wave, oracle, dev, q, k, v, 2, B, Hq, Hkv, S, True, heads, rows, waves)
     assert err <= TOL, err
 
 
@@ -138,10 +149,11 @@ def uniform_bits(n, dt, seed, bound):
     return t.view(torch.int16).numpy().view(np.uint16)
 
 
+@WAVES
 @pytest.mark.parametrize("dt,bound", [(2, 1.0), (1, 0.5)])
 @pytest.mark.parametrize("B,Hq,Hkv,S,causal", [(1, 2, 2, 512, False), (2, 4, 2, 300, True),
                                                (1, 1, 1, 64, False)])
-def test_fixed_max_mode(wave, oracle, dev, dt, bound, B, Hq, Hkv, S, causal):
+def test_fixed_max_mode(wave, oracle, dev, dt, bound, B, Hq, Hkv, S, causal, waves):
     """qk_max_abs mode (wave_flash_attention.py:63-75, :108-113): inputs
     within the declared bound, every row against the double-precision
     softmax at 2e-2."""
@@ -152,7 +164,7 @@ def test_fixed_max_mode(wave, oracle, dev, dt, bound, B, Hq, Hkv, S, causal):
     qt = to_dev(q, TDT[dt], dev).view(B, Hq, S, D)
     kt = to_dev(k, TDT[dt], dev).view(B, Hkv, S, D)
     vt = to_dev(v, TDT[dt], dev).view(B, Hkv, S, D)
-    o = wave.flash_attention(qt, kt, vt, causal=causal, qk_max_abs=bound)
+    o = wave.flash_attention(qt, kt, vt, causal=causal, qk_max_abs=bound, waves=waves)
     torch.cuda.synchronize()
     got = oracle.bits_to_f32(to_bits(o).reshape(B * Hq, S, D), dt)
     hh, rr = np.meshgrid(np.arange(B * Hq), np.arange(S), indexing="ij")
@@ -171,3 +183,13 @@ def test_fixed_max_reference_inputs(wave, oracle, dev):
     fixed = wave.flash_attention(qt, kt, vt, qk_max_abs=1.0).float()
     adaptive = wave.flash_attention(qt, kt, vt).float()
     assert float((fixed - adaptive).abs().max()) <= TOL
+
+
+def test_config_launch_rejects_bad_waves_and_bounds(wave, dev):
+    x = torch.zeros((1, 1, 256, 128), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):
+        wave.flash_attention(x, x, x, waves=6)
+    with pytest.raises(ValueError):
+        wave.flash_attention(x, x, x, waves=4, qk_max_abs=-1.0)
+    with pytest.raises(ValueError):  # 2^(-2 * bound) below the bf16 normal range
+        wave.flash_attention(x, x, x, waves=4, qk_max_abs=2.0)

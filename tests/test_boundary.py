@@ -144,6 +144,16 @@ def test_fa_bounded_rejects_bad_bound(wave, dtype, bound):
     assert "qk_max_abs" in wave.runtime.lib().wave_last_error().decode()
 
 
+@pytest.mark.parametrize("waves,bound", [(6, 0.0), (0, 0.0), (4, -1.0), (4, float("nan")),
+                                         (8, 2.0)])
+def test_fa_config_rejects_bad_waves_and_bounds(wave, waves, bound):
+    """wave_fa_fwd_config_launch: waves 4 or 8 (wave_flash_attention.py:81-82);
+    a non-zero qk_max_abs is validated as wave_fa_fwd_bounded_launch's."""
+    L = wave.runtime.lib()
+    assert L.wave_fa_fwd_config_launch(16, 32, 48, 64, 1, 1, 1, 256, 128, 2, 0, 0.0, bound,
+                                       waves, None) == -1
+
+
 def test_fa_f32_rejects_bad_arguments(wave):
     L = wave.runtime.lib()
     assert L.wave_fa_f32_launch(None, 32, 48, 64, 16, 16, 32, None) == -1
@@ -173,6 +183,7 @@ ABI_SYMBOLS = {
     "mxfp4_": ("wmma_f16_matmul_tiled", 5 * 8 + 4, "mxfp4"),
     "streamk_": ("gfx950_f16_streamk_gemm", 5 * 8 + 4, "streamk"),
     "fa_bf16_": ("flash_attention_bf16_gfx950", 4 * 8, "fa"),
+    "fa4_bf16_": ("flash_attention_bf16_gfx950", 4 * 8, "fa"),
     "fa32_": ("flash_attention_f32", 4 * 8, "fa32"),
 }
 

@@ -260,6 +260,39 @@ def test_fa_f32_runner_launch(co, oracle, dev, threads):
     assert float(np.abs(O.cpu().numpy() - oracle.fa_f32_reference(q, k, v)).max()) <= 3e-3
 
 
+@pytest.mark.parametrize("name,qk", [("fa4_bf16_b1_h2_s512", None),
+                                     ("fa4_bf16_b1_h2_s512_qk1", 1.0)])
+def test_fa4_bf16_runner_default_launch(co, wave, dev, name, qk):
+    """The 4-wave code objects under the FA runner's defaults (--threads 256
+    --dynamic-lds 68096; wave_flash_attention.py:114-135): bit-identical to
+    the C ABI's 4-wave kernel."""
+    B, H, S, D = 1, 2, 512, 128
+    g = torch.Generator(device="cpu").manual_seed(31)
+    q, k, v = ((torch.rand((B, H, S, D), generator=g) * 2 - 1).to(torch.bfloat16).to(dev)
+               for _ in range(3))
+    o = torch.full_like(q, float("nan"))
+    with co.CodeObject(name) as mod:
+        mod.kernel("flash_attention_bf16_gfx950").launch((S // 256, B * H), (256,),
+                                                         [q, k, v, o], dynamic_lds=68096)
+    ref = wave.flash_attention(q, k, v, qk_max_abs=qk, waves=4)
+    torch.cuda.synchronize()
+    assert torch.equal(o, ref)
+
+
+@pytest.mark.parametrize("block,lds", [(128, 68096), (256, 45056 - 1024)])
+def test_fa4_bf16_outside_contract_writes_nothing(co, dev, block, lds):
+    """Another block size (below the 256 the object is built for; above it
+    the runtime refuses the launch, its registers do not fit two waves per
+    SIMD) or too little dynamic LDS: the kernel returns without writing."""
+    q = torch.zeros((1, 2, 512, 128), dtype=torch.bfloat16, device=dev)
+    o = torch.full_like(q, 3.0)
+    with co.CodeObject("fa4_bf16_b1_h2_s512") as mod:
+        mod.kernel("flash_attention_bf16_gfx950").launch((2, 2), (block,), [q, q, q, o],
+                                                         dynamic_lds=lds)
+        torch.cuda.synchronize()
+    assert bool((o == 3.0).all())
+
+
 def test_fa_bf16_fixed_max_code_object(co, wave, oracle, dev):
     """The reference's qk_max_abs=1 profile as a code object
     (-DWAVE_ABI_FA_QK_MAX_ABS=1.0): bit-identical to
