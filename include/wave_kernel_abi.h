@@ -98,11 +98,16 @@ typedef struct {
  *   launched by tools/wave-fa-calibrate/wave-fa-gfx950-runner.cpp:396-428.
  * Q, K, V, O [B*H][S][128] bf16; non-causal; scale 1/sqrt(128).
  * Launch: grid (S/256, B*H), block 512, dynamic LDS >= 102400 bytes (the
- *   runner's 8-wave setting --threads 512 --dynamic-lds 136192 works; its
- *   4-wave default of 68096 bytes does not). */
+ *   runner's 8-wave setting --threads 512 --dynamic-lds 136192 works).
+ * Built with -DWAVE_ABI_FA_WAVES=4 (the reference's waves=4 configuration,
+ *   wave_flash_attention.py:44-93): block 256, dynamic LDS >= 67584 bytes,
+ *   so the runner's 4-wave default --threads 256 --dynamic-lds 68096 works;
+ *   two such CTAs share a CU. */
 #define WAVE_ABI_FA_SYMBOL "flash_attention_bf16_gfx950"
 #define WAVE_ABI_FA_BLOCK 512
 #define WAVE_ABI_FA_MIN_LDS 102400
+#define WAVE_ABI_FA4_BLOCK 256
+#define WAVE_ABI_FA4_MIN_LDS 67584
 typedef struct {
   const void *Q;
   const void *K;
