@@ -24,6 +24,8 @@ struct GemmArgs {
   // group-major [K/32][M] and [K/32][N].
   const void *a_scale = nullptr;
   const void *b_scale = nullptr;
+  // MXFP4 with B and both scales in the AITER preshuffled layouts.
+  bool aiter = false;
 };
 
 constexpr int kTileEdge = 256;

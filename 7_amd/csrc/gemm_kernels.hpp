@@ -85,6 +85,9 @@ using DefaultCfg = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE, WAVE_GEMM_WAVES>;
 #define WAVE_FP4_WAVES 8
 #endif
 using Fp4Cfg = Cfg<32, 4, WAVE_FP4_WAVES, 4 * 512>;
+// MXFP4 with AITER-preshuffled B and scales: the scale area holds whole
+// 256-byte AITER scale blocks (32 rows x 8 groups), 8 for A and 8 for B.
+using Fp4ACfg = Cfg<32, 4, WAVE_FP4_WAVES, 16 * 256>;
 
 // LDS geometry of an operand tile.  The tile is stored as 128-byte
 // "super-rows" of eight 16-byte slots: with BK = 64 super-row R is tile row
@@ -198,27 +201,43 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
   constexpr uint32_t kPBuf = COL_MAJOR ? 0 : C::OPB;
   constexpr uint32_t kQBuf = COL_MAJOR ? C::OPB : 0;
 
+  // AITER (kMXFP4A): B arrives preshuffled, so the B tile sits in LDS as
+  // 16 row blocks of 1 KiB, each [4 chunks of 16 B][16 rows] (one K stage
+  // of one 16-row block is one contiguous KiB of the AITER buffer).
+  constexpr bool kAiter = IN_DT == kMXFP4A;
+  constexpr bool kPAiter = kAiter && !COL_MAJOR, kQAiter = kAiter && COL_MAJOR;
   // Fragment read offsets: row r of the operand tile, chunk (2*kk + hi).
   // slot = (slot_base + 2*kk + hi) ^ swz8(R) = (2*kk) ^ [slot_base ^ hi ^ swz8(R)]
+  // AITER B tile: (r/16)*1024 + (2*kk + hi)*256 + (r%16)*16.
+  auto aiter_off = [&](uint32_t buf, uint32_t r) {
+    return buf + (r >> 4) * 1024u + (lane >> 5) * 256u + (r & 15u) * 16u;
+  };
   uint32_t poff[TP], pswz[TP], qoff[TQ], qswz[TQ];
 #pragma unroll
   for (int t = 0; t < TP; ++t) {
     const uint32_t pr = wp * (TP * 32) + t * 32 + (lane & 31);
     const uint32_t pR = Geo<C>::super_row(pr);
-    poff[t] = kPBuf + pR * 128u;
+    poff[t] = kPAiter ? aiter_off(kPBuf, pr) : kPBuf + pR * 128u;
     pswz[t] = swz8(pR) ^ Geo<C>::slot_base(pr) ^ (lane >> 5);
   }
 #pragma unroll
   for (int t = 0; t < TQ; ++t) {
     const uint32_t qr = wq * (TQ * 32) + t * 32 + (lane & 31);
     const uint32_t qR = Geo<C>::super_row(qr);
-    qoff[t] = kQBuf + qR * 128u;
+    qoff[t] = kQAiter ? aiter_off(kQBuf, qr) : kQBuf + qR * 128u;
     qswz[t] = swz8(qR) ^ Geo<C>::slot_base(qr) ^ (lane >> 5);
   }
 
-  // MXFP4: offsets of this lane's P / Q tile rows in a stage's scale area
-  // ([group][A rows | B rows], 512 bytes per 32-value group).
+  // MXFP4: offsets of this lane's P / Q tile rows in a stage's scale area.
+  // Canonical: [group][A rows | B rows], 512 bytes per 32-value group.
+  // AITER: [A blocks | B blocks] of 256 bytes per 32 rows, byte
+  // g*64 + (r%16)*4 + (kt&1)*2 + (r%32)/16 for group g of the stage (the
+  // block covers 8 groups = two stages).
   uint32_t psc[TP], qsc[TQ];
+  auto aiter_sc = [&](bool is_b, uint32_t r) {
+    return 2 * C::OPB + (is_b ? 2048u : 0u) + (r >> 5) * 256u + (lane >> 5) * 64u +
+           (r & 15u) * 4u + ((r >> 4) & 1u);
+  };
   if constexpr (IN_DT == kMXFP4) {
 #pragma unroll
     for (int t = 0; t < TP; ++t)
@@ -226,6 +245,13 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
 #pragma unroll
     for (int t = 0; t < TQ; ++t)
       qsc[t] = 2 * C::OPB + (COL_MAJOR ? 256u : 0u) + wq * (TQ * 32) + t * 32 + (lane & 31);
+  } else if constexpr (kAiter) {
+#pragma unroll
+    for (int t = 0; t < TP; ++t)
+      psc[t] = aiter_sc(!COL_MAJOR, wp * (TP * 32) + t * 32 + (lane & 31));
+#pragma unroll
+    for (int t = 0; t < TQ; ++t)
+      qsc[t] = aiter_sc(COL_MAJOR, wq * (TQ * 32) + t * 32 + (lane & 31));
   }
 
   // Fragments of one 16-wide K slice: TP P tiles + TQ Q tiles, 16 bytes each
@@ -239,13 +265,22 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
     const uint8_t *s = smem + stage * C::STAGE;
     const uint32_t x = (uint32_t)(2 * kk);
     if (j < TQ)
-      f.q[j] = *reinterpret_cast<const u32x4 *>(s + qoff[j] + ((x ^ qswz[j]) << 4));
+      f.q[j] = *reinterpret_cast<const u32x4 *>(
+          s + qoff[j] + (kQAiter ? x * 256u : ((x ^ qswz[j]) << 4)));
     else
-      f.p[j - TQ] = *reinterpret_cast<const u32x4 *>(s + poff[j - TQ] +
-                                                     ((x ^ pswz[j - TQ]) << 4));
+      f.p[j - TQ] = *reinterpret_cast<const u32x4 *>(
+          s + poff[j - TQ] + (kPAiter ? x * 256u : ((x ^ pswz[j - TQ]) << 4)));
     if constexpr (IN_DT == kMXFP4) {
       // Lane half h holds the slice's 32-value group 2*kk + h.
       const uint8_t *sg = s + (x + (lane >> 5)) * 512u;
+      if (j < TQ)
+        f.sq[j] = sg[qsc[j]];
+      else
+        f.sp[j - TQ] = sg[psc[j - TQ]];
+    } else if constexpr (kAiter) {
+      // Group 2*kk + h of the stage; the stage's half of the AITER block is
+      // kt & 1 = stage & 1 (the ring has an even number of stages).
+      const uint8_t *sg = s + x * 64u + (stage & 1u) * 2u;
       if (j < TQ)
         f.sq[j] = sg[qsc[j]];
       else
@@ -274,7 +309,7 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       }
 #pragma unroll
       for (int tq = 0; tq < TQ; ++tq) {
-        if constexpr (IN_DT == kMXFP4)
+        if constexpr (is_fp4(IN_DT))
           acc[tp][tq] = mfma_fp4_32x32x64(cur.p[tp], cur.q[tq], acc[tp][tq], cur.sp[tp],
                                           cur.sq[tq]);
         else
@@ -322,16 +357,35 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
     // jobs w*SJ .. w*SJ+SJ-1 into [group][A rows | B rows] of the stage's
     // scale area.  All 64 lanes take part, so the loop body stays one basic
     // block and its explicit instruction order holds.
-    constexpr int SJ = IN_DT == kMXFP4 ? 8 / C::WAVES : 0;
+    // AITER: 16 jobs, (A if j < 8, else B) x the 256-byte scale block of
+    // rows 32*(j%8) .. +31 that holds the stage's groups.
+    static_assert(!kAiter || C::NSTAGE % 2 == 0, "AITER scale half follows stage parity");
+    constexpr int SJ = IN_DT == kMXFP4 ? 8 / C::WAVES : kAiter ? 16 / C::WAVES : 0;
     uint32_t lds_sc[SJ > 0 ? SJ : 1], g_sc[SJ > 0 ? SJ : 1];
-    if constexpr (SJ > 0) {
+    // AITER scale blocks per 32-row block: ceil(groups / 8), groups = K/32
+    // (p.K counts 16-bit units, 4 fp4 values each).
+    const uint32_t g8 = ((uint32_t)p.K + 63u) / 64u;
+    if constexpr (IN_DT == kMXFP4) {
 #pragma unroll
       for (int s = 0; s < SJ; ++s) {
         const uint32_t j = wave * SJ + s, grp = j >> 1;
         lds_sc[s] = lds_addr(smem) + 2 * C::OPB + grp * 512 + (j & 1) * 256;
         g_sc[s] = grp * (uint32_t)((j & 1) ? p.N : p.M) + ((j & 1) ? n0 : m0) + lane * 4;
       }
+    } else if constexpr (kAiter) {
+#pragma unroll
+      for (int s = 0; s < SJ; ++s) {
+        const uint32_t j = wave * SJ + s, u = j & 7u;
+        lds_sc[s] = lds_addr(smem) + 2 * C::OPB + (j >> 3) * 2048u + u * 256u;
+        g_sc[s] = ((uint32_t)((j >> 3) ? n0 : m0) / 32u + u) * g8 * 256u + lane * 4u;
+      }
     }
+    // AITER B: per-lane offset of its 16 bytes in the 1 KiB run of row
+    // block (wave*DMA + i); a row block spans 16 rows x 2*p.K bytes.
+    uint32_t goff_b[C::DMA];
+#pragma unroll
+    for (int i = 0; i < C::DMA; ++i)
+      goff_b[i] = kAiter ? (wave * C::DMA + i) * 32u * (uint32_t)p.K + lane * 16u : goff[i];
     // DMA d of one stage (0 <= d < 2*DMA): A chunks first, then B; MXFP4
     // adds d = 2*DMA (A scales) and 2*DMA + 1 (B scales).
     auto issue_one = [&](uint32_t stage, int kt, int d) {
@@ -339,14 +393,19 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       if (d < C::DMA) {
         dma16(l + d * 1024, a_tile + (size_t)kt * C::RB, goff[d]);
       } else if (d < 2 * C::DMA) {
-        dma16(l + C::OPB + (d - C::DMA) * 1024, b_tile + (size_t)kt * C::RB,
-              goff[d - C::DMA]);
+        dma16(l + C::OPB + (d - C::DMA) * 1024,
+              b_tile + (size_t)kt * (kAiter ? 1024 : C::RB), goff_b[d - C::DMA]);
       } else if constexpr (IN_DT == kMXFP4) {
         const int s = d - 2 * C::DMA;
         const bool is_b = ((wave * SJ + s) & 1) != 0;
         const uint32_t g0 = (uint32_t)kt * 4u * (uint32_t)(is_b ? p.N : p.M);
         dma4(lds_sc[s] + stage * C::STAGE, is_b ? (const void *)p.b_scale : p.a_scale,
              g_sc[s] + g0);
+      } else if constexpr (kAiter) {
+        const int s = d - 2 * C::DMA;
+        const bool is_b = ((wave * SJ + s) >> 3) != 0;
+        dma4(lds_sc[s] + stage * C::STAGE, is_b ? (const void *)p.b_scale : p.a_scale,
+             g_sc[s] + ((uint32_t)kt >> 1) * 256u);
       }
     };
     constexpr int kDmaPerStage = 2 * C::DMA + SJ;
@@ -569,12 +628,13 @@ __device__ __forceinline__ void store_tile_lds(const Params &p, int m0, int n0, 
 // One 256x256 output tile: CTA `raw` of a grid of tiles_m * tiles_n CTAs.
 // smem: DefaultCfg::SMEM bytes of 1024-byte-aligned LDS.
 template <int IN_DT>
-using CfgFor = std::conditional_t<IN_DT == kMXFP4, Fp4Cfg, DefaultCfg>;
+using CfgFor = std::conditional_t<IN_DT == kMXFP4, Fp4Cfg,
+                                  std::conditional_t<IN_DT == kMXFP4A, Fp4ACfg, DefaultCfg>>;
 
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
 __device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *smem) {
   using C = CfgFor<IN_DT>;
-  static_assert(IN_DT != kMXFP4 || !MASKED, "MXFP4 takes whole tiles only");
+  static_assert(!is_fp4(IN_DT) || !MASKED, "MXFP4 takes whole tiles only");
   int tm, tn;
   tile_coords(raw, p.tiles_m, p.tiles_n, p.group_m, true, tm, tn);
   // The tile origin is uniform; readfirstlane keeps it (and the DMA bases

@@ -8,20 +8,34 @@
 //   C[m][n] = sum_k (a[m][k] * 2^(sa[k/32][m]-127)) * (b[n][k] * 2^(sb[k/32][n]-127))
 // with fp32 accumulation; A, B row-major packed two fp4 per byte (low
 // nibble = even k), scales group-major (the reference's canonical layout).
+// With GemmArgs::aiter, B and both scale arrays come in the AITER
+// preshuffled layouts instead (runner.cpp:1223-1283; wave_matmul.py:891-935):
+// B byte (n, kb) at (((n/16 * K/64 + kb/32) * 2 + kb%32/16) * 16 + n%16) * 16
+// + kb%16, scale (group g, row r) at (r/32 * G8 + g/8) * 256 + (g%4) * 64 +
+// (r%16) * 4 + (g%8/4) * 2 + r%32/16 with rows padded to 256 and groups to
+// a multiple of 8 (G8 = padded groups / 8).
 #include "gemm_kernels.hpp"
 
 namespace wave {
 namespace gemm {
 
 namespace {
-template <int OUT>
+template <int IN, int OUT>
 hipError_t launch_out(const Params &p, bool cm, hipStream_t s) {
-  const dim3 grid(p.tiles_m * p.tiles_n), block(Fp4Cfg::THREADS);
+  const dim3 grid(p.tiles_m * p.tiles_n), block(CfgFor<IN>::THREADS);
   if (cm)
-    hipLaunchKernelGGL((tiled_kernel<kMXFP4, OUT, true, false, 8>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((tiled_kernel<IN, OUT, true, false, 8>), grid, block, 0, s, p);
   else
-    hipLaunchKernelGGL((tiled_kernel<kMXFP4, OUT, false, false, 8>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((tiled_kernel<IN, OUT, false, false, 8>), grid, block, 0, s, p);
   return hipGetLastError();
+}
+template <int IN>
+hipError_t launch_in(const Params &p, int out_dtype, bool cm, hipStream_t s) {
+  if (out_dtype == kF32)
+    return launch_out<IN, kF32>(p, cm, s);
+  if (out_dtype == kF16)
+    return launch_out<IN, kF16>(p, cm, s);
+  return launch_out<IN, kBF16>(p, cm, s);
 }
 } // namespace
 
@@ -42,11 +56,9 @@ hipError_t launch_mxfp4(const GemmArgs &g, hipStream_t stream) {
     p.group_m = p.tiles_m;
   p.ldc = g.col_major ? g.M : g.N;
   p.c_vec_ok = 1;
-  if (g.out_dtype == kF32)
-    return launch_out<kF32>(p, g.col_major, stream);
-  if (g.out_dtype == kF16)
-    return launch_out<kF16>(p, g.col_major, stream);
-  return launch_out<kBF16>(p, g.col_major, stream);
+  if (g.aiter)
+    return launch_in<kMXFP4A>(p, g.out_dtype, g.col_major, stream);
+  return launch_in<kMXFP4>(p, g.out_dtype, g.col_major, stream);
 }
 
 } // namespace gemm

@@ -17,6 +17,9 @@
 //     :1792-1794): packed e2m1 A [M][K/2], B [N][K/2], e8m0 scales
 //     [K/32][M], [K/32][N].  -DWAVE_ABI_MXFP4 -DWAVE_ABI_M= -DWAVE_ABI_N=
 //     -DWAVE_ABI_K= -DWAVE_ABI_OUT=kF32|kF16|kBF16 -DWAVE_ABI_CM=0|1
+//     [-DWAVE_ABI_MXFP4_AITER: B and scales in the AITER layouts
+//     (--mxfp4-input-layout aiter, runner.cpp:1223-1283); dynamic LDS
+//     >= 147456]
 //   gfx950_f16_streamk_gemm(const f16* A, const f16* B, f16* C, f32* scratch,
 //                           u32* counters, int32 workers)
 //     (wave_matmul.py:11556-11567; runner.cpp:1811-1816; column-major C,
@@ -126,19 +129,26 @@ extern "C" __global__ __launch_bounds__(256, 1) void wmma_f16_matmul_tiled(
 #endif
 
 #ifdef WAVE_ABI_MXFP4
-extern "C" __global__ __launch_bounds__(wave::gemm::Fp4Cfg::THREADS, 1) void wmma_f16_matmul_tiled(
+#ifdef WAVE_ABI_MXFP4_AITER
+constexpr int kAbiFp4 = kMXFP4A;  // AITER-preshuffled B and scales
+#else
+constexpr int kAbiFp4 = kMXFP4;
+#endif
+using AbiFp4Cfg = wave::gemm::CfgFor<kAbiFp4>;
+extern "C" __global__ __launch_bounds__(AbiFp4Cfg::THREADS, 1) void wmma_f16_matmul_tiled(
     const uint8_t *A, const uint8_t *B, void *C, const uint8_t *A_scale, const uint8_t *B_scale,
     int trip) {
   using namespace wave::gemm;
   extern __shared__ __attribute__((aligned(1024))) uint8_t dsmem[];
   (void)trip;
-  if (blockDim.x != Fp4Cfg::THREADS || blockDim.y != 1 || blockDim.z != 1 ||
-      dynamic_lds_bytes() < (uint32_t)Fp4Cfg::SMEM)
+  if (blockDim.x != AbiFp4Cfg::THREADS || blockDim.y != 1 || blockDim.z != 1 ||
+      dynamic_lds_bytes() < (uint32_t)AbiFp4Cfg::SMEM)
     return;
   constexpr int M = WAVE_ABI_M, N = WAVE_ABI_N, K = WAVE_ABI_K;
   static_assert(M > 0 && N > 0 && M % kTile == 0 && N % kTile == 0 && K > 0 && K % 128 == 0,
                 "MXFP4 code objects take whole 256x256 tiles and K % 128 == 0");
-  static_assert((uint64_t)(K / 32) * (M > N ? M : N) < (1ull << 32), "scale offsets");
+  static_assert((uint64_t)((K / 32 + 7) / 8 * 8) * (M > N ? M : N) < (1ull << 32),
+                "scale offsets");
   constexpr bool CM = WAVE_ABI_CM != 0;
   constexpr int OUT_BYTES = WAVE_ABI_OUT == kF32 ? 4 : 2;
   if (!(aligned16(A) && aligned16(B) && aligned16(A_scale) && aligned16(B_scale)) ||
@@ -161,7 +171,7 @@ extern "C" __global__ __launch_bounds__(wave::gemm::Fp4Cfg::THREADS, 1) void wmm
   const int tiles = p.tiles_m * p.tiles_n;
   const int ctas = gridDim.x * gridDim.y;
   for (int raw = blockIdx.y * gridDim.x + blockIdx.x; raw < tiles; raw += ctas)
-    tiled_cta<kMXFP4, WAVE_ABI_OUT, CM, false, 8>(p, raw, dsmem);
+    tiled_cta<kAbiFp4, WAVE_ABI_OUT, CM, false, 8>(p, raw, dsmem);
 }
 #endif
 

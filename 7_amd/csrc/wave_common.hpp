@@ -18,7 +18,11 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Element type codes of the C ABI (include/wave_runtime.h).
-enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2, kMXFP4 = 3 };
+// kMXFP4: packed e2m1 with group-major e8m0 scales (canonical layout);
+// kMXFP4A: the same values with B and both scale arrays in the AITER
+// preshuffled layouts.
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2, kMXFP4 = 3, kMXFP4A = 4 };
+constexpr bool is_fp4(int dt) { return dt == kMXFP4 || dt == kMXFP4A; }
 
 // v_mfma_f32_32x32x16_{f16,bf16}: D[32x32] += A[32x16] * B[16x32].
 // Lane l supplies A[l%32][8*(l/32) .. +8] and B[8*(l/32) .. +8][l%32] as

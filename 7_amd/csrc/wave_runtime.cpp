@@ -69,6 +69,49 @@ int streamk_sizes(int M, int N, int workers, size_t *scratch, size_t *counters) 
   return WAVE_OK;
 }
 
+// Shared MXFP4 checks and launch (canonical or AITER input layout).
+int gemm_mxfp4(const void *A, const void *B, void *C, const void *A_scale,
+               const void *B_scale, int M, int N, int K, int out_dtype, int c_layout,
+               bool aiter, void *stream, const char *name) {
+  if (!A || !B || !C || !A_scale || !B_scale)
+    return fail(WAVE_ERR_INVALID, "gemm_mxfp4: null A, B, C or scale pointer");
+  if (M <= 0 || N <= 0 || K <= 0)
+    return fail(WAVE_ERR_INVALID, "gemm_mxfp4: M=%d N=%d K=%d must be positive", M, N, K);
+  if (!is_out_dtype(out_dtype))
+    return fail(WAVE_ERR_INVALID, "gemm_mxfp4: output dtype %d is not f32/f16/bf16",
+                out_dtype);
+  if (c_layout != WAVE_ROW_MAJOR && c_layout != WAVE_COL_MAJOR)
+    return fail(WAVE_ERR_INVALID, "gemm_mxfp4: layout %d is not row/column-major", c_layout);
+  if (K % 128)
+    return fail(WAVE_ERR_INVALID, "gemm_mxfp4: K=%d is not a multiple of 128", K);
+  if (M % 256 || N % 256)
+    return fail(WAVE_ERR_UNSUPPORTED, "gemm_mxfp4: M=%d N=%d must be multiples of 256", M, N);
+  const size_t out_bytes = out_dtype == WAVE_F32 ? 4 : 2;
+  if (((uintptr_t)A | (uintptr_t)B | (uintptr_t)A_scale | (uintptr_t)B_scale) & 15u)
+    return fail(WAVE_ERR_UNSUPPORTED, "gemm_mxfp4: A, B and scales must be 16-byte aligned");
+  if ((uintptr_t)C % (4 * out_bytes))
+    return fail(WAVE_ERR_UNSUPPORTED, "gemm_mxfp4: C must be aligned to 4 elements");
+  // Per-lane scale offsets are 32-bit: (K/32 groups, padded to 8 for AITER)
+  // x max(M, N) bytes.
+  const uint64_t groups = aiter ? ((uint64_t)K / 32 + 7) / 8 * 8 : (uint64_t)K / 32;
+  if (groups * (uint64_t)(M > N ? M : N) >= (1ull << 32))
+    return fail(WAVE_ERR_UNSUPPORTED, "gemm_mxfp4: scale array exceeds 2^32 bytes");
+  wave::gemm::GemmArgs g;
+  g.A = A;
+  g.B = B;
+  g.C = C;
+  g.a_scale = A_scale;
+  g.b_scale = B_scale;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.in_dtype = 3;  // wave::kMXFP4
+  g.aiter = aiter;
+  g.out_dtype = out_dtype;
+  g.col_major = c_layout == WAVE_COL_MAJOR;
+  return hip_status(wave::gemm::launch_mxfp4(g, static_cast<hipStream_t>(stream)), name);
+}
+
 template <typename T> void *to_global(wave_memref_1d *m) {
   return static_cast<void *>(static_cast<T *>(m->data) + m->offset);
 }
@@ -129,41 +172,15 @@ int wave_gemm_launch(const void *A, const void *B, void *C, int M, int N, int K,
 int wave_gemm_mxfp4_launch(const void *A, const void *B, void *C, const void *A_scale,
                            const void *B_scale, int M, int N, int K, int out_dtype,
                            int c_layout, void *stream) {
-  if (!A || !B || !C || !A_scale || !B_scale)
-    return fail(WAVE_ERR_INVALID, "gemm_mxfp4: null A, B, C or scale pointer");
-  if (M <= 0 || N <= 0 || K <= 0)
-    return fail(WAVE_ERR_INVALID, "gemm_mxfp4: M=%d N=%d K=%d must be positive", M, N, K);
-  if (!is_out_dtype(out_dtype))
-    return fail(WAVE_ERR_INVALID, "gemm_mxfp4: output dtype %d is not f32/f16/bf16",
-                out_dtype);
-  if (c_layout != WAVE_ROW_MAJOR && c_layout != WAVE_COL_MAJOR)
-    return fail(WAVE_ERR_INVALID, "gemm_mxfp4: layout %d is not row/column-major", c_layout);
-  if (K % 128)
-    return fail(WAVE_ERR_INVALID, "gemm_mxfp4: K=%d is not a multiple of 128", K);
-  if (M % 256 || N % 256)
-    return fail(WAVE_ERR_UNSUPPORTED, "gemm_mxfp4: M=%d N=%d must be multiples of 256", M, N);
-  const size_t out_bytes = out_dtype == WAVE_F32 ? 4 : 2;
-  if (((uintptr_t)A | (uintptr_t)B | (uintptr_t)A_scale | (uintptr_t)B_scale) & 15u)
-    return fail(WAVE_ERR_UNSUPPORTED, "gemm_mxfp4: A, B and scales must be 16-byte aligned");
-  if ((uintptr_t)C % (4 * out_bytes))
-    return fail(WAVE_ERR_UNSUPPORTED, "gemm_mxfp4: C must be aligned to 4 elements");
-  // Per-lane scale offsets are 32-bit: (K/32) groups of max(M, N) bytes.
-  if ((uint64_t)(K / 32) * (uint64_t)(M > N ? M : N) >= (1ull << 32))
-    return fail(WAVE_ERR_UNSUPPORTED, "gemm_mxfp4: (K/32)*max(M,N) exceeds 2^32");
-  wave::gemm::GemmArgs g;
-  g.A = A;
-  g.B = B;
-  g.C = C;
-  g.a_scale = A_scale;
-  g.b_scale = B_scale;
-  g.M = M;
-  g.N = N;
-  g.K = K;
-  g.in_dtype = 3;  // wave::kMXFP4
-  g.out_dtype = out_dtype;
-  g.col_major = c_layout == WAVE_COL_MAJOR;
-  return hip_status(wave::gemm::launch_mxfp4(g, static_cast<hipStream_t>(stream)),
+  return gemm_mxfp4(A, B, C, A_scale, B_scale, M, N, K, out_dtype, c_layout, false, stream,
                     "wave_gemm_mxfp4_launch");
+}
+
+int wave_gemm_mxfp4_aiter_launch(const void *A, const void *B, void *C, const void *A_scale,
+                                 const void *B_scale, int M, int N, int K, int out_dtype,
+                                 int c_layout, void *stream) {
+  return gemm_mxfp4(A, B, C, A_scale, B_scale, M, N, K, out_dtype, c_layout, true, stream,
+                    "wave_gemm_mxfp4_aiter_launch");
 }
 
 int wave_gemm_streamk_workspace_bytes(int M, int N, int workers,

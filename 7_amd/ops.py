@@ -63,23 +63,35 @@ def gemm(a: torch.Tensor, b: torch.Tensor, *, out_dtype="f16",
 
 def gemm_mxfp4(a: torch.Tensor, b: torch.Tensor, a_scale: torch.Tensor,
                b_scale: torch.Tensor, *, out_dtype="f32", layout: str = "row",
+               input_layout: str = "canonical",
                out: torch.Tensor | None = None) -> torch.Tensor:
     """MXFP4 scaled GEMM (the reference's ``mxfp4`` input type,
     wave_matmul.py:996-1022): A [M, K/2] and B [N, K/2] uint8, two e2m1
     values per byte (low nibble = even k); a_scale [K/32, M] and b_scale
     [K/32, N] uint8 e8m0.  C[m, n] = sum_k a[m, k] 2^(sa[k/32, m]-127) *
     b[n, k] 2^(sb[k/32, n]-127), fp32 accumulate.  layout as in gemm().
+
+    input_layout "aiter": b [N, K/2] holds the AITER-preshuffled bytes and
+    the scales are the AITER blocks (1-D, M*G8*8 and N*G8*8 bytes with G8 =
+    ceil(K/256); wave_gemm_mxfp4_aiter_launch).
     """
+    aiter = input_layout == "aiter"
+    if input_layout not in ("canonical", "aiter"):
+        raise ValueError("input_layout must be 'canonical' or 'aiter'")
     for t, name in ((a, "a"), (b, "b"), (a_scale, "a_scale"), (b_scale, "b_scale")):
         _need(t, name)
-        if t.dtype != torch.uint8 or t.dim() != 2:
-            raise ValueError(f"{name} must be a 2-D uint8 tensor")
+        if t.dtype != torch.uint8 or t.dim() != (1 if aiter and "scale" in name else 2):
+            raise ValueError(f"{name} has the wrong dtype or rank")
     M, KB = a.shape
     N = b.shape[0]
     K = 2 * KB
     if b.shape[1] != KB:
         raise ValueError("a must be [M, K/2] and b [N, K/2]")
-    if K % 32 or tuple(a_scale.shape) != (K // 32, M) or tuple(b_scale.shape) != (K // 32, N):
+    if aiter:
+        g8 = (K // 32 + 7) // 8
+        if K % 32 or a_scale.numel() != M * g8 * 8 or b_scale.numel() != N * g8 * 8:
+            raise ValueError("AITER scales must hold M*G8*8 and N*G8*8 bytes")
+    elif K % 32 or tuple(a_scale.shape) != (K // 32, M) or tuple(b_scale.shape) != (K // 32, N):
         raise ValueError("scales must be [K/32, M] and [K/32, N]")
     odt = _dtype(out_dtype)
     shape = (M, N) if layout == "row" else (N, M)
@@ -88,9 +100,10 @@ def gemm_mxfp4(a: torch.Tensor, b: torch.Tensor, a_scale: torch.Tensor,
     elif tuple(out.shape) != shape or out.dtype != odt:
         raise ValueError("out has the wrong shape or dtype")
     _need(out, "out")
-    rt.check(rt.lib().wave_gemm_mxfp4_launch(
-        a.data_ptr(), b.data_ptr(), out.data_ptr(), a_scale.data_ptr(), b_scale.data_ptr(),
-        M, N, K, _DT[odt], rt.ROW_MAJOR if layout == "row" else rt.COL_MAJOR, _stream(a)))
+    fn = rt.lib().wave_gemm_mxfp4_aiter_launch if aiter else rt.lib().wave_gemm_mxfp4_launch
+    rt.check(fn(a.data_ptr(), b.data_ptr(), out.data_ptr(), a_scale.data_ptr(),
+                b_scale.data_ptr(), M, N, K, _DT[odt],
+                rt.ROW_MAJOR if layout == "row" else rt.COL_MAJOR, _stream(a)))
     return out
 
 

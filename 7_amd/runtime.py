@@ -27,6 +27,7 @@ _SZ = ctypes.c_size_t
 _SIGNATURES = {
     "wave_gemm_launch": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "wave_gemm_mxfp4_launch": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "wave_gemm_mxfp4_aiter_launch": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "wave_gemm_streamk_workspace_bytes": (_I, [_I, _I, _I, ctypes.POINTER(_SZ),
                                                ctypes.POINTER(_SZ)]),
     "wave_gemm_streamk_launch": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P]),

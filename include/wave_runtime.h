@@ -113,6 +113,21 @@ int wave_gemm_mxfp4_launch(const void *A, const void *B, void *C,
                            int N, int K, int out_dtype, int c_layout,
                            void *stream);
 
+/* The same product with the reference's AITER input layout
+ * (--mxfp4-input-layout aiter; runner.cpp:1223-1283 makeAITERBBytes /
+ * makeAITERScaleBytes, wave_matmul.py:891-935): A as above; B preshuffled,
+ * byte (n, kb) of the [N][K/2] matrix at
+ * (((n/16 * K/64 + kb/32) * 2 + kb%32/16) * 16 + n%16) * 16 + kb%16; both
+ * scale arrays as 256-byte blocks of 32 rows x 8 groups, scale (g, r) at
+ * (r/32 * G8 + g/8) * 256 + (g%4) * 64 + (r%16) * 4 + (g%8/4) * 2 + r%32/16,
+ * rows padded to a multiple of 256 and groups to a multiple of 8 (G8 =
+ * padded groups / 8; pad bytes are never read).  Same limits as
+ * wave_gemm_mxfp4_launch. */
+int wave_gemm_mxfp4_aiter_launch(const void *A, const void *B, void *C,
+                                 const void *A_scale, const void *B_scale, int M,
+                                 int N, int K, int out_dtype, int c_layout,
+                                 void *stream);
+
 /* ---- flash-attention forward --------------------------------------------
  * O = softmax(Q K^T * scale) V.  Q, O: [batch][q_heads][seq][head_dim];
  * K, V: [batch][kv_heads][seq][head_dim]; dtype f16 or bf16 for all four;

@@ -86,6 +86,14 @@ def test_mxfp4_rejects_bad_arguments(wave, kw, status):
     assert L.wave_last_error()
 
 
+def test_mxfp4_aiter_rejects_bad_arguments(wave):
+    L = wave.runtime.lib()
+    args = [256, 512, 1024, 2048, 4096]
+    assert L.wave_gemm_mxfp4_aiter_launch(*args, 256, 256, 200, 0, 0, None) == -1
+    assert L.wave_gemm_mxfp4_aiter_launch(*args, 384, 256, 256, 0, 0, None) == -2
+    assert L.wave_gemm_mxfp4_aiter_launch(None, *args[1:], 256, 256, 256, 0, 0, None) == -1
+
+
 def test_streamk_workspace_sizes(wave):
     # runner.cpp:393-412 and rand_int_test.cpp:216-227: 5 workers ->
     # 5*2*256*256*4 bytes of scratch; 512x768 -> 6 counters
@@ -181,6 +189,7 @@ def test_product_does_not_import_oracle():
 ABI_SYMBOLS = {
     "gemm_": ("wmma_f16_matmul_tiled", 3 * 8 + 4, "matmul"),
     "mxfp4_": ("wmma_f16_matmul_tiled", 5 * 8 + 4, "mxfp4"),
+    "mxfp4a_": ("wmma_f16_matmul_tiled", 5 * 8 + 4, "mxfp4"),
     "streamk_": ("gfx950_f16_streamk_gemm", 5 * 8 + 4, "streamk"),
     "fa_bf16_": ("flash_attention_bf16_gfx950", 4 * 8, "fa"),
     "fa4_bf16_": ("flash_attention_bf16_gfx950", 4 * 8, "fa"),

@@ -9,6 +9,10 @@ oracle bit for bit, and f16 / bf16 outputs are one RNE rounding of it.  The
 Python builder's inputs (codes 1.0 / 2.0, scales 0x7f - group) are exact in
 the same way.  Larger K is held to the runner's own limit,
 1e-2 + 1e-3 * |expected| (runner.cpp:925-960 validateRowMajorOutput).
+The AITER input layout (wave_gemm_mxfp4_aiter_launch) gets its operands
+from the oracle's AITER shuffles, which are pinned to the reference runner's
+makeAITERBBytes / makeAITERScaleBytes; it must give the canonical result
+bit for bit.
 """
 
 import numpy as np
@@ -137,3 +141,37 @@ def test_rejects_unsupported_shapes(wave, dev):
         wave.gemm_mxfp4(z(128, 64), z(256, 64), z(4, 128), z(4, 256))
     with pytest.raises(ValueError):  # scale shape
         wave.gemm_mxfp4(z(256, 64), z(256, 64), z(4, 256), z(2, 256))
+
+
+def aiter_operands(oracle, b, sa, sb, N, K):
+    M = sa.shape[1]
+    return (oracle.mxfp4_aiter_b(b, N, K).reshape(N, K // 2),
+            oracle.mxfp4_aiter_scales(sa, M, K), oracle.mxfp4_aiter_scales(sb, N, K))
+
+
+@pytest.mark.parametrize("out_dt", [0, 1])
+@pytest.mark.parametrize("layout", ["row", "col"])
+@pytest.mark.parametrize("shape", [(256, 256, 256), (256, 512, 384), (512, 256, 1024)])
+def test_aiter_layout_bit_exact(wave, oracle, dev, out_dt, layout, shape):
+    """K = 384 leaves the second 8-group scale block half used (padding)."""
+    M, N, K = shape
+    print(f"mxfp4 aiter {shape} out={out_dt} {layout}", flush=True)
+    a, b, sa, sb = oracle.mxfp4_operands(M, N, K, 9)
+    ba, saa, sba = aiter_operands(oracle, b, sa, sb, N, K)
+    c = wave.gemm_mxfp4(up(a, dev), up(ba, dev), up(saa, dev), up(sba, dev),
+                        out_dtype=ODT[out_dt], layout=layout, input_layout="aiter")
+    torch.cuda.synchronize()
+    c = c.t() if layout == "col" else c
+    assert_exact(oracle, c, oracle.gemm_mxfp4(a, b, sa, sb), out_dt)
+
+
+def test_aiter_matches_canonical_large_k(wave, oracle, dev):
+    M, N, K = 1024, 2048, 8192
+    a, b, sa, sb = oracle.mxfp4_operands(M, N, K, 4)
+    ba, saa, sba = aiter_operands(oracle, b, sa, sb, N, K)
+    ref = wave.gemm_mxfp4(up(a, dev), up(b, dev), up(sa, dev), up(sb, dev),
+                          out_dtype=torch.float16)
+    got = wave.gemm_mxfp4(up(a, dev), up(ba, dev), up(saa, dev), up(sba, dev),
+                          out_dtype=torch.float16, input_layout="aiter")
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)

@@ -159,6 +159,23 @@ def test_mxfp4_outside_contract_writes_nothing(co, oracle, dev, block, lds):
     assert bool((C == 3.0).all())
 
 
+def test_mxfp4_aiter_code_object(co, oracle, dev):
+    """-DWAVE_ABI_MXFP4_AITER: the same symbol and arguments, B and scales in
+    the AITER layouts (--mxfp4-input-layout aiter), dynamic LDS 147456."""
+    M, N, K = 256, 512, 384
+    a, b, sa, sb = oracle.mxfp4_operands(M, N, K, 7)
+    ba = oracle.mxfp4_aiter_b(b, N, K)
+    saa, sba = oracle.mxfp4_aiter_scales(sa, M, K), oracle.mxfp4_aiter_scales(sb, N, K)
+    C = torch.full((M, N), float("nan"), dtype=torch.float16, device=dev)
+    with co.CodeObject("mxfp4a_f16_rm_256x512x384") as mod:
+        mod.kernel("wmma_f16_matmul_tiled").launch(
+            (2,), (512,), [up8(a, dev), up8(ba, dev), C, up8(saa, dev), up8(sba, dev), 0],
+            dynamic_lds=147456)
+        torch.cuda.synchronize()
+    exp = oracle.round_output(oracle.gemm_mxfp4(a, b, sa, sb), 1)
+    assert np.array_equal(to_bits(C), exp)
+
+
 def test_mxfp4_4096_matches_c_abi(co, wave, dev):
     """The 4096x4096x8192 f16 column-major code object (the reference's MXFP4
     profile layout) computes what wave_gemm_mxfp4_launch computes, bit for
