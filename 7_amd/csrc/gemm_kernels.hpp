@@ -44,6 +44,12 @@
 #ifndef WAVE_GEMM_WAVES
 #define WAVE_GEMM_WAVES 4
 #endif
+#ifndef WAVE_GEMM_READ_ORDER
+#define WAVE_GEMM_READ_ORDER 0
+#endif
+#ifndef WAVE_GEMM_PRE_RG
+#define WAVE_GEMM_PRE_RG 4  // MFMA groups that carry the pre-barrier reads
+#endif
 
 namespace wave {
 namespace gemm {
@@ -260,8 +266,12 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
     u32x4 p[TP], q[TQ];
     uint32_t sp[TP], sq[TQ];
   };
-  // Fragment j of a slice: j < TQ -> Q tile j, else P tile j - TQ.
-  auto read_one = [&](Frag &f, uint32_t stage, int kk, int j) {
+  // Fragment j of a slice: j < TQ -> Q tile j, else P tile j - TQ.  With
+  // WAVE_GEMM_READ_ORDER 1 (4 x 4 tiles) the reads run P0, Q0-Q3, P1-P3, so
+  // the first MFMA row of the next slice finds P0 read a whole step early.
+  auto read_one = [&](Frag &f, uint32_t stage, int kk, int jr) {
+    constexpr bool kP0First = WAVE_GEMM_READ_ORDER == 1 && TP == 4 && TQ == 4;
+    const int j = !kP0First ? jr : jr == 0 ? TQ : jr <= TQ ? jr - 1 : jr;
     const uint8_t *s = smem + stage * C::STAGE;
     const uint32_t x = (uint32_t)(2 * kk);
     if (j < TQ)
@@ -298,13 +308,15 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
   // and hook(tp) (the DMA issues assigned to that group).  sched_barrier
   // keeps the compiler from regrouping them, so DMA and LDS traffic stay
   // spread through the MFMA stream.
+  // RG: the reads are spread over the first RG groups only.
   auto step = [&](const Frag &cur, Frag &nxt, bool read, uint32_t nstage,
-                  int nkk, auto hook) {
+                  int nkk, auto hook, auto rg_tag) {
+    constexpr int RG = decltype(rg_tag)::value;
 #pragma unroll
     for (int tp = 0; tp < TP; ++tp) {
-      if (read) {
+      if (read && tp < RG) {
 #pragma unroll
-        for (int j = tp * NREAD / TP; j < (tp + 1) * NREAD / TP; ++j)
+        for (int j = tp * NREAD / RG; j < (tp + 1) * NREAD / RG; ++j)
           read_one(nxt, nstage, nkk, j);
       }
 #pragma unroll
@@ -325,11 +337,18 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
   // stage barrier while the next stage's slice 0 is read into f[0].
   Frag f[2];
   constexpr int kLast = (C::KS - 1) & 1;
+  // The step just before a stage barrier keeps its last group free of
+  // fragment reads: the barrier's lgkmcnt(0) then finds them done.
   auto body_h = [&](uint32_t stage, auto hook) {
 #pragma unroll
-    for (int kk = 0; kk + 1 < C::KS; ++kk)
-      step(f[kk & 1], f[(kk + 1) & 1], true, stage, kk + 1,
-           [&](int tp) { hook(kk * 4 + tp); });
+    for (int kk = 0; kk + 1 < C::KS; ++kk) {
+      if (kk + 2 < C::KS)
+        step(f[kk & 1], f[(kk + 1) & 1], true, stage, kk + 1,
+             [&](int tp) { hook(kk * 4 + tp); }, std::integral_constant<int, TP>{});
+      else
+        step(f[kk & 1], f[(kk + 1) & 1], true, stage, kk + 1,
+             [&](int tp) { hook(kk * 4 + tp); }, std::integral_constant<int, WAVE_GEMM_PRE_RG>{});
+    }
   };
   auto body = [&](uint32_t stage) { body_h(stage, no_hook); };
 
@@ -454,17 +473,18 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       vm_wait_barrier<kVm>();
       stage = (stage + 1) % C::NSTAGE;
       step(f[kLast], f[0], true, stage, 0,
-           [&](int tp) { issue_groups(ahead, kt_ahead, G1 + tp); });
+           [&](int tp) { issue_groups(ahead, kt_ahead, G1 + tp); },
+           std::integral_constant<int, TP>{});
     }
     // Drain: nothing more to issue; wait for everything.
     for (; i + 1 < nk; ++i) {
       body(stage);
       vm_wait_barrier();
       stage = (stage + 1) % C::NSTAGE;
-      step(f[kLast], f[0], true, stage, 0, no_hook);
+      step(f[kLast], f[0], true, stage, 0, no_hook, std::integral_constant<int, TP>{});
     }
     body(stage);
-    step(f[kLast], f[0], false, 0, 0, no_hook);
+    step(f[kLast], f[0], false, 0, 0, no_hook, std::integral_constant<int, TP>{});
     vm_wait_barrier();
   } else {
     // VGPR-staged loads with bounds checks (ragged M/N/K, unaligned K);
@@ -508,7 +528,8 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       if (i + 1 < nk)
         store(stage ^ 1);
       lds_barrier();
-      step(f[kLast], f[0], i + 1 < nk, stage ^ 1, 0, no_hook);
+      step(f[kLast], f[0], i + 1 < nk, stage ^ 1, 0, no_hook,
+           std::integral_constant<int, TP>{});
     }
   }
 }
