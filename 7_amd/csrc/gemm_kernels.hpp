@@ -50,6 +50,17 @@
 #ifndef WAVE_GEMM_PRE_RG
 #define WAVE_GEMM_PRE_RG 4  // MFMA groups that carry the pre-barrier reads
 #endif
+// MFMA shape of the tiled f16/bf16 kernel's whole-tile path: 32 selects
+// v_mfma_f32_32x32x16, 16 selects v_mfma_f32_16x16x32.  Ragged tiles,
+// Stream-K and MXFP4 always use the 32x32 shapes.
+#ifndef WAVE_GEMM_MF
+#define WAVE_GEMM_MF 16
+#endif
+// With one MFMA slice per stage (16x16x32 at BK = 32): MFMA groups of a
+// step that carry the next stage's fragment reads (0 = all of them).
+#ifndef WAVE_GEMM_KS1_RG
+#define WAVE_GEMM_KS1_RG 0
+#endif
 
 namespace wave {
 namespace gemm {
@@ -60,20 +71,29 @@ constexpr int kSKUnit = 64;  // Stream-K work unit: 64 K elements of one tile
 
 // LDS ring geometry for BK elements of K per stage and NSTAGE stages, and
 // the wave grid: WAVES waves, WPN along P (the MFMA row / C-contiguous
-// dimension) x WQN along Q, each owning TP x TQ MFMA 32x32 tiles.
+// dimension) x WQN along Q, each owning TP x TQ MFMA tiles of MF x MF.
 // SCALE_: bytes per stage of MXFP4 e8m0 scales after the A and B tiles.
-template <int BK_, int NSTAGE_, int WAVES_, int SCALE_ = 0> struct Cfg {
+// MF_: MFMA tile edge, 32 (32x32x16: K slice 16) or 16 (16x16x32: K slice
+// 32).  Accumulator register r of lane l holds D[8*(r/4) + 4*(l/MF) + r%4]
+// [l%MF] of its tile in both shapes (NG = MF*MF/256 groups of 4).
+template <int BK_, int NSTAGE_, int WAVES_, int SCALE_ = 0, int MF_ = 32> struct Cfg {
   static constexpr int BK = BK_;
   static constexpr int SCALE = SCALE_;
   static constexpr int NSTAGE = NSTAGE_;
   static constexpr int WAVES = WAVES_;
+  static constexpr int MF = MF_;
   static constexpr int THREADS = 64 * WAVES;
   static constexpr int WPN = 2, WQN = WAVES / 2;
-  static constexpr int TP = 8 / WPN, TQ = 8 / WQN;
-  static_assert(TP == 4 && (TQ == 4 || TQ == 2), "4 or 8 waves");
+  static constexpr int TP = 128 / MF, TQ = 256 / WQN / MF;
+  static_assert((MF == 32 || MF == 16) && (WAVES == 4 || WAVES == 8), "4 or 8 waves");
+  static constexpr int NG = MF * MF / 256;       // 4-register accumulator groups
+  using Acc = std::conditional_t<MF == 32, f32x16, f32x4>;
+  static constexpr int KSL = 512 / MF;           // K elements per MFMA slice
+  static constexpr int CHS = KSL / 8;            // 16-byte row chunks per slice
   static constexpr int RB = BK * 2;              // bytes per operand row
   static constexpr int CPR = BK / 8;             // 16-byte chunks per row
-  static constexpr int KS = BK / 16;             // MFMA K slices per stage
+  static constexpr int KS = BK / KSL;            // MFMA K slices per stage
+  static_assert(KS >= 1 && BK % KSL == 0, "BK holds whole MFMA slices");
   static constexpr int OPB = kTile * RB;         // bytes per operand tile
   static constexpr int STAGE = 2 * OPB + SCALE;  // A + B (+ scales)
   static constexpr int SMEM = NSTAGE * STAGE;
@@ -82,6 +102,8 @@ template <int BK_, int NSTAGE_, int WAVES_, int SCALE_ = 0> struct Cfg {
   static_assert(SMEM <= 160 * 1024, "LDS ring exceeds 160 KiB");
 };
 using DefaultCfg = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE, WAVE_GEMM_WAVES>;
+// Whole tiles of the tiled f16/bf16 kernel (same ring and wave grid).
+using TileCfg = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE, WAVE_GEMM_WAVES, 0, WAVE_GEMM_MF>;
 // MXFP4: the same ring with K counted in 16-bit units (one 64-byte row
 // chunk = 128 fp4 values per stage, one MFMA 32x32x64 per 32-byte slice)
 // and 2 KiB of scales per stage: four 32-value groups x (256 A + 256 B)
@@ -198,8 +220,10 @@ template <class C, int IN_DT, bool COL_MAJOR, bool MASKED, int VEC>
 __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
                                          int kt_begin, int kt_end,
                                          uint8_t *smem,
-                                         f32x16 (&acc)[C::TP][C::TQ]) {
-  constexpr int TP = C::TP, TQ = C::TQ, NREAD = TP + TQ;
+                                         typename C::Acc (&acc)[C::TP][C::TQ]) {
+  constexpr int TP = C::TP, TQ = C::TQ, NREAD = TP + TQ, MF = C::MF;
+  static_assert(MF == 32 || !is_fp4(IN_DT), "MXFP4 runs on 32x32x64 MFMAs");
+  static_assert(C::KS >= 2 || !MASKED, "the bounds-checked path needs two slices a stage");
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wp = wave % C::WPN, wq = wave / C::WPN;
@@ -212,26 +236,27 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
   // of one 16-row block is one contiguous KiB of the AITER buffer).
   constexpr bool kAiter = IN_DT == kMXFP4A;
   constexpr bool kPAiter = kAiter && !COL_MAJOR, kQAiter = kAiter && COL_MAJOR;
-  // Fragment read offsets: row r of the operand tile, chunk (2*kk + hi).
-  // slot = (slot_base + 2*kk + hi) ^ swz8(R) = (2*kk) ^ [slot_base ^ hi ^ swz8(R)]
-  // AITER B tile: (r/16)*1024 + (2*kk + hi)*256 + (r%16)*16.
+  // Fragment read offsets: lane l reads row r = (tile base) + l%MF of the
+  // operand tile, chunk CHS*kk + hi with hi = l/MF.
+  // slot = (slot_base + CHS*kk + hi) ^ swz8(R) = (CHS*kk) ^ [slot_base ^ hi ^ swz8(R)]
+  // AITER B tile (MF = 32): (r/16)*1024 + (2*kk + hi)*256 + (r%16)*16.
   auto aiter_off = [&](uint32_t buf, uint32_t r) {
     return buf + (r >> 4) * 1024u + (lane >> 5) * 256u + (r & 15u) * 16u;
   };
   uint32_t poff[TP], pswz[TP], qoff[TQ], qswz[TQ];
 #pragma unroll
   for (int t = 0; t < TP; ++t) {
-    const uint32_t pr = wp * (TP * 32) + t * 32 + (lane & 31);
+    const uint32_t pr = wp * (TP * MF) + t * MF + (lane % MF);
     const uint32_t pR = Geo<C>::super_row(pr);
     poff[t] = kPAiter ? aiter_off(kPBuf, pr) : kPBuf + pR * 128u;
-    pswz[t] = swz8(pR) ^ Geo<C>::slot_base(pr) ^ (lane >> 5);
+    pswz[t] = swz8(pR) ^ Geo<C>::slot_base(pr) ^ (lane / MF);
   }
 #pragma unroll
   for (int t = 0; t < TQ; ++t) {
-    const uint32_t qr = wq * (TQ * 32) + t * 32 + (lane & 31);
+    const uint32_t qr = wq * (TQ * MF) + t * MF + (lane % MF);
     const uint32_t qR = Geo<C>::super_row(qr);
     qoff[t] = kQAiter ? aiter_off(kQBuf, qr) : kQBuf + qR * 128u;
-    qswz[t] = swz8(qR) ^ Geo<C>::slot_base(qr) ^ (lane >> 5);
+    qswz[t] = swz8(qR) ^ Geo<C>::slot_base(qr) ^ (lane / MF);
   }
 
   // MXFP4: offsets of this lane's P / Q tile rows in a stage's scale area.
@@ -260,7 +285,7 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       qsc[t] = aiter_sc(COL_MAJOR, wq * (TQ * 32) + t * 32 + (lane & 31));
   }
 
-  // Fragments of one 16-wide K slice: TP P tiles + TQ Q tiles, 16 bytes each
+  // Fragments of one K slice: TP P tiles + TQ Q tiles, 16 bytes each
   // (MXFP4: 64 fp4 values per slice, plus each lane's e8m0 scale byte).
   struct Frag {
     u32x4 p[TP], q[TQ];
@@ -273,7 +298,7 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
     constexpr bool kP0First = WAVE_GEMM_READ_ORDER == 1 && TP == 4 && TQ == 4;
     const int j = !kP0First ? jr : jr == 0 ? TQ : jr <= TQ ? jr - 1 : jr;
     const uint8_t *s = smem + stage * C::STAGE;
-    const uint32_t x = (uint32_t)(2 * kk);
+    const uint32_t x = (uint32_t)(C::CHS * kk);
     if (j < TQ)
       f.q[j] = *reinterpret_cast<const u32x4 *>(
           s + qoff[j] + (kQAiter ? x * 256u : ((x ^ qswz[j]) << 4)));
@@ -324,8 +349,10 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
         if constexpr (is_fp4(IN_DT))
           acc[tp][tq] = mfma_fp4_32x32x64(cur.p[tp], cur.q[tq], acc[tp][tq], cur.sp[tp],
                                           cur.sq[tq]);
-        else
+        else if constexpr (MF == 32)
           acc[tp][tq] = mfma32x32x16<IN_DT>(cur.p[tp], cur.q[tq], acc[tp][tq]);
+        else
+          mfma16x16x32_acc<IN_DT>(acc[tp][tq], cur.p[tp], cur.q[tq]);
       }
       hook(tp);
       __builtin_amdgcn_sched_barrier(0);
@@ -337,17 +364,17 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
   // stage barrier while the next stage's slice 0 is read into f[0].
   Frag f[2];
   constexpr int kLast = (C::KS - 1) & 1;
-  // The step just before a stage barrier keeps its last group free of
-  // fragment reads: the barrier's lgkmcnt(0) then finds them done.
+  // The step just before a stage barrier spreads its fragment reads over its
+  // first WAVE_GEMM_PRE_RG groups.
   auto body_h = [&](uint32_t stage, auto hook) {
 #pragma unroll
     for (int kk = 0; kk + 1 < C::KS; ++kk) {
       if (kk + 2 < C::KS)
         step(f[kk & 1], f[(kk + 1) & 1], true, stage, kk + 1,
-             [&](int tp) { hook(kk * 4 + tp); }, std::integral_constant<int, TP>{});
+             [&](int tp) { hook(kk * TP + tp); }, std::integral_constant<int, TP>{});
       else
         step(f[kk & 1], f[(kk + 1) & 1], true, stage, kk + 1,
-             [&](int tp) { hook(kk * 4 + tp); }, std::integral_constant<int, WAVE_GEMM_PRE_RG>{});
+             [&](int tp) { hook(kk * TP + tp); }, std::integral_constant<int, WAVE_GEMM_PRE_RG>{});
     }
   };
   auto body = [&](uint32_t stage) { body_h(stage, no_hook); };
@@ -435,13 +462,13 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
     };
     // Steady-state DMA schedule: the D2 issues of the prefetched stage are
     // spread over the G1 MFMA row groups before the stage barrier and (with
-    // three or more stages) the G2 = 4 groups after it: issue d follows
+    // three or more stages) the G2 = TP groups after it: issue d follows
     // group d*G/D2.  At the barrier of iteration i stage i+1 must be
     // complete; issued after it are stages i+2 .. i+NSTAGE-2 and the P
     // pre-barrier issues of stage i+NSTAGE-1, hence vmcnt(D2*(NSTAGE-3)+P).
     constexpr int D2 = kDmaPerStage;
-    constexpr int G1 = (C::KS - 1) * 4;
-    constexpr int G2 = C::NSTAGE >= 3 ? 4 : 0;
+    constexpr int G1 = (C::KS - 1) * TP;
+    constexpr int G2 = C::NSTAGE >= 3 ? TP : 0;
     constexpr int G = G1 + G2;
     constexpr int P = (G1 * D2 + G - 1) / G;  // #d with d*G/D2 < G1
     constexpr int kVm = D2 * (C::NSTAGE - 3) + P;
@@ -458,9 +485,50 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       if (s < nk)
         issue(s, kt_begin + s);
     vm_wait_barrier();
-    read_frags(f[0], 0, 0);
     uint32_t stage = 0;
     int i = 0;
+    if constexpr (C::KS == 1) {
+      // One MFMA slice per stage: each step is one barrier (stage i+1 has
+      // landed) and one MFMA pass that multiplies stage i, reads stage
+      // i+1's fragments and issues stage i+NSTAGE-1's DMA (issue d after
+      // group d * TP / D2).  The fragments alternate between f[0] and f[1],
+      // two steps per loop trip, and every step is the same code: past the
+      // last stage the DMA re-issues the last stage into the slot of stage
+      // i-1 (no later step reads it) and the last step's fragment reads
+      // land in f[] unused.  An odd stage count gets one leading step on
+      // zero fragments (stage -1), which adds exact zeros to the
+      // accumulators.
+      constexpr int kRg = WAVE_GEMM_KS1_RG > 0 ? WAVE_GEMM_KS1_RG : TP;
+      static_assert(kRg >= 1 && kRg <= TP, "read groups within the step");
+      const auto rg = std::integral_constant<int, kRg>{};
+      auto next = [&](Frag &cur, Frag &nxt) {
+        const uint32_t ahead = (stage + C::NSTAGE - 1) % C::NSTAGE;
+        const int kt_ahead = min(kt_begin + i + C::NSTAGE - 1, kt_end - 1);
+        vm_wait_barrier<kVm>();
+        stage = (stage + 1) % C::NSTAGE;
+        step(cur, nxt, true, stage, 0,
+             [&](int tp) { issue_groups(ahead, kt_ahead, tp); }, rg);
+        ++i;
+      };
+      if (nk & 1) {
+        f[0] = Frag{};
+        stage = C::NSTAGE - 1;
+        i = -1;
+      } else {
+        read_frags(f[0], 0, 0);
+      }
+      // The accumulators' zero fill is VALU: keep it 2+ wait states ahead
+      // of the first asm MFMA.
+      asm volatile("s_nop 4" ::: "memory");
+      for (int t = i; t < nk; t += 2) {
+        next(f[0], f[1]);
+        next(f[1], f[0]);
+      }
+      mfma_asm_drain();
+      vm_wait_barrier();
+      return;
+    }
+    read_frags(f[0], 0, 0);
     for (; i + C::NSTAGE - 1 < nk; ++i) {
       const uint32_t ahead = (stage + C::NSTAGE - 1) % C::NSTAGE;
       const int kt_ahead = kt_begin + i + C::NSTAGE - 1;
@@ -563,14 +631,15 @@ __device__ __forceinline__ void store_tile(const Params &p, int m0, int n0,
   const int wp = wave % C::WPN, wq = wave / C::WPN;
   const int P0 = COL_MAJOR ? m0 : n0, Q0 = COL_MAJOR ? n0 : m0;
   const int Pext = COL_MAJOR ? p.M : p.N, Qext = COL_MAJOR ? p.N : p.M;
+  constexpr int MF = C::MF;
 #pragma unroll
   for (int tq = 0; tq < C::TQ; ++tq) {
-    const int q = Q0 + wq * (C::TQ * 32) + tq * 32 + (lane & 31);
+    const int q = Q0 + wq * (C::TQ * MF) + tq * MF + (lane % MF);
 #pragma unroll
     for (int tp = 0; tp < C::TP; ++tp) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int pp = P0 + wp * (C::TP * 32) + tp * 32 + 8 * g + 4 * (lane >> 5);
+      for (int g = 0; g < C::NG; ++g) {
+        const int pp = P0 + wp * (C::TP * MF) + tp * MF + 8 * g + 4 * (lane / MF);
         const f32x4 v = get(tp, tq, g);
         const size_t idx = (size_t)q * p.ldc + pp;
         if constexpr (!MASKED) {
@@ -613,16 +682,19 @@ __device__ __forceinline__ void store_tile_lds(const Params &p, int m0, int n0, 
   const int wp = wave % C::WPN, wq = wave / C::WPN;
   const int P0 = COL_MAJOR ? m0 : n0, Q0 = COL_MAJOR ? n0 : m0;
   char *out = reinterpret_cast<char *>(p.C);
+  constexpr int MF = C::MF;
 #pragma unroll
   for (int tq = 0; tq < C::TQ; ++tq) {
-    const uint32_t r = (uint32_t)(wq * (C::TQ * 32) + tq * 32) + (lane & 31);
-    const uint32_t half = ((lane >> 5) ^ (r >> 4)) & 1u;
+    const uint32_t r = (uint32_t)(wq * (C::TQ * MF) + tq * MF) + (lane % MF);
 #pragma unroll
     for (int tp = 0; tp < C::TP; ++tp) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        // Elements wp*TP*32 + tp*32 + 8g + 4*(lane/32) .. +3 of line r.
-        const uint32_t c = wp * (C::TP * 4) + tp * 4 + g;
+      for (int g = 0; g < C::NG; ++g) {
+        // Elements e .. e+3 of line r, e = wp*TP*MF + tp*MF + 8g + 4*(lane/MF):
+        // chunk e/8, half (e/4)%2.
+        const uint32_t e = wp * (C::TP * MF) + tp * MF + 8 * g + 4 * (lane / MF);
+        const uint32_t c = e >> 3;
+        const uint32_t half = ((e >> 2) ^ (r >> 4)) & 1u;
         const f32x4 v = get(tp, tq, g);
         *reinterpret_cast<u32x2 *>(smem + r * LINE + ((c ^ (r % CH)) * 16) + half * 8) =
             u32x2{pack2<OUT_DT>(v[0], v[1]), pack2<OUT_DT>(v[2], v[3])};
@@ -650,11 +722,14 @@ __device__ __forceinline__ void store_tile_lds(const Params &p, int m0, int n0, 
 // smem: DefaultCfg::SMEM bytes of 1024-byte-aligned LDS.
 template <int IN_DT>
 using CfgFor = std::conditional_t<IN_DT == kMXFP4, Fp4Cfg,
-                                  std::conditional_t<IN_DT == kMXFP4A, Fp4ACfg, DefaultCfg>>;
+                                  std::conditional_t<IN_DT == kMXFP4A, Fp4ACfg, TileCfg>>;
 
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
 __device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *smem) {
-  using C = CfgFor<IN_DT>;
+  // Whole tiles run TileCfg's MFMA shape; ragged tiles the 32x32 one.
+  using C = std::conditional_t<MASKED, DefaultCfg, CfgFor<IN_DT>>;
+  static_assert(C::SMEM == CfgFor<IN_DT>::SMEM && C::THREADS == CfgFor<IN_DT>::THREADS,
+                "one LDS size and block size per input type");
   static_assert(!is_fp4(IN_DT) || !MASKED, "MXFP4 takes whole tiles only");
   int tm, tn;
   tile_coords(raw, p.tiles_m, p.tiles_n, p.group_m, true, tm, tn);
@@ -662,12 +737,12 @@ __device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *sme
   // derived from it) in SGPRs, as the DMA's scalar base operand requires.
   const int m0 = __builtin_amdgcn_readfirstlane(tm * kTile);
   const int n0 = __builtin_amdgcn_readfirstlane(tn * kTile);
-  f32x16 acc[C::TP][C::TQ];
+  typename C::Acc acc[C::TP][C::TQ];
 #pragma unroll
   for (int i = 0; i < C::TP; ++i)
 #pragma unroll
     for (int j = 0; j < C::TQ; ++j)
-      acc[i][j] = f32x16{};
+      acc[i][j] = typename C::Acc{};
   const int kt_n = (p.K + C::BK - 1) / C::BK;
   mainloop<C, IN_DT, COL_MAJOR, MASKED, VEC>(p, m0, n0, 0, kt_n, smem, acc);
   auto get = [&](int tp, int tq, int g) {
@@ -731,6 +806,7 @@ template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
 __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t *smem,
                                             int *arrival) {
   using C = DefaultCfg;
+  static_assert(C::MF == 32, "the partial layout below is the 32x32 accumulator's");
   const int tiles = p.tiles_m * p.tiles_n;
   const int iters = (p.K + kSKUnit - 1) / kSKUnit;
   const int ksteps = (p.K + C::BK - 1) / C::BK;  // mainloop steps per tile

@@ -39,6 +39,29 @@ __device__ __forceinline__ f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c) {
         0);
 }
 
+// v_mfma_f32_16x16x32_{f16,bf16} on an AGPR accumulator, in place:
+// D[16x16] += A[16x32] * B[32x16].  Lane l supplies A[l%16][8*(l/16) .. +8]
+// and B[8*(l/16) .. +8][l%16]; accumulator register r of lane l holds
+// D[4*(l/16) + r][l%16].  Issued from inline asm: with the builtin, hipcc
+// copies srcC into a scratch AGPR tuple for most of a 64-tile (256-AGPR)
+// accumulator grid and spills.  The compiler's hazard checks do not see an
+// asm MFMA, so the caller keeps two rules: an accumulator written by VALU
+// (its zero fill) is at least 2 wait states old when an MFMA reads it, and
+// mfma_asm_drain() separates the last MFMA from any other access to its
+// accumulators.  srcA/srcB need nothing beyond the s_waitcnt the compiler
+// inserts for their LDS loads (the MFMA reads them at issue).
+template <int DT>
+__device__ __forceinline__ void mfma16x16x32_acc(f32x4 &acc, u32x4 a, u32x4 b) {
+  if constexpr (DT == kF16)
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  else
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// 24 wait states: more than the 8-pass MFMA's result latency (passes + 3).
+__device__ __forceinline__ void mfma_asm_drain() {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+}
+
 // v_mfma_scale_f32_32x32x64_f8f6f4 with fp4 (e2m1) A and B: D[32x32] +=
 // (A * sa)[32x64] * (B * sb)[64x32].  Lane l supplies 32 fp4 values (16
 // bytes, two per byte, low nibble first) of row l%32 (A) / column l%32 (B)

@@ -66,7 +66,10 @@ def test_integration_64x96x64_seed37(wave, oracle, dev):
 @pytest.mark.parametrize("layout", ["row", "col"])
 @pytest.mark.parametrize("shape", [(256, 256, 64), (512, 768, 192), (32, 32, 64),
                                    (300, 200, 100), (1, 1, 1), (257, 513, 4100),
-                                   (130, 70, 63), (64, 96, 64)])
+                                   (130, 70, 63), (64, 96, 64),
+                                   # whole tiles with an odd number of 32-deep
+                                   # K stages (1, 3, 5)
+                                   (256, 512, 32), (512, 256, 96), (256, 256, 160)])
 def test_bucket_inputs_bit_exact(wave, oracle, dev, in_dt, out_dt, layout, shape):
     M, N, K = shape
     _, _, c, ref = run_gemm(wave, oracle, dev, M, N, K, in_dt, out_dt, layout, seed=9)
