@@ -123,8 +123,11 @@ using Fp4ACfg = Cfg<32, 4, WAVE_FP4_WAVES, 16 * 256>;
 // Logical slot lc of super-row R lives at physical slot lc ^ swz8(R), so the
 // 16 rows read together by a ds_read_b128 (one logical chunk, consecutive
 // rows) land in 16 distinct 16-byte bank groups: rocprofv3 reports
-// SQ_LDS_BANK_CONFLICT = 0 for this layout, while 64-byte rows with a
-// 2-bit swizzle measured one conflict cycle per LDS cycle.
+// SQ_LDS_BANK_CONFLICT = 0 for the 32x32 fragment reads, while 64-byte rows
+// with a 2-bit swizzle measured one conflict cycle per LDS cycle.  The
+// 16x16 fragment reads (16 rows x 4 chunks per instruction) measure 4
+// conflict cycles per 8 active cycles with this swizzle and with a variant
+// that separates chunks c, c^1 and c^2 of every 8-row group alike.
 __device__ __forceinline__ uint32_t swz8(uint32_t R) { return (R ^ (R >> 3)) & 7u; }
 
 template <class C> struct Geo {
