@@ -182,13 +182,15 @@ __device__ __forceinline__ void fwd4_cta(const Params &p, int raw, uint8_t *smem
       }
     };
     auto rowmax = [&](const f32x16 (&sc)[2]) {
-      float mx = sc[0][0];
+      float mq[4] = {sc[0][0], sc[0][1], sc[1][0], sc[1][1]};
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          mx = fmaxf(mx, sc[j][r]);
-      return fmaxf(mx, __shfl_xor(mx, 32)) * c;
+        for (int r = 2; r < 16; ++r)
+          mq[2 * j + (r & 1)] = fmaxf(mq[2 * j + (r & 1)], sc[j][r]);
+      float lo, hi;
+      half_pair(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])), lo, hi);
+      return fmaxf(lo, hi) * c;
     };
     // Lazy rescale: raise the running max only when it grows by > 8 (log2).
     auto update_max = [&](float mx) {
@@ -285,7 +287,9 @@ __device__ __forceinline__ void fwd4_cta(const Params &p, int raw, uint8_t *smem
           store_vt_rows(vb ^ 1, e, tr[0], tr[1], tr[2], tr[3]);
         __builtin_amdgcn_sched_barrier(0);
       }
-      return fmaxf(mx, __shfl_xor(mx, 32)) * c;
+      float lo, hi;
+      half_pair(mx, lo, hi);
+      return fmaxf(lo, hi) * c;
     };
 
     // ---- software pipeline over key tiles ----------------------------------
@@ -335,7 +339,9 @@ __device__ __forceinline__ void fwd4_cta(const Params &p, int raw, uint8_t *smem
     }
 
     // Normalise and store O[my_q][d], d = 32*dt + 8*(r/4) + 4*half + r%4.
-    const float total = lsum + __shfl_xor(lsum, 32);
+    float s_lo, s_hi;
+    half_pair(lsum, s_lo, s_hi);
+    const float total = s_lo + s_hi;
     const float inv = total > 0.f ? 1.0f / total : 0.f;
     if (my_q < p.seq_q) {
       uint16_t *orow = Oh + (size_t)my_q * kD + 4 * half;

@@ -352,13 +352,17 @@ __device__ __forceinline__ void fwd_pp_cta(const Params &p, int raw, uint8_t *sm
   auto softmax = [&](f32x16 (&sc)[2], int t) {
     mask(sc, t);
     if constexpr (!FIXED) {
-      float mx = sc[0][0];
+      // Four independent max chains (a short dependency path), then the
+      // other half of the row from lane l ^ 32.
+      float mq[4] = {sc[0][0], sc[0][1], sc[1][0], sc[1][1]};
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          mx = fmaxf(mx, sc[j][r]);
-      update_max(fmaxf(mx, __shfl_xor(mx, 32)) * c);
+        for (int r = 2; r < 16; ++r)
+          mq[2 * j + (r & 1)] = fmaxf(mq[2 * j + (r & 1)], sc[j][r]);
+      float lo, hi;
+      half_pair(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])), lo, hi);
+      update_max(fmaxf(lo, hi) * c);
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -478,7 +482,9 @@ __device__ __forceinline__ void fwd_pp_cta(const Params &p, int raw, uint8_t *sm
 
   // Normalise and store O[my_q][d], d = 32*dt + 8*(r/4) + 4*half + r%4.
   // Lanes l and l^32 hold the sums of complementary key halves.
-  const float total = lsum + __shfl_xor(lsum, 32);
+  float s_lo, s_hi;
+  half_pair(lsum, s_lo, s_hi);
+  const float total = s_lo + s_hi;
   const float inv = total > 0.f ? 1.0f / total : 0.f;
   if (my_q < p.seq_q) {
     uint16_t *orow = Oh + (size_t)my_q * kD + 4 * half;

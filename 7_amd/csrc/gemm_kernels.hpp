@@ -112,10 +112,14 @@ using TileCfg = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE, WAVE_GEMM_WAVES, 0, WAVE_GEM
 #ifndef WAVE_FP4_WAVES
 #define WAVE_FP4_WAVES 8
 #endif
-using Fp4Cfg = Cfg<32, 4, WAVE_FP4_WAVES, 4 * 512>;
+// MFMA shape of the MXFP4 path: 32 (32x32x64) or 16 (16x16x128).
+#ifndef WAVE_FP4_MF
+#define WAVE_FP4_MF 32
+#endif
+using Fp4Cfg = Cfg<32, 4, WAVE_FP4_WAVES, 4 * 512, WAVE_FP4_MF>;
 // MXFP4 with AITER-preshuffled B and scales: the scale area holds whole
 // 256-byte AITER scale blocks (32 rows x 8 groups), 8 for A and 8 for B.
-using Fp4ACfg = Cfg<32, 4, WAVE_FP4_WAVES, 16 * 256>;
+using Fp4ACfg = Cfg<32, 4, WAVE_FP4_WAVES, 16 * 256, WAVE_FP4_MF>;
 
 // LDS geometry of an operand tile.  The tile is stored as 128-byte
 // "super-rows" of eight 16-byte slots: with BK = 64 super-row R is tile row
@@ -224,8 +228,14 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
                                          int kt_begin, int kt_end,
                                          uint8_t *smem,
                                          typename C::Acc (&acc)[C::TP][C::TQ]) {
+  // The tile origin and K range are uniform for every caller; readfirstlane
+  // keeps them, and the DMA bases derived from them, in SGPRs (the DMA's
+  // scalar base operand) where a caller's control flow hides that (Stream-K).
+  m0 = __builtin_amdgcn_readfirstlane(m0);
+  n0 = __builtin_amdgcn_readfirstlane(n0);
+  kt_begin = __builtin_amdgcn_readfirstlane(kt_begin);
+  kt_end = __builtin_amdgcn_readfirstlane(kt_end);
   constexpr int TP = C::TP, TQ = C::TQ, NREAD = TP + TQ, MF = C::MF;
-  static_assert(MF == 32 || !is_fp4(IN_DT), "MXFP4 runs on 32x32x64 MFMAs");
   static_assert(C::KS >= 2 || !MASKED, "the bounds-checked path needs two slices a stage");
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63;
@@ -242,9 +252,9 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
   // Fragment read offsets: lane l reads row r = (tile base) + l%MF of the
   // operand tile, chunk CHS*kk + hi with hi = l/MF.
   // slot = (slot_base + CHS*kk + hi) ^ swz8(R) = (CHS*kk) ^ [slot_base ^ hi ^ swz8(R)]
-  // AITER B tile (MF = 32): (r/16)*1024 + (2*kk + hi)*256 + (r%16)*16.
+  // AITER B tile: (r/16)*1024 + (CHS*kk + hi)*256 + (r%16)*16.
   auto aiter_off = [&](uint32_t buf, uint32_t r) {
-    return buf + (r >> 4) * 1024u + (lane >> 5) * 256u + (r & 15u) * 16u;
+    return buf + (r >> 4) * 1024u + (lane / MF) * 256u + (r & 15u) * 16u;
   };
   uint32_t poff[TP], pswz[TP], qoff[TQ], qswz[TQ];
 #pragma unroll
@@ -269,23 +279,23 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
   // block covers 8 groups = two stages).
   uint32_t psc[TP], qsc[TQ];
   auto aiter_sc = [&](bool is_b, uint32_t r) {
-    return 2 * C::OPB + (is_b ? 2048u : 0u) + (r >> 5) * 256u + (lane >> 5) * 64u +
+    return 2 * C::OPB + (is_b ? 2048u : 0u) + (r >> 5) * 256u + (lane / MF) * 64u +
            (r & 15u) * 4u + ((r >> 4) & 1u);
   };
   if constexpr (IN_DT == kMXFP4) {
 #pragma unroll
     for (int t = 0; t < TP; ++t)
-      psc[t] = 2 * C::OPB + (COL_MAJOR ? 0u : 256u) + wp * (TP * 32) + t * 32 + (lane & 31);
+      psc[t] = 2 * C::OPB + (COL_MAJOR ? 0u : 256u) + wp * (TP * MF) + t * MF + (lane % MF);
 #pragma unroll
     for (int t = 0; t < TQ; ++t)
-      qsc[t] = 2 * C::OPB + (COL_MAJOR ? 256u : 0u) + wq * (TQ * 32) + t * 32 + (lane & 31);
+      qsc[t] = 2 * C::OPB + (COL_MAJOR ? 256u : 0u) + wq * (TQ * MF) + t * MF + (lane % MF);
   } else if constexpr (kAiter) {
 #pragma unroll
     for (int t = 0; t < TP; ++t)
-      psc[t] = aiter_sc(!COL_MAJOR, wp * (TP * 32) + t * 32 + (lane & 31));
+      psc[t] = aiter_sc(!COL_MAJOR, wp * (TP * MF) + t * MF + (lane % MF));
 #pragma unroll
     for (int t = 0; t < TQ; ++t)
-      qsc[t] = aiter_sc(COL_MAJOR, wq * (TQ * 32) + t * 32 + (lane & 31));
+      qsc[t] = aiter_sc(COL_MAJOR, wq * (TQ * MF) + t * MF + (lane % MF));
   }
 
   // Fragments of one K slice: TP P tiles + TQ Q tiles, 16 bytes each
@@ -309,14 +319,14 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       f.p[j - TQ] = *reinterpret_cast<const u32x4 *>(
           s + poff[j - TQ] + (kPAiter ? x * 256u : ((x ^ pswz[j - TQ]) << 4)));
     if constexpr (IN_DT == kMXFP4) {
-      // Lane half h holds the slice's 32-value group 2*kk + h.
-      const uint8_t *sg = s + (x + (lane >> 5)) * 512u;
+      // Lane part h = l/MF holds the slice's 32-value group CHS*kk + h.
+      const uint8_t *sg = s + (x + lane / MF) * 512u;
       if (j < TQ)
         f.sq[j] = sg[qsc[j]];
       else
         f.sp[j - TQ] = sg[psc[j - TQ]];
     } else if constexpr (kAiter) {
-      // Group 2*kk + h of the stage; the stage's half of the AITER block is
+      // Group CHS*kk + h of the stage; the stage's half of the AITER block is
       // kt & 1 = stage & 1 (the ring has an even number of stages).
       const uint8_t *sg = s + x * 64u + (stage & 1u) * 2u;
       if (j < TQ)
@@ -349,9 +359,11 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       }
 #pragma unroll
       for (int tq = 0; tq < TQ; ++tq) {
-        if constexpr (is_fp4(IN_DT))
+        if constexpr (is_fp4(IN_DT) && MF == 32)
           acc[tp][tq] = mfma_fp4_32x32x64(cur.p[tp], cur.q[tq], acc[tp][tq], cur.sp[tp],
                                           cur.sq[tq]);
+        else if constexpr (is_fp4(IN_DT))
+          mfma_fp4_16x16x128_acc(acc[tp][tq], cur.p[tp], cur.q[tq], cur.sp[tp], cur.sq[tq]);
         else if constexpr (MF == 32)
           acc[tp][tq] = mfma32x32x16<IN_DT>(cur.p[tp], cur.q[tq], acc[tp][tq]);
         else
@@ -721,6 +733,22 @@ __device__ __forceinline__ void store_tile_lds(const Params &p, int m0, int n0, 
   lds_barrier();
 }
 
+// Store one finished tile: 16-bit output of a whole tile goes through LDS
+// (store_tile_lds) when C allows 16-byte line runs; f32 output, twice the
+// bytes, is bound by HBM writes either way and is stored directly (measured
+// faster), as are ragged tiles.
+template <class C, int OUT_DT, bool COL_MAJOR, bool MASKED, typename Get>
+__device__ __forceinline__ void store_out(const Params &p, int m0, int n0, uint8_t *smem,
+                                          Get get) {
+  if constexpr (!MASKED && OUT_DT != kF32) {
+    if ((((uintptr_t)p.C | (uintptr_t)p.ldc * 2) & 15) == 0) {
+      store_tile_lds<C, OUT_DT, COL_MAJOR>(p, m0, n0, smem, get);
+      return;
+    }
+  }
+  store_tile<C, OUT_DT, COL_MAJOR, MASKED>(p, m0, n0, get);
+}
+
 // One 256x256 output tile: CTA `raw` of a grid of tiles_m * tiles_n CTAs.
 // smem: DefaultCfg::SMEM bytes of 1024-byte-aligned LDS.
 template <int IN_DT>
@@ -752,15 +780,7 @@ __device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *sme
     return f32x4{acc[tp][tq][4 * g], acc[tp][tq][4 * g + 1],
                  acc[tp][tq][4 * g + 2], acc[tp][tq][4 * g + 3]};
   };
-  // 16-bit output goes through LDS; f32 output, twice the bytes, is bound by
-  // HBM writes either way and is stored directly (measured faster).
-  if constexpr (!MASKED && OUT_DT != kF32) {
-    if ((((uintptr_t)p.C | (uintptr_t)p.ldc * 2) & 15) == 0) {
-      store_tile_lds<C, OUT_DT, COL_MAJOR>(p, m0, n0, smem, get);
-      return;
-    }
-  }
-  store_tile<C, OUT_DT, COL_MAJOR, MASKED>(p, m0, n0, get);
+  store_out<C, OUT_DT, COL_MAJOR, MASKED>(p, m0, n0, smem, get);
 }
 
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
@@ -808,8 +828,11 @@ __device__ __forceinline__ int sk_slot(int total, int workers, int w, int tile,
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
 __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t *smem,
                                             int *arrival) {
-  using C = DefaultCfg;
-  static_assert(C::MF == 32, "the partial layout below is the 32x32 accumulator's");
+  // Whole-tile ranges run TileCfg's MFMA shape; ragged tiles the 32x32 one.
+  using C = std::conditional_t<MASKED, DefaultCfg, TileCfg>;
+  static_assert(C::SMEM == DefaultCfg::SMEM && C::THREADS == DefaultCfg::THREADS,
+                "one LDS size and block size");
+  constexpr int NR = C::NG * 4;  // accumulator registers per MFMA tile
   const int tiles = p.tiles_m * p.tiles_n;
   const int iters = (p.K + kSKUnit - 1) / kSKUnit;
   const int ksteps = (p.K + C::BK - 1) / C::BK;  // mainloop steps per tile
@@ -819,13 +842,13 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
   const bool aligned = (total % p.workers == 0) && ((total / p.workers) % iters == 0);
 
   constexpr int TP = C::TP, TQ = C::TQ, NT = C::THREADS;
-  f32x16 acc[TP][TQ];
+  typename C::Acc acc[TP][TQ];
   auto zero = [&]() {
 #pragma unroll
     for (int i = 0; i < TP; ++i)
 #pragma unroll
       for (int j = 0; j < TQ; ++j)
-        acc[i][j] = f32x16{};
+        acc[i][j] = typename C::Acc{};
   };
   auto whole_tile = [&](int tile) {
     int tm, tn;
@@ -833,8 +856,8 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
     zero();
     mainloop<C, IN_DT, COL_MAJOR, MASKED, VEC>(p, tm * kTile, tn * kTile, 0,
                                                ksteps, smem, acc);
-    store_tile<C, OUT_DT, COL_MAJOR, MASKED>(
-        p, tm * kTile, tn * kTile, [&](int tp, int tq, int g) {
+    store_out<C, OUT_DT, COL_MAJOR, MASKED>(
+        p, tm * kTile, tn * kTile, smem, [&](int tp, int tq, int g) {
           return f32x4{acc[tp][tq][4 * g], acc[tp][tq][4 * g + 1],
                        acc[tp][tq][4 * g + 2], acc[tp][tq][4 * g + 3]};
         });
@@ -871,8 +894,8 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
 #pragma unroll
       for (int tq = 0; tq < TQ; ++tq)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          mine[((tp * TQ + tq) * 16 + r) * NT + threadIdx.x] = acc[tp][tq][r];
+        for (int r = 0; r < NR; ++r)
+          mine[((tp * TQ + tq) * NR + r) * NT + threadIdx.x] = acc[tp][tq][r];
     ++slot;
     const int first_owner = sk_owner(total, p.workers, tile * iters);
     const int last_owner = sk_owner(total, p.workers, (tile + 1) * iters - 1);
@@ -898,7 +921,7 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
 #pragma unroll
             for (int e = 0; e < 4; ++e)
               s[e] += __builtin_nontemporal_load(
-                  part + ((tp * TQ + tq) * 16 + 4 * g + e) * NT +
+                  part + ((tp * TQ + tq) * NR + 4 * g + e) * NT +
                   threadIdx.x);
           }
           return s;

@@ -77,6 +77,35 @@ __device__ __forceinline__ f32x16 mfma_fp4_32x32x64(u32x4 a, u32x4 b, f32x16 c, 
                                                          (int)sb);
 }
 
+// v_mfma_scale_f32_16x16x128_f8f6f4 with fp4 (e2m1) A and B on an AGPR
+// accumulator, in place: D[16x16] += (A * sa)[16x128] * (B * sb)[128x16].
+// Lane l supplies 32 fp4 values (16 bytes, low nibble first) of row l%16
+// (A) / column l%16 (B) at K offset 32*(l/16), and in byte 0 of sa / sb the
+// e8m0 scale of exactly those 32 values; accumulator layout as
+// mfma16x16x32_acc, and the same asm hazard rules.
+__device__ __forceinline__ void mfma_fp4_16x16x128_acc(f32x4 &acc, u32x4 a, u32x4 b,
+                                                       uint32_t sa, uint32_t sb) {
+  asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %4 op_sel_hi:[0,0,0] "
+               "cbsz:4 blgp:4"
+               : "+a"(acc)
+               : "v"(a), "v"(b), "v"(sa), "v"(sb));
+}
+
+// x from this lane (a) and from lane l ^ 32 (b), ordered by lane half: in
+// every lane a holds the lower-half lane's value and b the upper-half
+// lane's, so a + b and max(a, b) are bit-identical across the pair.  One
+// v_permlane32_swap_b32 (gfx950: swaps the upper 32 lanes of its first
+// operand with the lower 32 lanes of its second) instead of an LDS
+// permute.  Inline asm with two registers: hipcc folds the builtin's two
+// results into one register when both operands are the same value.  The
+// s_nops give the swap's VALU read/write hazards their wait states.
+__device__ __forceinline__ void half_pair(float x, float &a, float &b) {
+  uint32_t lo = __builtin_bit_cast(uint32_t, x), hi = lo;
+  asm volatile("s_nop 2\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 2" : "+v"(lo), "+v"(hi));
+  a = __builtin_bit_cast(float, lo);
+  b = __builtin_bit_cast(float, hi);
+}
+
 // 32-bit LDS byte address of a __shared__ object (address space 3).
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
   return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
