@@ -124,17 +124,26 @@ using Fp4ACfg = Cfg<32, 4, WAVE_FP4_WAVES, 16 * 256, WAVE_FP4_MF>;
 // LDS geometry of an operand tile.  The tile is stored as 128-byte
 // "super-rows" of eight 16-byte slots: with BK = 64 super-row R is tile row
 // R; with BK = 32 it holds row R in slots 0-3 and row R + 128 in slots 4-7.
-// Logical slot lc of super-row R lives at physical slot lc ^ swz8(R), so the
-// 16 rows read together by a ds_read_b128 (one logical chunk, consecutive
-// rows) land in 16 distinct 16-byte bank groups: rocprofv3 reports
-// SQ_LDS_BANK_CONFLICT = 0 for the 32x32 fragment reads, while 64-byte rows
-// with a 2-bit swizzle measured one conflict cycle per LDS cycle.  The
-// 16x16 fragment reads (16 rows x 4 chunks per instruction) measure 4
-// conflict cycles per 8 active cycles with this swizzle and with a variant
-// that separates chunks c, c^1 and c^2 of every 8-row group alike.
-__device__ __forceinline__ uint32_t swz8(uint32_t R) { return (R ^ (R >> 3)) & 7u; }
+// Logical slot lc of super-row R lives at physical slot lc ^ Geo<C>::swz(R).
+// rocprofv3 (SQ_LDS_BANK_CONFLICT, SQ_LDS_IDX_ACTIVE) on the fragment
+// reads, in the kernel and in a probe of single ds_read_b128 lane patterns:
+//  * 32x32 fragments (32 consecutive rows at one chunk) with
+//    swz_rr(R) = (R ^ R>>3) & 7: 4 LDS cycles per read, no conflict;
+//  * 16x16 fragments (16 consecutive rows x 4 chunks): 8 cycles per read,
+//    half of them conflict cycles, with every slot permutation tried
+//    (swz_rr, two others chosen to separate the chunks of each row class,
+//    no swizzle: 16).
+// swz_16(R) = 2*((R>>2)&3) + ((R>>4)&1) gives the 16x16 path no fewer LDS
+// cycles but measured 1-3 % faster than swz_rr there (8192^3 f16
+// 1282-1287 -> 1314 TFLOP/s, bf16 1353-1360 -> 1365-1382, same box), while
+// it costs 32x32 fragments a 2-way conflict; so each MFMA shape has its own.
+__device__ __forceinline__ uint32_t swz_rr(uint32_t R) { return (R ^ (R >> 3)) & 7u; }
+__device__ __forceinline__ uint32_t swz_16(uint32_t R) { return ((R >> 1) & 6u) | ((R >> 4) & 1u); }
 
 template <class C> struct Geo {
+  static __device__ __forceinline__ uint32_t swz(uint32_t R) {
+    return C::MF == 16 ? swz_16(R) : swz_rr(R);
+  }
   // (tile row, 16-byte chunk) -> (super-row, logical slot)
   static __device__ __forceinline__ uint32_t super_row(uint32_t row) {
     return C::CPR == 8 ? row : (row & 127u);
@@ -145,7 +154,7 @@ template <class C> struct Geo {
   // Inverse, for the loaders: physical slot p of super-row R holds tile row
   // row_of(R, p) chunk chunk_of(R, p).
   static __device__ __forceinline__ uint32_t logical(uint32_t R, uint32_t p) {
-    return p ^ swz8(R);
+    return p ^ swz(R);
   }
   static __device__ __forceinline__ uint32_t row_of(uint32_t R, uint32_t p) {
     return C::CPR == 8 ? R : R + 128u * (logical(R, p) >> 2);
@@ -251,7 +260,7 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
   constexpr bool kPAiter = kAiter && !COL_MAJOR, kQAiter = kAiter && COL_MAJOR;
   // Fragment read offsets: lane l reads row r = (tile base) + l%MF of the
   // operand tile, chunk CHS*kk + hi with hi = l/MF.
-  // slot = (slot_base + CHS*kk + hi) ^ swz8(R) = (CHS*kk) ^ [slot_base ^ hi ^ swz8(R)]
+  // slot = (slot_base + CHS*kk + hi) ^ swz(R) = (CHS*kk) ^ [slot_base ^ hi ^ swz(R)]
   // AITER B tile: (r/16)*1024 + (CHS*kk + hi)*256 + (r%16)*16.
   auto aiter_off = [&](uint32_t buf, uint32_t r) {
     return buf + (r >> 4) * 1024u + (lane / MF) * 256u + (r & 15u) * 16u;
@@ -262,14 +271,14 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
     const uint32_t pr = wp * (TP * MF) + t * MF + (lane % MF);
     const uint32_t pR = Geo<C>::super_row(pr);
     poff[t] = kPAiter ? aiter_off(kPBuf, pr) : kPBuf + pR * 128u;
-    pswz[t] = swz8(pR) ^ Geo<C>::slot_base(pr) ^ (lane / MF);
+    pswz[t] = Geo<C>::swz(pR) ^ Geo<C>::slot_base(pr) ^ (lane / MF);
   }
 #pragma unroll
   for (int t = 0; t < TQ; ++t) {
     const uint32_t qr = wq * (TQ * MF) + t * MF + (lane % MF);
     const uint32_t qR = Geo<C>::super_row(qr);
     qoff[t] = kQAiter ? aiter_off(kQBuf, qr) : kQBuf + qR * 128u;
-    qswz[t] = swz8(qR) ^ Geo<C>::slot_base(qr) ^ (lane / MF);
+    qswz[t] = Geo<C>::swz(qR) ^ Geo<C>::slot_base(qr) ^ (lane / MF);
   }
 
   // MXFP4: offsets of this lane's P / Q tile rows in a stage's scale area.
