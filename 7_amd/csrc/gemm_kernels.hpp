@@ -553,6 +553,8 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       return;
     }
     read_frags(f[0], 0, 0);
+    if constexpr (MF == 16)  // asm MFMAs: the one-slice path's hazard rules
+      asm volatile("s_nop 4" ::: "memory");
     for (; i + C::NSTAGE - 1 < nk; ++i) {
       const uint32_t ahead = (stage + C::NSTAGE - 1) % C::NSTAGE;
       const int kt_ahead = kt_begin + i + C::NSTAGE - 1;
@@ -577,6 +579,8 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
     }
     body(stage);
     step(f[kLast], f[0], false, 0, 0, no_hook, std::integral_constant<int, TP>{});
+    if constexpr (MF == 16)
+      mfma_asm_drain();
     vm_wait_barrier();
   } else {
     // VGPR-staged loads with bounds checks (ragged M/N/K, unaligned K);
