@@ -237,13 +237,11 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
                                          int kt_begin, int kt_end,
                                          uint8_t *smem,
                                          typename C::Acc (&acc)[C::TP][C::TQ]) {
-  // The tile origin and K range are uniform for every caller; readfirstlane
-  // keeps them, and the DMA bases derived from them, in SGPRs (the DMA's
-  // scalar base operand) where a caller's control flow hides that (Stream-K).
+  // The tile origin is uniform for every caller; readfirstlane keeps it, and
+  // the DMA bases derived from it, in SGPRs (the DMA's scalar base operand)
+  // where a caller's control flow hides that (Stream-K's ticket loop).
   m0 = __builtin_amdgcn_readfirstlane(m0);
   n0 = __builtin_amdgcn_readfirstlane(n0);
-  kt_begin = __builtin_amdgcn_readfirstlane(kt_begin);
-  kt_end = __builtin_amdgcn_readfirstlane(kt_end);
   constexpr int TP = C::TP, TQ = C::TQ, NREAD = TP + TQ, MF = C::MF;
   static_assert(C::KS >= 2 || !MASKED, "the bounds-checked path needs two slices a stage");
   const uint32_t wave = uniform(threadIdx.x >> 6);
