@@ -20,9 +20,25 @@ struct FwdArgs {
   float scale = 0.f;        // softmax scale; 0 selects 1/sqrt(head_dim)
   float qk_max_abs = 0.f;   // > 0: |Q|, |K| <= qk_max_abs, fixed-max kernel
   int waves = 8;            // 8: ping-pong kernel; 4: the 4-wave kernel
+  float *lse = nullptr;     // optional [batch][q_heads][seq_q] row log-sum-exp
 };
 
 hipError_t launch_fwd(const FwdArgs &args, hipStream_t stream);
+
+// Backward (attention_bwd.hip): dQ, dK, dV of O = softmax(scale Q K^T) V from
+// dO, O and the forward's lse.  Layouts as FwdArgs (seq_q = seq_k = seq);
+// delta: caller scratch [batch][q_heads][seq] floats.  seq % 64 == 0.
+struct BwdArgs {
+  const void *Q = nullptr, *K = nullptr, *V = nullptr, *O = nullptr, *dO = nullptr;
+  const float *lse = nullptr;  // [batch][q_heads][seq]: ln sum_k exp(scale q.k)
+  float *delta = nullptr;      // [batch][q_heads][seq] scratch
+  void *dQ = nullptr, *dK = nullptr, *dV = nullptr;
+  int batch = 1, q_heads = 1, kv_heads = 1, seq = 0;
+  int dtype = 1;
+  int causal = 0;
+  float scale = 0.f;           // 0 selects 1/sqrt(128)
+};
+hipError_t launch_bwd(const BwdArgs &args, hipStream_t stream);
 
 // flash_attention_f32 ABI: Q [block_m][head_dim] f16 already multiplied by
 // log2(e)/sqrt(head_dim), K/V [seq_n][head_dim] f16, O [block_m][head_dim]

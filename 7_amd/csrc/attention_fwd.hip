@@ -24,6 +24,7 @@ hipError_t launch_fwd(const FwdArgs &a, hipStream_t stream) {
   p.causal = a.causal;
   const float scale = a.scale > 0.f ? a.scale : 1.0f / std::sqrt((float)a.head_dim);
   p.scale_log2 = scale * kLog2e;
+  p.lse = a.lse;
   // Fixed-max mode: |s * scale| <= head_dim * qk_max_abs^2 * scale, in log2
   // units (wave_flash_attention.py:108-113 with scale = 1/sqrt(128)).
   p.fixed_max = (float)((double)kLog2e * scale * a.head_dim * a.qk_max_abs * a.qk_max_abs);

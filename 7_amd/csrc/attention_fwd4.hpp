@@ -343,6 +343,8 @@ __device__ __forceinline__ void fwd4_cta(const Params &p, int raw, uint8_t *smem
     half_pair(lsum, s_lo, s_hi);
     const float total = s_lo + s_hi;
     const float inv = total > 0.f ? 1.0f / total : 0.f;
+    if (p.lse != nullptr && half == 0 && my_q < p.seq_q)
+      p.lse[(size_t)bh * p.seq_q + my_q] = (m + __builtin_log2f(total)) * kLn2;
     if (my_q < p.seq_q) {
       uint16_t *orow = Oh + (size_t)my_q * kD + 4 * half;
 #pragma unroll

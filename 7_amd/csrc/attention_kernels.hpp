@@ -48,6 +48,7 @@ namespace wave {
 namespace attention {
 
 constexpr int kD = 128;
+constexpr float kLn2 = 0.69314718055994531f;
 constexpr int kBN = 64;                          // keys per tile
 constexpr int kKRowBytes = kD * 2;               // 256
 constexpr int kKBytes = kBN * kKRowBytes;        // 16 KiB
@@ -64,6 +65,7 @@ struct Params {
   int causal;
   float scale_log2;  // softmax scale * log2(e)
   float fixed_max;   // fixed-max kernels: the row max of every row (log2 units)
+  float *lse;        // optional [batch*q_heads][seq_q]: ln sum_k exp(scale * q.k)
 };
 
 // Linear CTA id -> (batch*head, query block).
@@ -486,6 +488,9 @@ __device__ __forceinline__ void fwd_pp_cta(const Params &p, int raw, uint8_t *sm
   half_pair(lsum, s_lo, s_hi);
   const float total = s_lo + s_hi;
   const float inv = total > 0.f ? 1.0f / total : 0.f;
+  // sum_k 2^(c*s_k) = total * 2^m, so ln sum_k e^(scale*s_k) = (m + log2 total) ln 2.
+  if (p.lse != nullptr && half == 0 && my_q < p.seq_q)
+    p.lse[(size_t)bh * p.seq_q + my_q] = (m + __builtin_log2f(total)) * kLn2;
   if (my_q < p.seq_q) {
     uint16_t *orow = Oh + (size_t)my_q * kD + 4 * half;
 #pragma unroll

@@ -274,7 +274,7 @@ int check_qk_bound(float qk_max_abs, float scale, int head_dim, int dtype) {
 
 int fa_fwd(const void *Q, const void *K, const void *V, void *O, int batch, int q_heads,
            int kv_heads, int seq, int head_dim, int dtype, int causal, float scale,
-           float qk_max_abs, int waves, void *stream, const char *name) {
+           float qk_max_abs, int waves, void *stream, const char *name, float *lse = nullptr) {
   if (waves != 4 && waves != 8)
     return fail(WAVE_ERR_INVALID, "fa: waves=%d must be 4 or 8", waves);
   if (!Q || !K || !V || !O)
@@ -315,9 +315,74 @@ int fa_fwd(const void *Q, const void *K, const void *V, void *O, int batch, int 
   a.scale = scale;
   a.qk_max_abs = qk_max_abs;
   a.waves = waves;
+  a.lse = lse;
   return hip_status(wave::attention::launch_fwd(a, static_cast<hipStream_t>(stream)), name);
 }
 } // namespace
+
+int wave_fa_fwd_lse_launch(const void *Q, const void *K, const void *V, void *O, float *lse,
+                           int batch, int q_heads, int kv_heads, int seq, int head_dim,
+                           int dtype, int causal, float scale, void *stream) {
+  if (!lse)
+    return fail(WAVE_ERR_INVALID, "wave_fa_fwd_lse_launch: null lse");
+  if (reinterpret_cast<uintptr_t>(lse) & 15)
+    return fail(WAVE_ERR_INVALID, "wave_fa_fwd_lse_launch: lse must be 16-byte aligned");
+  return fa_fwd(Q, K, V, O, batch, q_heads, kv_heads, seq, head_dim, dtype, causal, scale, 0.f,
+                8, stream, "wave_fa_fwd_lse_launch", lse);
+}
+
+int wave_fa_bwd_launch(const void *Q, const void *K, const void *V, const void *O,
+                       const void *dO, const float *lse, float *delta, void *dQ, void *dK,
+                       void *dV, int batch, int q_heads, int kv_heads, int seq, int head_dim,
+                       int dtype, int causal, float scale, void *stream) {
+  if (!Q || !K || !V || !O || !dO || !lse || !delta || !dQ || !dK || !dV)
+    return fail(WAVE_ERR_INVALID, "fa_bwd: null pointer argument");
+  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || seq <= 0)
+    return fail(WAVE_ERR_INVALID, "fa_bwd: batch=%d q_heads=%d kv_heads=%d seq=%d must be positive",
+                batch, q_heads, kv_heads, seq);
+  if (q_heads % kv_heads != 0)
+    return fail(WAVE_ERR_INVALID, "fa_bwd: q_heads=%d not a multiple of kv_heads=%d", q_heads,
+                kv_heads);
+  if (!is_in_dtype(dtype))
+    return fail(WAVE_ERR_INVALID, "fa_bwd: dtype %d is not f16/bf16", dtype);
+  if (causal != 0 && causal != 1)
+    return fail(WAVE_ERR_INVALID, "fa_bwd: causal=%d must be 0 or 1", causal);
+  if (!(scale >= 0.f) || scale != scale)
+    return fail(WAVE_ERR_INVALID, "fa_bwd: scale must be >= 0");
+  if (head_dim != 128)
+    return fail(WAVE_ERR_UNSUPPORTED, "fa_bwd: head_dim=%d (only 128 is built)", head_dim);
+  if (seq % 64 != 0)
+    return fail(WAVE_ERR_UNSUPPORTED, "fa_bwd: seq=%d must be a multiple of 64", seq);
+  if ((int64_t)batch * q_heads * seq > INT32_MAX / 2)
+    return fail(WAVE_ERR_UNSUPPORTED, "fa_bwd: problem too large");
+  const uintptr_t bits = reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(K) |
+                         reinterpret_cast<uintptr_t>(V) | reinterpret_cast<uintptr_t>(O) |
+                         reinterpret_cast<uintptr_t>(dO) | reinterpret_cast<uintptr_t>(lse) |
+                         reinterpret_cast<uintptr_t>(delta) | reinterpret_cast<uintptr_t>(dQ) |
+                         reinterpret_cast<uintptr_t>(dK) | reinterpret_cast<uintptr_t>(dV);
+  if (bits & 15)
+    return fail(WAVE_ERR_INVALID, "fa_bwd: every buffer must be 16-byte aligned");
+  wave::attention::BwdArgs a;
+  a.Q = Q;
+  a.K = K;
+  a.V = V;
+  a.O = O;
+  a.dO = dO;
+  a.lse = lse;
+  a.delta = delta;
+  a.dQ = dQ;
+  a.dK = dK;
+  a.dV = dV;
+  a.batch = batch;
+  a.q_heads = q_heads;
+  a.kv_heads = kv_heads;
+  a.seq = seq;
+  a.dtype = dtype;
+  a.causal = causal;
+  a.scale = scale;
+  return hip_status(wave::attention::launch_bwd(a, static_cast<hipStream_t>(stream)),
+                    "wave_fa_bwd_launch");
+}
 
 int wave_fa_fwd_launch(const void *Q, const void *K, const void *V, void *O,
                        int batch, int q_heads, int kv_heads, int seq,

@@ -197,6 +197,57 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     return out
 
 
+def _fa_shapes(q, k, v):
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _need(t, n)
+        if t.dim() != 4:
+            raise ValueError(f"{n} must be [batch, heads, seq, head_dim]")
+    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("q, k, v must share an f16 or bf16 dtype")
+    B, Hq, S, D = q.shape
+    if k.shape != v.shape or k.shape[0] != B or k.shape[2] != S or k.shape[3] != D:
+        raise ValueError("k and v must be [batch, kv_heads, seq, head_dim]")
+    return B, Hq, k.shape[1], S, D
+
+
+def flash_attention_lse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
+                        causal: bool = False, scale: float | None = None
+                        ) -> tuple[torch.Tensor, torch.Tensor]:
+    """The online-softmax forward plus each row's log-sum-exp
+    lse[b, h, q] = ln sum_k exp(scale * q.k) (float32), for flash_attention_bwd
+    (wave_fa_fwd_lse_launch)."""
+    B, Hq, Hkv, S, D = _fa_shapes(q, k, v)
+    out = torch.empty_like(q)
+    lse = torch.empty((B, Hq, S), dtype=torch.float32, device=q.device)
+    rt.check(rt.lib().wave_fa_fwd_lse_launch(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(), B, Hq, Hkv, S,
+        D, _DT[q.dtype], int(causal), float(scale or 0.0), _stream(q)))
+    return out, lse
+
+
+def flash_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+                        do: torch.Tensor, lse: torch.Tensor, *, causal: bool = False,
+                        scale: float | None = None
+                        ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """dQ, dK, dV of O = softmax(scale Q K^T) V given dO, O and the forward's
+    lse (flash_attention_lse); wave_fa_bwd_launch.  seq % 64 == 0."""
+    B, Hq, Hkv, S, D = _fa_shapes(q, k, v)
+    for t, n in ((o, "o"), (do, "do")):
+        _need(t, n)
+        if t.shape != q.shape or t.dtype != q.dtype:
+            raise ValueError(f"{n} must match q")
+    _need(lse, "lse")
+    if lse.dtype != torch.float32 or tuple(lse.shape) != (B, Hq, S):
+        raise ValueError("lse must be float32 [batch, q_heads, seq]")
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    delta = torch.empty((B, Hq, S), dtype=torch.float32, device=q.device)
+    rt.check(rt.lib().wave_fa_bwd_launch(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), lse.data_ptr(),
+        delta.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, Hq, Hkv, S, D,
+        _DT[q.dtype], int(causal), float(scale or 0.0), _stream(q)))
+    return dq, dk, dv
+
+
 def flash_attention_f32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                         out: torch.Tensor | None = None) -> torch.Tensor:
     """The flash_attention_f32 ABI: q [block_m, D] f16 pre-scaled by

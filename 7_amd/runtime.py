@@ -39,6 +39,9 @@ _SIGNATURES = {
     "wave_fa_fwd_config_launch": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _F, _I,
                                        _P]),
     "wave_fa_f32_launch": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    "wave_fa_fwd_lse_launch": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P]),
+    "wave_fa_bwd_launch": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,
+                                _I, _I, _F, _P]),
     "wave_status_string": (ctypes.c_char_p, [_I]),
     "wave_last_error": (ctypes.c_char_p, []),
     "wave_device_mfma_peak": (_I, [_I, ctypes.POINTER(ctypes.c_double),

@@ -169,6 +169,29 @@ int wave_fa_fwd_config_launch(const void *Q, const void *K, const void *V, void 
                               int head_dim, int dtype, int causal, float scale,
                               float qk_max_abs, int waves, void *stream);
 
+/* The online-softmax forward of wave_fa_fwd_launch that also writes each
+ * query row's log-sum-exp, lse[b][h][q] = ln sum_k exp(scale * Q[q].K[k])
+ * over the unmasked keys (float32, 16-byte aligned), for the backward below.
+ * No counterpart in the reference (its forward returns O only); the lse
+ * convention is flash-attention's. */
+int wave_fa_fwd_lse_launch(const void *Q, const void *K, const void *V, void *O, float *lse,
+                           int batch, int q_heads, int kv_heads, int seq, int head_dim,
+                           int dtype, int causal, float scale, void *stream);
+
+/* ---- flash-attention backward --------------------------------------------
+ * dQ, dK, dV of O = softmax(scale * Q K^T) V (causal and GQA as the forward;
+ * dK, dV sum over the q heads of each KV head) from dO, O and the lse of
+ * wave_fa_fwd_lse_launch: P = exp(scale Q K^T - lse), dV = P^T dO,
+ * dS = P o (dO V^T - rowsum(dO o O)), dQ = scale dS K, dK = scale dS^T Q,
+ * fp32 accumulation, one rounding to dtype.  Layouts as the forward; delta is
+ * caller scratch of batch * q_heads * seq floats.  Requires seq % 64 == 0,
+ * head_dim 128 and 16-byte aligned buffers.  The reference has no backward:
+ * no counterpart to replace. */
+int wave_fa_bwd_launch(const void *Q, const void *K, const void *V, const void *O,
+                       const void *dO, const float *lse, float *delta, void *dQ, void *dK,
+                       void *dV, int batch, int q_heads, int kv_heads, int seq, int head_dim,
+                       int dtype, int causal, float scale, void *stream);
+
 /* ---- flash_attention_f32 ------------------------------------------------
  * Replaces `flash_attention_f32(Q, K, V, O)` (wave_attention.py:1406-1441;
  * wave-fa-calibrate-runner.cpp:346-361): Q [block_m][head_dim] f16

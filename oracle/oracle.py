@@ -308,3 +308,45 @@ def streamk_worker_segments(tile_count: int, k_iterations: int, workers: int, wo
         raise ValueError("bad Stream-K segment arguments")
     return [(int(t[i]), int(kb[i]), int(ke[i]), None if sl[i] < 0 else int(sl[i]))
             for i in range(n)]
+
+
+def fa_backward(q, k, v, do, *, scale: float | None = None, causal: bool = False,
+                o_delta=None):
+    """Float64 flash-attention forward and backward for q [B, Hq, S, D], k/v
+    [B, Hkv, S, D], do [B, Hq, S, D] (arrays of the dtype-rounded values).
+
+    Returns (o, lse, dq, dk, dv): o = softmax(scale Q K^T) V with key > query
+    masked when causal, lse = ln sum_k exp(scale q.k) per row, and the
+    gradients dV = P^T dO, dS = P o (dO V^T - rowsum(dO o O)), dQ = scale dS K,
+    dK = scale dS^T Q, with dK and dV summed over the q heads of each KV head.
+    No reference counterpart (the reference has no backward): these are the
+    textbook gradients of softmax attention, pinned against torch autograd
+    in tests/test_oracle_fa_bwd.py.  o_delta: the O to use in
+    rowsum(dO o O) (a kernel's own rounded output), default the exact one."""
+    q, k, v, do = (np.asarray(x, dtype=np.float64) for x in (q, k, v, do))
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    g = Hq // Hkv
+    sc = 1.0 / np.sqrt(D) if not scale else float(scale)
+    kk = np.repeat(k, g, axis=1)
+    vv = np.repeat(v, g, axis=1)
+    s = sc * np.einsum("bhqd,bhkd->bhqk", q, kk)
+    if causal:
+        mask = np.triu(np.ones((S, S), dtype=bool), 1)
+        s = np.where(mask, -np.inf, s)
+    m = s.max(axis=-1, keepdims=True)
+    e = np.exp(s - m)
+    tot = e.sum(axis=-1, keepdims=True)
+    p = e / tot
+    lse = (m + np.log(tot))[..., 0]
+    o = np.einsum("bhqk,bhkd->bhqd", p, vv)
+    dvv = np.einsum("bhqk,bhqd->bhkd", p, do)
+    dp = np.einsum("bhqd,bhkd->bhqk", do, vv)
+    o_d = o if o_delta is None else np.asarray(o_delta, dtype=np.float64)
+    delta = (do * o_d).sum(axis=-1, keepdims=True)
+    ds = p * (dp - delta)
+    dq = sc * np.einsum("bhqk,bhkd->bhqd", ds, kk)
+    dkk = sc * np.einsum("bhqk,bhqd->bhkd", ds, q)
+    dk = dkk.reshape(B, Hkv, g, S, D).sum(axis=2)
+    dv = dvv.reshape(B, Hkv, g, S, D).sum(axis=2)
+    return o, lse, dq, dk, dv
