@@ -251,6 +251,23 @@ def main():
                           "value": round(fa_tf, 2), "unit": "TFLOP/s",
                           "ms_per_step": round(fa_ms, 4),
                           "frac_of_mfma_peak": round(fa_tf / MFMA_PEAK_TFLOPS, 4)})
+        if args.workload == "all":
+            # Backward (no reference counterpart) on the same shape: delta,
+            # dK/dV and dQ kernels; FLOPs counted as flash-attention does,
+            # 2.5 x the forward's (five S x S x D products).
+            o, lse = wave.flash_attention_lse(q, k, v)
+            do = torch.randn((B, H, S, D), generator=gq).to(torch.float16).to(dev)
+            bw_ms = time_launches(lambda: wave.flash_attention_bwd(q, k, v, o, do, lse), 5, 1,
+                                  torch)
+            bw_tf = 10.0 * B * H * S * S * D / (bw_ms * 1e-3) / 1e12
+            log(f"fa bwd f16 B4 H32 S4096 D128: {bw_ms * 1e3:.1f} us/launch, {bw_tf:.1f} TFLOP/s "
+                f"({100 * bw_tf / MFMA_PEAK_TFLOPS:.1f}%)")
+            secondary.append({"workload": "fa_bwd_f16_b4_h32_s4096_d128_noncausal",
+                              "value": round(bw_tf, 2), "unit": "TFLOP/s",
+                              "ms_per_step": round(bw_ms, 4),
+                              "frac_of_mfma_peak": round(bw_tf / MFMA_PEAK_TFLOPS, 4),
+                              "flops": "10*B*H*S^2*D"})
+            del do, lse
         del q, k, v, o
 
     if args.workload == "all" and not args.no_ref_compare:
