@@ -21,13 +21,16 @@
 //  * bwd_q_kernel: one CTA per 64-query block of one q head; it loops over
 //    the key blocks (causal: up to the diagonal) and accumulates dQ.
 // Every product is an "NT" product C[m][n] = sum_k A[m][k] B[n][k] of 32x32
-// tiles on v_mfma_f32_32x32x16 with both operands read as 16-byte row chunks
-// from LDS; the operands that the products need K-contiguous the other way
-// (Q^T, dO^T, K^T) are written to LDS transposed when a block is loaded, and
-// P^T / dS^T (dS for dQ) go through LDS between the score products and the
-// gradient products.  LDS rows are padded by 16 bytes (272 B for 128-element
-// rows, 144 B for 64-element rows) so the 32 rows a fragment read touches
-// start in different bank groups.
+// tiles on v_mfma_f32_32x32x16.  The operands fixed for a CTA (K, V in the
+// dK/dV kernel; Q, dO in the dQ kernel) are held as MFMA fragments in
+// registers; the rest are read as 16-byte row chunks from LDS.  Operands
+// needed K-contiguous the other way (Q^T, dO^T, K^T) are written to LDS
+// transposed when a block is loaded, and P^T / dS^T (dS for dQ) go through
+// LDS between the score products and the gradient products.  LDS tiles are
+// unpadded with XOR-swizzled 16-byte chunks (256-byte rows: chunk c of row
+// r at c ^ (r % 16); 128-byte rows: at c ^ ((r / 2) % 8)), so that 16
+// consecutive rows read at one chunk cover all 16 bank groups: 80 KiB
+// (dK/dV) and 56 KiB (dQ) of LDS, two CTAs per CU.
 #include "attention.hpp"
 #include "wave_common.hpp"
 
@@ -38,12 +41,18 @@ namespace {
 
 constexpr int kBD = 128;               // head dim
 constexpr int kBlk = 64;               // query or key rows per block
-constexpr int kRP = kBD * 2 + 16;      // 272: pitch of a [64][128] row tile
-constexpr int kTP = kBlk * 2 + 16;     // 144: pitch of [128][64] and [64][64] tiles
-constexpr int kRowTile = kBlk * kRP;   // 17408 bytes
-constexpr int kColTile = kBD * kTP;    // 18432 bytes
-constexpr int kSqTile = kBlk * kTP;    // 9216 bytes
+constexpr int kWide = kBlk * 256;      // [64][128] 16-bit tile: 16 KiB
+constexpr int kNarrowT = kBD * 128;    // [128][64] tile: 16 KiB
+constexpr int kNarrowS = kBlk * 128;   // [64][64] tile: 8 KiB
 constexpr float kLog2eB = 1.4426950408889634f;
+
+// Byte offset of (row r, byte b) in a tile of ROWB-byte rows.
+template <int ROWB> __device__ __forceinline__ uint32_t swz(uint32_t r) {
+  return ROWB == 256 ? (r & 15u) : ((r >> 1) & 7u);
+}
+template <int ROWB> __device__ __forceinline__ uint32_t toff(uint32_t r, uint32_t b) {
+  return r * ROWB + ((((b >> 4) ^ swz<ROWB>(r))) << 4) + (b & 15u);
+}
 
 struct BwdParams {
   const uint16_t *Q, *K, *V, *O, *dO;
@@ -56,24 +65,45 @@ struct BwdParams {
   float scale_log2;   // scale * log2(e)
 };
 
-// acc += A[32 rows][K] * B[32 rows][K]^T, K = 16 * NK, both row-major in LDS
-// with the given pitch (bytes), 16-bit elements.
-template <int DT, int NK>
-__device__ __forceinline__ void mma_nt(f32x16 &acc, const uint8_t *A, int pa, const uint8_t *B,
-                                       int pb) {
-  const uint32_t lane = threadIdx.x & 63;
-  const uint8_t *ar = A + (lane & 31) * pa + (lane >> 5) * 16;
-  const uint8_t *br = B + (lane & 31) * pb + (lane >> 5) * 16;
+// acc += A[32 rows][K] * B^T with A rows a0 .. a0+31 of a ROWB-byte-row LDS
+// tile, K = 16 * NK, and B as per-slice register fragments bf[kk] (lane l:
+// row l % 32 of B, elements 16 kk + 8 (l / 32) .. +8) (mma_nt_reg) or as
+// rows b0 .. b0+31 of an LDS tile of the same row size (mma_nt_lds).
+template <int DT, int NK, int ROWB>
+__device__ __forceinline__ void mma_nt_reg(f32x16 &acc, const uint8_t *A, uint32_t a0,
+                                           const u32x4 (&bf)[NK]) {
+  const uint32_t lane = threadIdx.x & 63, ra = a0 + (lane & 31);
+  const uint32_t s = (lane >> 5) ^ swz<ROWB>(ra);
 #pragma unroll
   for (int kk = 0; kk < NK; ++kk) {
-    const u32x4 a = *reinterpret_cast<const u32x4 *>(ar + 32 * kk);
-    const u32x4 b = *reinterpret_cast<const u32x4 *>(br + 32 * kk);
+    const u32x4 a = *reinterpret_cast<const u32x4 *>(A + ra * ROWB + (((2u * kk) ^ s) << 4));
+    acc = mfma32x32x16<DT>(a, bf[kk], acc);
+  }
+}
+template <int DT, int NK, int ROWB>
+__device__ __forceinline__ void mma_nt_lds(f32x16 &acc, const uint8_t *A, uint32_t a0,
+                                           const uint8_t *B, uint32_t b0) {
+  const uint32_t lane = threadIdx.x & 63, ra = a0 + (lane & 31), rb = b0 + (lane & 31);
+  const uint32_t sa = (lane >> 5) ^ swz<ROWB>(ra), sb = (lane >> 5) ^ swz<ROWB>(rb);
+#pragma unroll
+  for (int kk = 0; kk < NK; ++kk) {
+    const u32x4 a = *reinterpret_cast<const u32x4 *>(A + ra * ROWB + (((2u * kk) ^ sa) << 4));
+    const u32x4 b = *reinterpret_cast<const u32x4 *>(B + rb * ROWB + (((2u * kk) ^ sb) << 4));
     acc = mfma32x32x16<DT>(a, b, acc);
   }
 }
 
-// Load a [64][128] block of rows (row stride 128 elements) into LDS row-major
-// (pitch kRP) and, when T != nullptr, transposed ([128][64], pitch kTP).
+// MFMA fragments of 32 rows of a [rows][128] global block (row0 = the
+// lane's row): lane l holds elements 16 kk + 8 (l / 32) .. +8 for kk < 8.
+__device__ __forceinline__ void load_frags(const uint16_t *row, u32x4 (&f)[8]) {
+  const uint32_t lane = threadIdx.x & 63;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk)
+    f[kk] = *reinterpret_cast<const u32x4 *>(row + 16 * kk + 8 * (lane >> 5));
+}
+
+// Load a [64][128] block of rows (row stride 128 elements) into LDS (wide
+// tile R) and, when T != nullptr, transposed ([128][64] narrow tile T).
 // Thread t handles row pairs x 16-byte chunks: unit u = t + 256*i, row pair
 // u / 16, chunk u % 16.
 __device__ __forceinline__ void load_block(const uint16_t *src, uint8_t *R, uint8_t *T) {
@@ -83,15 +113,15 @@ __device__ __forceinline__ void load_block(const uint16_t *src, uint8_t *R, uint
     const uint32_t u = t + 256u * i, rp = u >> 4, c = u & 15u;
     const u32x4 a = *reinterpret_cast<const u32x4 *>(src + (size_t)(2 * rp) * kBD + 8 * c);
     const u32x4 b = *reinterpret_cast<const u32x4 *>(src + (size_t)(2 * rp + 1) * kBD + 8 * c);
-    *reinterpret_cast<u32x4 *>(R + (2 * rp) * kRP + 16 * c) = a;
-    *reinterpret_cast<u32x4 *>(R + (2 * rp + 1) * kRP + 16 * c) = b;
+    *reinterpret_cast<u32x4 *>(R + toff<256>(2 * rp, 16 * c)) = a;
+    *reinterpret_cast<u32x4 *>(R + toff<256>(2 * rp + 1, 16 * c)) = b;
     if (T != nullptr) {
       // Element d = 8c + e of rows 2rp, 2rp+1 -> T[8c + e][2rp .. 2rp+1].
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        *reinterpret_cast<uint32_t *>(T + (8 * c + 2 * e) * kTP + 4 * rp) =
+        *reinterpret_cast<uint32_t *>(T + toff<128>(8 * c + 2 * e, 4 * rp)) =
             __builtin_amdgcn_perm(b[e], a[e], 0x05040100u);
-        *reinterpret_cast<uint32_t *>(T + (8 * c + 2 * e + 1) * kTP + 4 * rp) =
+        *reinterpret_cast<uint32_t *>(T + toff<128>(8 * c + 2 * e + 1, 4 * rp)) =
             __builtin_amdgcn_perm(b[e], a[e], 0x07060302u);
       }
     }
@@ -139,25 +169,26 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(BwdParams p, int rows) {
 
 // dK, dV of one 64-key block of one KV head.
 template <int DT, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void bwd_kv_kernel(BwdParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[4 * kRowTile + 2 * kColTile + 2 * kSqTile];
-  uint8_t *sK = smem, *sV = sK + kRowTile, *sQ = sV + kRowTile, *sdO = sQ + kRowTile;
-  uint8_t *sQt = sdO + kRowTile, *sdOt = sQt + kColTile;
-  uint8_t *sPt = sdOt + kColTile, *sdSt = sPt + kSqTile;
+__global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kWide + 2 * kNarrowT + 2 * kNarrowS];
+  uint8_t *sQ = smem, *sdO = sQ + kWide, *sQt = sdO + kWide, *sdOt = sQt + kNarrowT;
+  uint8_t *sPt = sdOt + kNarrowT, *sdSt = sPt + kNarrowS;
   const int nb = p.seq / kBlk;
   const int kb = (int)blockIdx.x % nb, bhk = (int)blockIdx.x / nb;
   const int b = bhk / p.kv_heads, hkv = bhk - b * p.kv_heads;
   const int group = p.q_heads / p.kv_heads;
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const size_t kv_off = ((size_t)bhk * p.seq + (size_t)kb * kBlk) * kBD;
-  load_block(p.K + kv_off, sK, nullptr);
-  load_block(p.V + kv_off, sV, nullptr);
 
   // Score tiles: wave w computes S[q][key] for q half w&1, key half w>>1;
   // lane l holds key kh2*32 + l%32 and queries qh2*32 + 8g + 4(l/32) + e.
   const int qh2 = wave & 1, kh2 = wave >> 1;
   // Gradient tiles: key half w&1, d quarters 2(w>>1), 2(w>>1)+1.
   const int kh = wave & 1, dq = wave >> 1;
+  // K and V rows of this wave's key half as B fragments, for the whole CTA.
+  u32x4 kf[8], vf[8];
+  load_frags(p.K + kv_off + (size_t)(kh2 * 32 + (lane & 31)) * kBD, kf);
+  load_frags(p.V + kv_off + (size_t)(kh2 * 32 + (lane & 31)) * kBD, vf);
   f32x16 dv[2] = {f32x16{}, f32x16{}}, dk[2] = {f32x16{}, f32x16{}};
   const int key = kb * kBlk + kh2 * 32 + (int)(lane & 31);
   for (int hq = hkv * group; hq < (hkv + 1) * group; ++hq) {
@@ -182,8 +213,8 @@ __global__ __launch_bounds__(256, 1) void bwd_kv_kernel(BwdParams p) {
       }
       __syncthreads();
       f32x16 s = {}, dp = {};
-      mma_nt<DT, 8>(s, sQ + qh2 * 32 * kRP, kRP, sK + kh2 * 32 * kRP, kRP);
-      mma_nt<DT, 8>(dp, sdO + qh2 * 32 * kRP, kRP, sV + kh2 * 32 * kRP, kRP);
+      mma_nt_reg<DT, 8, 256>(s, sQ, qh2 * 32, kf);
+      mma_nt_reg<DT, 8, 256>(dp, sdO, qh2 * 32, vf);
       // P and dS; P^T / dS^T rows = keys, 4 consecutive queries per store.
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -198,7 +229,8 @@ __global__ __launch_bounds__(256, 1) void bwd_kv_kernel(BwdParams p) {
           pv[e] = pr;
           dsv[e] = pr * (dp[r] - dl[r]);
         }
-        const uint32_t off = (kh2 * 32 + (lane & 31)) * kTP + 2 * (qh2 * 32 + 8 * g + 4 * (lane >> 5));
+        const uint32_t off =
+            toff<128>(kh2 * 32 + (lane & 31), 2 * (qh2 * 32 + 8 * g + 4 * (lane >> 5)));
         *reinterpret_cast<u32x2 *>(sPt + off) = u32x2{pack2<DT>(pv[0], pv[1]), pack2<DT>(pv[2], pv[3])};
         *reinterpret_cast<u32x2 *>(sdSt + off) =
             u32x2{pack2<DT>(dsv[0], dsv[1]), pack2<DT>(dsv[2], dsv[3])};
@@ -206,8 +238,8 @@ __global__ __launch_bounds__(256, 1) void bwd_kv_kernel(BwdParams p) {
       __syncthreads();
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        mma_nt<DT, 4>(dv[t], sPt + kh * 32 * kTP, kTP, sdOt + (2 * dq + t) * 32 * kTP, kTP);
-        mma_nt<DT, 4>(dk[t], sdSt + kh * 32 * kTP, kTP, sQt + (2 * dq + t) * 32 * kTP, kTP);
+        mma_nt_lds<DT, 4, 128>(dv[t], sPt, kh * 32, sdOt, (2 * dq + t) * 32);
+        mma_nt_lds<DT, 4, 128>(dk[t], sdSt, kh * 32, sQt, (2 * dq + t) * 32);
       }
     }
   }
@@ -221,23 +253,24 @@ __global__ __launch_bounds__(256, 1) void bwd_kv_kernel(BwdParams p) {
 
 // dQ of one 64-query block of one q head.
 template <int DT, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void bwd_q_kernel(BwdParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[4 * kRowTile + kColTile + kSqTile];
-  uint8_t *sQ = smem, *sdO = sQ + kRowTile, *sK = sdO + kRowTile, *sV = sK + kRowTile;
-  uint8_t *sKt = sV + kRowTile, *sdS = sKt + kColTile;
+__global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kWide + kNarrowT + kNarrowS];
+  uint8_t *sK = smem, *sV = sK + kWide, *sKt = sV + kWide, *sdS = sKt + kNarrowT;
   const int nb = p.seq / kBlk;
   const int qb = (int)blockIdx.x % nb, bh = (int)blockIdx.x / nb;
   const int b = bh / p.q_heads, hq = bh - b * p.q_heads;
   const int hkv = hq / (p.q_heads / p.kv_heads);
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const size_t q_off = ((size_t)bh * p.seq + (size_t)qb * kBlk) * kBD;
-  load_block(p.Q + q_off, sQ, nullptr);
-  load_block(p.dO + q_off, sdO, nullptr);
   // Score tiles: wave w computes S^T[key][q] for key half w&1, q half w>>1;
   // lane l holds query qh2*32 + l%32 and keys kh2*32 + 8g + 4(l/32) + e.
   const int kh2 = wave & 1, qh2 = wave >> 1;
   // dQ tiles: q half w&1, d quarters 2(w>>1), 2(w>>1)+1.
   const int qh = wave & 1, dq = wave >> 1;
+  // Q and dO rows of this wave's query half as B fragments, for the whole CTA.
+  u32x4 qf[8], dof[8];
+  load_frags(p.Q + q_off + (size_t)(qh2 * 32 + (lane & 31)) * kBD, qf);
+  load_frags(p.dO + q_off + (size_t)(qh2 * 32 + (lane & 31)) * kBD, dof);
   const int q = qb * kBlk + qh2 * 32 + (int)(lane & 31);
   const size_t row = (size_t)bh * p.seq + q;
   const float l2 = p.lse[row] * kLog2eB, dl = p.delta[row];
@@ -250,8 +283,8 @@ __global__ __launch_bounds__(256, 1) void bwd_q_kernel(BwdParams p) {
     load_block(p.V + kv_base + (size_t)kb * kBlk * kBD, sV, nullptr);
     __syncthreads();
     f32x16 st = {}, dpt = {};
-    mma_nt<DT, 8>(st, sK + kh2 * 32 * kRP, kRP, sQ + qh2 * 32 * kRP, kRP);
-    mma_nt<DT, 8>(dpt, sV + kh2 * 32 * kRP, kRP, sdO + qh2 * 32 * kRP, kRP);
+    mma_nt_reg<DT, 8, 256>(st, sK, kh2 * 32, qf);
+    mma_nt_reg<DT, 8, 256>(dpt, sV, kh2 * 32, dof);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       float dsv[4];
@@ -265,14 +298,15 @@ __global__ __launch_bounds__(256, 1) void bwd_q_kernel(BwdParams p) {
         dsv[e] = pr * (dpt[r] - dl);
       }
       // dS row q, 4 consecutive keys.
-      const uint32_t off = (qh2 * 32 + (lane & 31)) * kTP + 2 * (kh2 * 32 + 8 * g + 4 * (lane >> 5));
+      const uint32_t off =
+          toff<128>(qh2 * 32 + (lane & 31), 2 * (kh2 * 32 + 8 * g + 4 * (lane >> 5)));
       *reinterpret_cast<u32x2 *>(sdS + off) =
           u32x2{pack2<DT>(dsv[0], dsv[1]), pack2<DT>(dsv[2], dsv[3])};
     }
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < 2; ++t)
-      mma_nt<DT, 4>(dqa[t], sdS + qh * 32 * kTP, kTP, sKt + (2 * dq + t) * 32 * kTP, kTP);
+      mma_nt_lds<DT, 4, 128>(dqa[t], sdS, qh * 32, sKt, (2 * dq + t) * 32);
   }
   uint16_t *dQ = p.dQ + q_off;
 #pragma unroll
