@@ -63,6 +63,7 @@ struct BwdParams {
   int causal;
   float scale;        // softmax scale
   float scale_log2;   // scale * log2(e)
+  float inv_scale;    // 1 / scale
 };
 
 // acc += A[32 rows][K] * B^T with A rows a0 .. a0+31 of a ROWB-byte-row LDS
@@ -102,31 +103,42 @@ __device__ __forceinline__ void load_frags(const uint16_t *row, u32x4 (&f)[8]) {
     f[kk] = *reinterpret_cast<const u32x4 *>(row + 16 * kk + 8 * (lane >> 5));
 }
 
-// Load a [64][128] block of rows (row stride 128 elements) into LDS (wide
-// tile R) and, when T != nullptr, transposed ([128][64] narrow tile T).
+// A [64][128] block of rows (row stride 128 elements) in flight through
+// registers: fetch() issues the global loads, put() writes the rows to LDS
+// (wide tile R) and, when T != nullptr, transposed ([128][64] narrow tile T).
 // Thread t handles row pairs x 16-byte chunks: unit u = t + 256*i, row pair
 // u / 16, chunk u % 16.
-__device__ __forceinline__ void load_block(const uint16_t *src, uint8_t *R, uint8_t *T) {
-  const uint32_t t = threadIdx.x;
+struct BlockRegs {
+  u32x4 a[2], b[2];
+  __device__ __forceinline__ void fetch(const uint16_t *src) {
+    const uint32_t t = threadIdx.x;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const uint32_t u = t + 256u * i, rp = u >> 4, c = u & 15u;
-    const u32x4 a = *reinterpret_cast<const u32x4 *>(src + (size_t)(2 * rp) * kBD + 8 * c);
-    const u32x4 b = *reinterpret_cast<const u32x4 *>(src + (size_t)(2 * rp + 1) * kBD + 8 * c);
-    *reinterpret_cast<u32x4 *>(R + toff<256>(2 * rp, 16 * c)) = a;
-    *reinterpret_cast<u32x4 *>(R + toff<256>(2 * rp + 1, 16 * c)) = b;
-    if (T != nullptr) {
-      // Element d = 8c + e of rows 2rp, 2rp+1 -> T[8c + e][2rp .. 2rp+1].
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t u = t + 256u * i, rp = u >> 4, c = u & 15u;
+      a[i] = *reinterpret_cast<const u32x4 *>(src + (size_t)(2 * rp) * kBD + 8 * c);
+      b[i] = *reinterpret_cast<const u32x4 *>(src + (size_t)(2 * rp + 1) * kBD + 8 * c);
+    }
+  }
+  __device__ __forceinline__ void put(uint8_t *R, uint8_t *T) const {
+    const uint32_t t = threadIdx.x;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        *reinterpret_cast<uint32_t *>(T + toff<128>(8 * c + 2 * e, 4 * rp)) =
-            __builtin_amdgcn_perm(b[e], a[e], 0x05040100u);
-        *reinterpret_cast<uint32_t *>(T + toff<128>(8 * c + 2 * e + 1, 4 * rp)) =
-            __builtin_amdgcn_perm(b[e], a[e], 0x07060302u);
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t u = t + 256u * i, rp = u >> 4, c = u & 15u;
+      *reinterpret_cast<u32x4 *>(R + toff<256>(2 * rp, 16 * c)) = a[i];
+      *reinterpret_cast<u32x4 *>(R + toff<256>(2 * rp + 1, 16 * c)) = b[i];
+      if (T != nullptr) {
+        // Element d = 8c + e of rows 2rp, 2rp+1 -> T[8c + e][2rp .. 2rp+1].
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          *reinterpret_cast<uint32_t *>(T + toff<128>(8 * c + 2 * e, 4 * rp)) =
+              __builtin_amdgcn_perm(b[i][e], a[i][e], 0x05040100u);
+          *reinterpret_cast<uint32_t *>(T + toff<128>(8 * c + 2 * e + 1, 4 * rp)) =
+              __builtin_amdgcn_perm(b[i][e], a[i][e], 0x07060302u);
+        }
       }
     }
   }
-}
+};
 
 // Store a 32x32 fp32 accumulator tile (rows row0.., columns col0..) of a
 // [rows][128] 16-bit output, times mul.
@@ -191,56 +203,69 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdParams p) {
   load_frags(p.V + kv_off + (size_t)(kh2 * 32 + (lane & 31)) * kBD, vf);
   f32x16 dv[2] = {f32x16{}, f32x16{}}, dk[2] = {f32x16{}, f32x16{}};
   const int key = kb * kBlk + kh2 * 32 + (int)(lane & 31);
-  for (int hq = hkv * group; hq < (hkv + 1) * group; ++hq) {
-    const size_t bh = (size_t)b * p.q_heads + hq;
-    for (int qb = CAUSAL ? kb : 0; qb < nb; ++qb) {
-      __syncthreads();  // the previous block's readers are done
-      const size_t q_off = (bh * p.seq + (size_t)qb * kBlk) * kBD;
-      load_block(p.Q + q_off, sQ, sQt);
-      load_block(p.dO + q_off, sdO, sdOt);
-      // This lane's 16 query rows: lse (log2 units) and delta.
-      float l2[16], dl[16];
-      const size_t row0 = bh * p.seq + (size_t)qb * kBlk + qh2 * 32 + 4 * (lane >> 5);
+  // Work items: (q head of the group, query block), flattened; the next
+  // item's Q and dO rows are fetched while this one's products run.
+  const int qb0 = CAUSAL ? kb : 0, nq = nb - qb0, items = group * nq;
+  auto q_offset = [&](int it) {
+    const size_t bh = (size_t)b * p.q_heads + hkv * group + it / nq;
+    return (bh * p.seq + (size_t)(qb0 + it % nq) * kBlk) * kBD;
+  };
+  BlockRegs rq, rdo;
+  rq.fetch(p.Q + q_offset(0));
+  rdo.fetch(p.dO + q_offset(0));
+  for (int it = 0; it < items; ++it) {
+    const int qb = qb0 + it % nq;
+    const size_t row_base = q_offset(it) / kBD;  // bh * seq + qb * 64
+    __syncthreads();  // the previous item's readers are done
+    rq.put(sQ, sQt);
+    rdo.put(sdO, sdOt);
+    if (it + 1 < items) {
+      rq.fetch(p.Q + q_offset(it + 1));
+      rdo.fetch(p.dO + q_offset(it + 1));
+    }
+    // The score accumulator starts at -lse / scale and dP's at -delta
+    // (per query row), so exp2(c * s) = P and dp = dP - delta after the
+    // products.
+    f32x16 s, dp;
+    const size_t row0 = row_base + qh2 * 32 + 4 * (lane >> 5);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 a = *reinterpret_cast<const f32x4 *>(p.lse + row0 + 8 * g);
-        const f32x4 d = *reinterpret_cast<const f32x4 *>(p.delta + row0 + 8 * g);
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 a = *reinterpret_cast<const f32x4 *>(p.lse + row0 + 8 * g);
+      const f32x4 d = *reinterpret_cast<const f32x4 *>(p.delta + row0 + 8 * g);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          l2[4 * g + e] = a[e] * kLog2eB;
-          dl[4 * g + e] = d[e];
-        }
+      for (int e = 0; e < 4; ++e) {
+        s[4 * g + e] = -a[e] * p.inv_scale;
+        dp[4 * g + e] = -d[e];
       }
-      __syncthreads();
-      f32x16 s = {}, dp = {};
-      mma_nt_reg<DT, 8, 256>(s, sQ, qh2 * 32, kf);
-      mma_nt_reg<DT, 8, 256>(dp, sdO, qh2 * 32, vf);
-      // P and dS; P^T / dS^T rows = keys, 4 consecutive queries per store.
+    }
+    __syncthreads();
+    mma_nt_reg<DT, 8, 256>(s, sQ, qh2 * 32, kf);
+    mma_nt_reg<DT, 8, 256>(dp, sdO, qh2 * 32, vf);
+    // P and dS; P^T / dS^T rows = keys, 4 consecutive queries per store.
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        float pv[4], dsv[4];
+    for (int g = 0; g < 4; ++g) {
+      float pv[4], dsv[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * g + e;
-          const int q = qb * kBlk + qh2 * 32 + 8 * g + 4 * (int)(lane >> 5) + e;
-          float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], p.scale_log2, -l2[r]));
-          if (CAUSAL && key > q)
-            pr = 0.f;
-          pv[e] = pr;
-          dsv[e] = pr * (dp[r] - dl[r]);
-        }
-        const uint32_t off =
-            toff<128>(kh2 * 32 + (lane & 31), 2 * (qh2 * 32 + 8 * g + 4 * (lane >> 5)));
-        *reinterpret_cast<u32x2 *>(sPt + off) = u32x2{pack2<DT>(pv[0], pv[1]), pack2<DT>(pv[2], pv[3])};
-        *reinterpret_cast<u32x2 *>(sdSt + off) =
-            u32x2{pack2<DT>(dsv[0], dsv[1]), pack2<DT>(dsv[2], dsv[3])};
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * g + e;
+        const int q = qb * kBlk + qh2 * 32 + 8 * g + 4 * (int)(lane >> 5) + e;
+        float pr = __builtin_amdgcn_exp2f(s[r] * p.scale_log2);
+        if (CAUSAL && key > q)
+          pr = 0.f;
+        pv[e] = pr;
+        dsv[e] = pr * dp[r];
       }
-      __syncthreads();
+      const uint32_t off =
+          toff<128>(kh2 * 32 + (lane & 31), 2 * (qh2 * 32 + 8 * g + 4 * (lane >> 5)));
+      *reinterpret_cast<u32x2 *>(sPt + off) = u32x2{pack2<DT>(pv[0], pv[1]), pack2<DT>(pv[2], pv[3])};
+      *reinterpret_cast<u32x2 *>(sdSt + off) =
+          u32x2{pack2<DT>(dsv[0], dsv[1]), pack2<DT>(dsv[2], dsv[3])};
+    }
+    __syncthreads();
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        mma_nt_lds<DT, 4, 128>(dv[t], sPt, kh * 32, sdOt, (2 * dq + t) * 32);
-        mma_nt_lds<DT, 4, 128>(dk[t], sdSt, kh * 32, sQt, (2 * dq + t) * 32);
-      }
+    for (int t = 0; t < 2; ++t) {
+      mma_nt_lds<DT, 4, 128>(dv[t], sPt, kh * 32, sdOt, (2 * dq + t) * 32);
+      mma_nt_lds<DT, 4, 128>(dk[t], sdSt, kh * 32, sQt, (2 * dq + t) * 32);
     }
   }
   uint16_t *dK = p.dK + kv_off, *dV = p.dV + kv_off;
@@ -277,10 +302,17 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdParams p) {
   f32x16 dqa[2] = {f32x16{}, f32x16{}};
   const size_t kv_base = (size_t)(b * p.kv_heads + hkv) * p.seq * kBD;
   const int kb_end = CAUSAL ? qb + 1 : nb;
+  BlockRegs rk, rv;
+  rk.fetch(p.K + kv_base);
+  rv.fetch(p.V + kv_base);
   for (int kb = 0; kb < kb_end; ++kb) {
     __syncthreads();
-    load_block(p.K + kv_base + (size_t)kb * kBlk * kBD, sK, sKt);
-    load_block(p.V + kv_base + (size_t)kb * kBlk * kBD, sV, nullptr);
+    rk.put(sK, sKt);
+    rv.put(sV, nullptr);
+    if (kb + 1 < kb_end) {
+      rk.fetch(p.K + kv_base + (size_t)(kb + 1) * kBlk * kBD);
+      rv.fetch(p.V + kv_base + (size_t)(kb + 1) * kBlk * kBD);
+    }
     __syncthreads();
     f32x16 st = {}, dpt = {};
     mma_nt_reg<DT, 8, 256>(st, sK, kh2 * 32, qf);
@@ -348,6 +380,7 @@ hipError_t launch_bwd(const BwdArgs &a, hipStream_t stream) {
   p.causal = a.causal;
   p.scale = a.scale > 0.f ? a.scale : 1.0f / __builtin_sqrtf((float)kBD);
   p.scale_log2 = p.scale * kLog2eB;
+  p.inv_scale = 1.0f / p.scale;
   if (a.dtype == kF16)
     return a.causal ? launch_bwd_dt<kF16, true>(p, stream) : launch_bwd_dt<kF16, false>(p, stream);
   return a.causal ? launch_bwd_dt<kBF16, true>(p, stream) : launch_bwd_dt<kBF16, false>(p, stream);
