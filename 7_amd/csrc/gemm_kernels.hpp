@@ -844,6 +844,13 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
   static_assert(C::SMEM == DefaultCfg::SMEM && C::THREADS == DefaultCfg::THREADS,
                 "one LDS size and block size");
   constexpr int NR = C::NG * 4;  // accumulator registers per MFMA tile
+  // XCD-aware worker numbering, as for tiled CTAs: the dispatcher places
+  // workgroup i on XCD i % 8, so renumbering makes the workers of one XCD
+  // consecutive; their work units, and so their tiles, are then adjacent and
+  // share A/B panels in that XCD's L2.  Every use of the worker index below
+  // (intervals, owners, partial slots) takes the renumbered one.
+  if ((p.workers & 7) == 0)
+    worker = (worker & 7) * (p.workers >> 3) + (worker >> 3);
   const int tiles = p.tiles_m * p.tiles_n;
   const int iters = (p.K + kSKUnit - 1) / kSKUnit;
   const int ksteps = (p.K + C::BK - 1) / C::BK;  // mainloop steps per tile
