@@ -140,6 +140,13 @@ struct BlockRegs {
   }
 };
 
+// CTA id -> work index with the CTAs of one head on one XCD (the
+// dispatcher places workgroup i on XCD i % 8), so they share that head's
+// K/V or Q/dO rows in the XCD's L2.
+__device__ __forceinline__ int xcd_pid(int raw, int total) {
+  return (total & 7) == 0 ? (raw & 7) * (total >> 3) + (raw >> 3) : raw;
+}
+
 // Store a 32x32 fp32 accumulator tile (rows row0.., columns col0..) of a
 // [rows][128] 16-bit output, times mul.
 template <int DT>
@@ -186,7 +193,8 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdParams p) {
   uint8_t *sQ = smem, *sdO = sQ + kWide, *sQt = sdO + kWide, *sdOt = sQt + kNarrowT;
   uint8_t *sPt = sdOt + kNarrowT, *sdSt = sPt + kNarrowS;
   const int nb = p.seq / kBlk;
-  const int kb = (int)blockIdx.x % nb, bhk = (int)blockIdx.x / nb;
+  const int pid = xcd_pid((int)blockIdx.x, (int)gridDim.x);
+  const int kb = pid % nb, bhk = pid / nb;
   const int b = bhk / p.kv_heads, hkv = bhk - b * p.kv_heads;
   const int group = p.q_heads / p.kv_heads;
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -282,7 +290,8 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kWide + kNarrowT + kNarrowS];
   uint8_t *sK = smem, *sV = sK + kWide, *sKt = sV + kWide, *sdS = sKt + kNarrowT;
   const int nb = p.seq / kBlk;
-  const int qb = (int)blockIdx.x % nb, bh = (int)blockIdx.x / nb;
+  const int pid = xcd_pid((int)blockIdx.x, (int)gridDim.x);
+  const int qb = pid % nb, bh = pid / nb;
   const int b = bh / p.q_heads, hq = bh - b * p.q_heads;
   const int hkv = hq / (p.q_heads / p.kv_heads);
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
