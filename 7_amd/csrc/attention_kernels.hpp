@@ -217,14 +217,15 @@ __device__ __forceinline__ void fwd_pp_cta(const Params &p, int raw, uint8_t *sm
   // loads keys 2kp, 2kp+1 (kp = tg % 32) of d chunk dc = 8g + tg / 32.
   const int tg = threadIdx.x & 255;
   const int kp = tg & 31, dc = 8 * grp + (tg >> 5);
-  u32x4 vr[2];
-  auto load_v = [&](int kt) {
+  u32x4 vr[2], vr1[2];
+  auto load_v_to = [&](int kt, u32x4(&dst)[2]) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const uint32_t key = (uint32_t)min(kt * kBN + 2 * kp + i, p.seq_k - 1);
-      vr[i] = *reinterpret_cast<const u32x4 *>(Vh + key * kKRowBytes + 16 * dc);
+      dst[i] = *reinterpret_cast<const u32x4 *>(Vh + key * kKRowBytes + 16 * dc);
     }
   };
+  auto load_v = [&](int kt) { load_v_to(kt, vr); };
   // V^T column of key 2kp: 16-key groups stored as [0-3, 8-11, 4-7, 12-15].
   const int k2 = 2 * kp, blk = (k2 >> 2) & 3;
   const int vpos = 16 * (k2 >> 4) + 4 * (((blk & 1) << 1) | (blk >> 1)) + (k2 & 3);
@@ -395,14 +396,15 @@ __device__ __forceinline__ void fwd_pp_cta(const Params &p, int raw, uint8_t *sm
         pin(pf[j][sl]);
   };
   // This group's half of a V^T tile (from vr) at store base vst.
-  auto store_vt = [&](uint32_t vst) {
+  auto store_vt_from = [&](uint32_t vst, const u32x4(&src)[2]) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      lds_store4(vst + 2 * e * kVtPitch, __builtin_amdgcn_perm(vr[1][e], vr[0][e], 0x05040100u));
+      lds_store4(vst + 2 * e * kVtPitch, __builtin_amdgcn_perm(src[1][e], src[0][e], 0x05040100u));
       lds_store4(vst + (2 * e + 1) * kVtPitch,
-                 __builtin_amdgcn_perm(vr[1][e], vr[0][e], 0x07060302u));
+                 __builtin_amdgcn_perm(src[1][e], src[0][e], 0x07060302u));
     }
   };
+  auto store_vt = [&](uint32_t vst) { store_vt_from(vst, vr); };
 
   // One iteration t < ntiles - 1: G(t), barrier, SM(t+1), barrier.
   // PH = t % 4 fixes the buffer offsets.
@@ -428,16 +430,17 @@ __device__ __forceinline__ void fwd_pp_cta(const Params &p, int raw, uint8_t *sm
   // ---- prologue (all waves): K(0..3), V^T(0), B's half of V^T(1), S(0)
   // and its softmax --------------------------------------------------------
   f32x16 sa[2];
+  // Group B's V(1) is loaded with V(0), so the prologue waits on memory once.
   issue_k(0);
   issue_k(1);
   issue_k(2);
   load_v(0);
+  if (grp == 1)
+    load_v_to(1, vr1);
   vm_wait_barrier();
   store_vt(vt_store);
-  if (grp == 1) {
-    load_v(1);
-    store_vt(vt_store + kVtBytes);
-  }
+  if (grp == 1)
+    store_vt_from(vt_store + kVtBytes, vr1);
 #pragma unroll
   for (int i = 0; i < 16; ++i)
     sa[i & 1] = mfma32x32x16<DT>(kfrag(0, i), qf[i >> 1], i < 2 ? f32x16{} : sa[i & 1]);
