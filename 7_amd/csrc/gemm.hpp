@@ -26,6 +26,10 @@ struct GemmArgs {
   const void *b_scale = nullptr;
   // MXFP4 with B and both scales in the AITER preshuffled layouts.
   bool aiter = false;
+  // Tile-packed C for the reference blocking (bm, bn, wave_m_tiles,
+  // wave_n_tiles); computed in the column-major orientation.
+  bool packed = false;
+  int pk_bm = 1, pk_bn = 1, pk_wmt = 1, pk_wnt = 1;
 };
 
 constexpr int kTileEdge = 256;

@@ -87,7 +87,7 @@ int tiles_for(int extent) { return (extent + kTile - 1) / kTile; }
 int k_iterations(int K) { return (K + kSKUnit - 1) / kSKUnit; }
 
 hipError_t launch(const GemmArgs &g, hipStream_t stream) {
-  if (g.workers == 0 && !g.force_masked && skinny_supported(g))
+  if (g.workers == 0 && !g.force_masked && !g.packed && skinny_supported(g))
     return launch_skinny(g, stream);
   Params p{};
   p.A = static_cast<const uint16_t *>(g.A);
@@ -101,9 +101,19 @@ hipError_t launch(const GemmArgs &g, hipStream_t stream) {
   p.group_m = g.group_m > 0 ? g.group_m : WAVE_GEMM_GROUP_M;
   if (p.group_m > p.tiles_m)
     p.group_m = p.tiles_m;
-  p.ldc = g.col_major ? g.M : g.N;
+  const bool cm = g.col_major || g.packed;
+  p.ldc = cm ? g.M : g.N;
   const size_t out_bytes = g.out_dtype == kF32 ? 4 : 2;
   p.c_vec_ok = (p.ldc % 4 == 0) && aligned_to(g.C, 4 * out_bytes);
+  if (g.packed) {
+    p.pk = 1;
+    p.pk_bm = g.pk_bm;
+    p.pk_bn = g.pk_bn;
+    p.pk_wmt = g.pk_wmt;
+    p.pk_wnt = g.pk_wnt;
+    p.pk_nblocks = g.N / (16 * g.pk_bn * g.pk_wnt);
+    p.c_vec_ok = aligned_to(g.C, 4 * out_bytes);  // M % 16 == 0: whole 4-row groups
+  }
   p.scratch = static_cast<float *>(g.scratch);
   p.counters = static_cast<uint32_t *>(g.counters);
   p.workers = g.workers;
@@ -119,8 +129,8 @@ hipError_t launch(const GemmArgs &g, hipStream_t stream) {
     mode = 4;
   const bool sk = g.workers > 0;
   if (g.in_dtype == kF16)
-    return launch_in<kF16>(p, g.out_dtype, g.col_major, sk, mode, stream);
-  return launch_in<kBF16>(p, g.out_dtype, g.col_major, sk, mode, stream);
+    return launch_in<kF16>(p, g.out_dtype, cm, sk, mode, stream);
+  return launch_in<kBF16>(p, g.out_dtype, cm, sk, mode, stream);
 }
 
 } // namespace gemm

@@ -83,9 +83,16 @@ template <int BK_, int NSTAGE_, int WAVES_, int SCALE_ = 0, int MF_ = 32> struct
   static constexpr int WAVES = WAVES_;
   static constexpr int MF = MF_;
   static constexpr int THREADS = 64 * WAVES;
-  static constexpr int WPN = 2, WQN = WAVES / 2;
-  static constexpr int TP = 128 / MF, TQ = 256 / WQN / MF;
-  static_assert((MF == 32 || MF == 16) && (WAVES == 4 || WAVES == 8), "4 or 8 waves");
+  // Compute grid: VW virtual waves, WPN along P x WQN along Q.  With fewer
+  // than 4 waves each wave runs PASSES = VW / WAVES virtual waves in turn
+  // (one K loop each, all of them over the same LDS ring).
+  static constexpr int VW = WAVES < 4 ? 4 : WAVES;
+  static constexpr int PASSES = VW / WAVES;
+  static constexpr int WPN = VW >= 16 ? 4 : 2, WQN = VW / WPN;
+  static constexpr int TP = 256 / WPN / MF, TQ = 256 / WQN / MF;
+  static_assert((MF == 32 || MF == 16) && TP >= 1 && TQ >= 1, "MFMA tile shape");
+  static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4 || WAVES == 8 || WAVES == 16,
+                "1, 2, 4, 8 or 16 waves");
   static constexpr int NG = MF * MF / 256;       // 4-register accumulator groups
   using Acc = std::conditional_t<MF == 32, f32x16, f32x4>;
   static constexpr int KSL = 512 / MF;           // K elements per MFMA slice
@@ -101,9 +108,23 @@ template <int BK_, int NSTAGE_, int WAVES_, int SCALE_ = 0, int MF_ = 32> struct
   static_assert(OPB == 128 * 128 * (BK / 32), "super-row layout covers BK 32/64");
   static_assert(SMEM <= 160 * 1024, "LDS ring exceeds 160 KiB");
 };
-using DefaultCfg = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE, WAVE_GEMM_WAVES>;
-// Whole tiles of the tiled f16/bf16 kernel (same ring and wave grid).
-using TileCfg = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE, WAVE_GEMM_WAVES, 0, WAVE_GEMM_MF>;
+// Ragged tiles (bounds-checked path) with W waves per CTA (0: the library's
+// default wave count).
+template <int W = 0>
+using DefaultCfgW = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE, W == 0 ? WAVE_GEMM_WAVES : W>;
+using DefaultCfg = DefaultCfgW<>;
+// Whole tiles of the tiled f16/bf16 kernel (same ring and wave grid).  With
+// 8 or 16 waves (two or four per SIMD: 256 or 128 registers a wave) the
+// 16x16 path's two fragment sets do not fit next to its accumulators (8
+// waves: 12 VGPR spills), so those CTAs keep the 32x32 shape unless
+// WAVE_GEMM_MF8 says otherwise for 8 waves.
+#ifndef WAVE_GEMM_MF8
+#define WAVE_GEMM_MF8 32
+#endif
+template <int W = 0>
+using TileCfgW = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE, W == 0 ? WAVE_GEMM_WAVES : W, 0,
+                     W >= 16 ? 32 : W == 8 ? WAVE_GEMM_MF8 : WAVE_GEMM_MF>;
+using TileCfg = TileCfgW<>;
 // MXFP4: the same ring with K counted in 16-bit units (one 64-byte row
 // chunk = 128 fp4 values per stage, one MFMA 32x32x64 per 32-byte slice)
 // and 2 KiB of scales per stage: four 32-value groups x (256 A + 256 B)
@@ -116,10 +137,14 @@ using TileCfg = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE, WAVE_GEMM_WAVES, 0, WAVE_GEM
 #ifndef WAVE_FP4_MF
 #define WAVE_FP4_MF 32
 #endif
-using Fp4Cfg = Cfg<32, 4, WAVE_FP4_WAVES, 4 * 512, WAVE_FP4_MF>;
+template <int W = 0>
+using Fp4CfgW = Cfg<32, 4, W == 0 ? WAVE_FP4_WAVES : W, 4 * 512, WAVE_FP4_MF>;
+using Fp4Cfg = Fp4CfgW<>;
 // MXFP4 with AITER-preshuffled B and scales: the scale area holds whole
 // 256-byte AITER scale blocks (32 rows x 8 groups), 8 for A and 8 for B.
-using Fp4ACfg = Cfg<32, 4, WAVE_FP4_WAVES, 16 * 256, WAVE_FP4_MF>;
+template <int W = 0>
+using Fp4ACfgW = Cfg<32, 4, W == 0 ? WAVE_FP4_WAVES : W, 16 * 256, WAVE_FP4_MF>;
+using Fp4ACfg = Fp4ACfgW<>;
 
 // LDS geometry of an operand tile.  The tile is stored as 128-byte
 // "super-rows" of eight 16-byte slots: with BK = 64 super-row R is tile row
@@ -179,7 +204,40 @@ struct Params {
   float *scratch;
   uint32_t *counters;
   int workers;
+  // Tile-packed C (pk != 0; column-major MFMA orientation): the reference
+  // blocking whose 16x16 tile order C follows, and its CTA columns
+  // pk_nblocks = N / (16 * pk_bn * pk_wnt).
+  int pk, pk_bm, pk_bn, pk_wmt, pk_wnt, pk_nblocks;
 };
+
+// Tile-packed C, the reference's output_layout "tile-packed"
+// (wave_matmul.py:1279-1347 C pointers, :6351-6405 fragment stores; decoded
+// by the runner's getOutputCoordinate, wave-matmul-calibrate-runner.cpp
+// :772-834).  C is a sequence of 16x16 tiles, ordered by the reference's CTA
+// (row-major over its M_blocks x N_blocks grid), then wave (m_wave * BN +
+// n_wave), then wave tile (i * wave_n_tiles + j); inside a tile, element
+// (mi, nj) sits at (mi / 4) * 64 + nj * 4 + mi % 4 -- the 16x16 MFMA
+// accumulator order (lane (mi / 4) * 16 + nj, register mi % 4).  The index
+// is a sum of an m part and an n part.
+__device__ __forceinline__ size_t packed_m_part(const Params &p, int m) {
+  const int mt = m >> 4, mi = m & 15;
+  const int mtpb = p.pk_bm * p.pk_wmt;
+  const int wg = mt / mtpb, r = mt - wg * mtpb;
+  const int mw = r / p.pk_wmt, i = r - mw * p.pk_wmt;
+  const size_t wave_elems = (size_t)p.pk_wmt * p.pk_wnt * 256;
+  const size_t cta_elems = wave_elems * p.pk_bm * p.pk_bn;
+  return (size_t)wg * p.pk_nblocks * cta_elems + (size_t)mw * p.pk_bn * wave_elems +
+         (size_t)i * p.pk_wnt * 256 + (size_t)((mi >> 2) * 64 + (mi & 3));
+}
+__device__ __forceinline__ size_t packed_n_part(const Params &p, int n) {
+  const int nt = n >> 4, nj = n & 15;
+  const int ntpb = p.pk_bn * p.pk_wnt;
+  const int wg = nt / ntpb, r = nt - wg * ntpb;
+  const int nw = r / p.pk_wnt, j = r - nw * p.pk_wnt;
+  const size_t wave_elems = (size_t)p.pk_wmt * p.pk_wnt * 256;
+  const size_t cta_elems = wave_elems * p.pk_bm * p.pk_bn;
+  return (size_t)wg * cta_elems + (size_t)nw * wave_elems + (size_t)j * 256 + (size_t)nj * 4;
+}
 
 // Linear CTA id -> (tile_m, tile_n).  XCD remap then grouped ordering.
 __device__ __forceinline__ void tile_coords(int raw, int tiles_m, int tiles_n,
@@ -236,7 +294,8 @@ template <class C, int IN_DT, bool COL_MAJOR, bool MASKED, int VEC>
 __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
                                          int kt_begin, int kt_end,
                                          uint8_t *smem,
-                                         typename C::Acc (&acc)[C::TP][C::TQ]) {
+                                         typename C::Acc (&acc)[C::TP][C::TQ],
+                                         uint32_t pass = 0) {
   // The tile origin is uniform for every caller; readfirstlane keeps it, and
   // the DMA bases derived from it, in SGPRs (the DMA's scalar base operand)
   // where a caller's control flow hides that (Stream-K's ticket loop).
@@ -246,7 +305,9 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
   static_assert(C::KS >= 2 || !MASKED, "the bounds-checked path needs two slices a stage");
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63;
-  const uint32_t wp = wave % C::WPN, wq = wave / C::WPN;
+  // Virtual wave of this pass (fewer than 4 waves: PASSES > 1).
+  const uint32_t vw = wave + pass * C::WAVES;
+  const uint32_t wp = vw % C::WPN, wq = vw / C::WPN;
   // P operand (rows of the MFMA result) comes from B for row-major C.
   constexpr uint32_t kPBuf = COL_MAJOR ? 0 : C::OPB;
   constexpr uint32_t kQBuf = COL_MAJOR ? C::OPB : 0;
@@ -357,6 +418,7 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
   auto step = [&](const Frag &cur, Frag &nxt, bool read, uint32_t nstage,
                   int nkk, auto hook, auto rg_tag) {
     constexpr int RG = decltype(rg_tag)::value;
+    static_assert(RG >= 1 && RG <= TP, "every read group is one of the step's TP groups");
 #pragma unroll
     for (int tp = 0; tp < TP; ++tp) {
       if (read && tp < RG) {
@@ -396,7 +458,8 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
              [&](int tp) { hook(kk * TP + tp); }, std::integral_constant<int, TP>{});
       else
         step(f[kk & 1], f[(kk + 1) & 1], true, stage, kk + 1,
-             [&](int tp) { hook(kk * TP + tp); }, std::integral_constant<int, WAVE_GEMM_PRE_RG>{});
+             [&](int tp) { hook(kk * TP + tp); },
+             std::integral_constant<int, (WAVE_GEMM_PRE_RG < TP ? WAVE_GEMM_PRE_RG : TP)>{});
     }
   };
   auto body = [&](uint32_t stage) { body_h(stage, no_hook); };
@@ -583,44 +646,71 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
   } else {
     // VGPR-staged loads with bounds checks (ragged M/N/K, unaligned K);
     // two LDS stages, the next stage held in VGPRs during the current one.
+    // With 1 or 2 waves a stage is 16 or 8 chunks per operand and thread;
+    // those CTAs copy the next stage after the current one's MFMAs instead,
+    // 4 chunks at a time, so the staging registers stay within budget.
     constexpr int kChunks = C::DMA;  // per operand per thread
-    const uint16_t *arow[kChunks], *brow[kChunks];
-    int kcol[kChunks];
-#pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
+    constexpr bool kPrefetch = kChunks <= 4;
+    constexpr int kHeld = kPrefetch ? kChunks : 4;
+    // Source row (nullptr past the operand's end) and K column of chunk i.
+    auto chunk_src = [&](int i, bool is_b, int &kc) -> const uint16_t * {
       const uint32_t R = (wave * C::DMA + i) * 8 + (lane >> 3), ps = lane & 7;
       const int r = (int)Geo<C>::row_of(R, ps);
-      kcol[i] = (int)(Geo<C>::chunk_of(R, ps) * 8);
-      arow[i] = (m0 + r < p.M) ? p.A + (size_t)(m0 + r) * p.K : nullptr;
-      brow[i] = (n0 + r < p.N) ? p.B + (size_t)(n0 + r) * p.K : nullptr;
-    }
-    u32x4 ra[kChunks], rb[kChunks];
-    auto load = [&](int kt) {
+      kc = (int)(Geo<C>::chunk_of(R, ps) * 8);
+      if (is_b)
+        return (n0 + r < p.N) ? p.B + (size_t)(n0 + r) * p.K : nullptr;
+      return (m0 + r < p.M) ? p.A + (size_t)(m0 + r) * p.K : nullptr;
+    };
+    const uint16_t *arow[kHeld], *brow[kHeld];
+    int kcol[kHeld];
+    if constexpr (kPrefetch) {
 #pragma unroll
       for (int i = 0; i < kChunks; ++i) {
+        arow[i] = chunk_src(i, false, kcol[i]);
+        brow[i] = chunk_src(i, true, kcol[i]);
+      }
+    }
+    u32x4 ra[kHeld], rb[kHeld];
+    // Chunks i0 .. i0 + kHeld - 1 of K step kt into VGPRs, then into LDS.
+    auto load = [&](int kt, int i0) {
+#pragma unroll
+      for (int i = 0; i < kHeld; ++i) {
+        if constexpr (!kPrefetch) {
+          arow[i] = chunk_src(i0 + i, false, kcol[i]);
+          brow[i] = chunk_src(i0 + i, true, kcol[i]);
+        }
         ra[i] = load_chunk<VEC>(arow[i], kt * C::BK + kcol[i], p.K);
         rb[i] = load_chunk<VEC>(brow[i], kt * C::BK + kcol[i], p.K);
       }
     };
-    auto store = [&](uint32_t stage) {
-      uint8_t *s = smem + stage * C::STAGE + (wave * C::DMA * 1024) + lane * 16;
+    auto store = [&](uint32_t stage, int i0) {
+      uint8_t *s = smem + stage * C::STAGE + ((wave * C::DMA + i0) * 1024) + lane * 16;
 #pragma unroll
-      for (int i = 0; i < kChunks; ++i) {
+      for (int i = 0; i < kHeld; ++i) {
         *reinterpret_cast<u32x4 *>(s + i * 1024) = ra[i];
         *reinterpret_cast<u32x4 *>(s + C::OPB + i * 1024) = rb[i];
       }
     };
-    load(kt_begin);
-    store(0);
+    auto copy = [&](int kt, uint32_t stage) {
+      for (int i0 = 0; i0 < kChunks; i0 += kHeld) {
+        load(kt, i0);
+        store(stage, i0);
+      }
+    };
+    copy(kt_begin, 0);
     lds_barrier();
     read_frags(f[0], 0, 0);
     for (int i = 0; i < nk; ++i) {
       const uint32_t stage = i & 1;
-      if (i + 1 < nk)
-        load(kt_begin + i + 1);
+      if (kPrefetch && i + 1 < nk)
+        load(kt_begin + i + 1, 0);
       body(stage);
-      if (i + 1 < nk)
-        store(stage ^ 1);
+      if (i + 1 < nk) {
+        if constexpr (kPrefetch)
+          store(stage ^ 1, 0);
+        else
+          copy(kt_begin + i + 1, stage ^ 1);
+      }
       lds_barrier();
       step(f[kLast], f[0], i + 1 < nk, stage ^ 1, 0, no_hook,
            std::integral_constant<int, TP>{});
@@ -649,10 +739,14 @@ __device__ __forceinline__ void store1(void *C, size_t idx, float v) {
 
 // Write one lane's share of the 256x256 tile at (m0, n0).  `get(tp,tq,g)`
 // returns the 4 values of accumulator group g of MFMA tile (tp, tq).
-template <class C, int OUT_DT, bool COL_MAJOR, bool MASKED, typename Get>
+// PACKED: C is tile-packed (column-major orientation: pp is m and q is n;
+// pp % 4 == 0, so the 4 values are 4 consecutive elements in tile-packed
+// order too).
+template <class C, int OUT_DT, bool COL_MAJOR, bool MASKED, bool PACKED = false, typename Get>
 __device__ __forceinline__ void store_tile(const Params &p, int m0, int n0,
-                                           Get get) {
-  const uint32_t wave = threadIdx.x >> 6;
+                                           Get get, uint32_t pass = 0) {
+  static_assert(!PACKED || COL_MAJOR, "tile-packed C uses the column-major orientation");
+  const uint32_t wave = (threadIdx.x >> 6) + pass * C::WAVES;  // virtual wave
   const uint32_t lane = threadIdx.x & 63;
   const int wp = wave % C::WPN, wq = wave / C::WPN;
   const int P0 = COL_MAJOR ? m0 : n0, Q0 = COL_MAJOR ? n0 : m0;
@@ -667,7 +761,8 @@ __device__ __forceinline__ void store_tile(const Params &p, int m0, int n0,
       for (int g = 0; g < C::NG; ++g) {
         const int pp = P0 + wp * (C::TP * MF) + tp * MF + 8 * g + 4 * (lane / MF);
         const f32x4 v = get(tp, tq, g);
-        const size_t idx = (size_t)q * p.ldc + pp;
+        const size_t idx = PACKED ? packed_m_part(p, pp) + packed_n_part(p, q)
+                                  : (size_t)q * p.ldc + pp;
         if constexpr (!MASKED) {
           store4<OUT_DT>(p.C, idx, v);
         } else {
@@ -748,31 +843,36 @@ __device__ __forceinline__ void store_tile_lds(const Params &p, int m0, int n0, 
 // (store_tile_lds) when C allows 16-byte line runs; f32 output, twice the
 // bytes, is bound by HBM writes either way and is stored directly (measured
 // faster), as are ragged tiles.
-template <class C, int OUT_DT, bool COL_MAJOR, bool MASKED, typename Get>
+// Tile-packed C is stored directly: each wave's 64 lanes already write one
+// contiguous 16x16 tile.
+template <class C, int OUT_DT, bool COL_MAJOR, bool MASKED, bool PACKED = false, typename Get>
 __device__ __forceinline__ void store_out(const Params &p, int m0, int n0, uint8_t *smem,
                                           Get get) {
-  if constexpr (!MASKED && OUT_DT != kF32) {
+  if constexpr (!MASKED && !PACKED && OUT_DT != kF32) {
     if ((((uintptr_t)p.C | (uintptr_t)p.ldc * 2) & 15) == 0) {
       store_tile_lds<C, OUT_DT, COL_MAJOR>(p, m0, n0, smem, get);
       return;
     }
   }
-  store_tile<C, OUT_DT, COL_MAJOR, MASKED>(p, m0, n0, get);
+  store_tile<C, OUT_DT, COL_MAJOR, MASKED, PACKED>(p, m0, n0, get);
 }
 
-// One 256x256 output tile: CTA `raw` of a grid of tiles_m * tiles_n CTAs.
-// smem: DefaultCfg::SMEM bytes of 1024-byte-aligned LDS.
-template <int IN_DT>
-using CfgFor = std::conditional_t<IN_DT == kMXFP4, Fp4Cfg,
-                                  std::conditional_t<IN_DT == kMXFP4A, Fp4ACfg, TileCfg>>;
+// One 256x256 output tile: CTA `raw` of a grid of tiles_m * tiles_n CTAs,
+// with W waves (0: the library default).  smem: CfgFor<IN_DT, W>::SMEM bytes
+// of 1024-byte-aligned LDS.
+template <int IN_DT, int W = 0>
+using CfgFor = std::conditional_t<IN_DT == kMXFP4, Fp4CfgW<W>,
+                                  std::conditional_t<IN_DT == kMXFP4A, Fp4ACfgW<W>, TileCfgW<W>>>;
 
-template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
+template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC, int W = 0,
+          bool PACKED = false>
 __device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *smem) {
   // Whole tiles run TileCfg's MFMA shape; ragged tiles the 32x32 one.
-  using C = std::conditional_t<MASKED, DefaultCfg, CfgFor<IN_DT>>;
-  static_assert(C::SMEM == CfgFor<IN_DT>::SMEM && C::THREADS == CfgFor<IN_DT>::THREADS,
+  using C = std::conditional_t<MASKED, DefaultCfgW<W>, CfgFor<IN_DT, W>>;
+  static_assert(C::SMEM == CfgFor<IN_DT, W>::SMEM && C::THREADS == CfgFor<IN_DT, W>::THREADS,
                 "one LDS size and block size per input type");
   static_assert(!is_fp4(IN_DT) || !MASKED, "MXFP4 takes whole tiles only");
+  static_assert(!is_fp4(IN_DT) || C::WAVES == 4 || C::WAVES == 8, "MXFP4 runs 4 or 8 waves");
   int tm, tn;
   tile_coords(raw, p.tiles_m, p.tiles_n, p.group_m, true, tm, tn);
   // The tile origin is uniform; readfirstlane keeps it (and the DMA bases
@@ -780,24 +880,36 @@ __device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *sme
   const int m0 = __builtin_amdgcn_readfirstlane(tm * kTile);
   const int n0 = __builtin_amdgcn_readfirstlane(tn * kTile);
   typename C::Acc acc[C::TP][C::TQ];
+  auto zero = [&]() {
 #pragma unroll
-  for (int i = 0; i < C::TP; ++i)
+    for (int i = 0; i < C::TP; ++i)
 #pragma unroll
-    for (int j = 0; j < C::TQ; ++j)
-      acc[i][j] = typename C::Acc{};
+      for (int j = 0; j < C::TQ; ++j)
+        acc[i][j] = typename C::Acc{};
+  };
   const int kt_n = (p.K + C::BK - 1) / C::BK;
-  mainloop<C, IN_DT, COL_MAJOR, MASKED, VEC>(p, m0, n0, 0, kt_n, smem, acc);
   auto get = [&](int tp, int tq, int g) {
     return f32x4{acc[tp][tq][4 * g], acc[tp][tq][4 * g + 1],
                  acc[tp][tq][4 * g + 2], acc[tp][tq][4 * g + 3]};
   };
-  store_out<C, OUT_DT, COL_MAJOR, MASKED>(p, m0, n0, smem, get);
+  if constexpr (C::PASSES == 1) {
+    zero();
+    mainloop<C, IN_DT, COL_MAJOR, MASKED, VEC>(p, m0, n0, 0, kt_n, smem, acc);
+    store_out<C, OUT_DT, COL_MAJOR, MASKED, PACKED>(p, m0, n0, smem, get);
+  } else {
+    // Fewer than 4 waves: one K loop per virtual wave, each stored directly.
+    for (uint32_t pass = 0; pass < (uint32_t)C::PASSES; ++pass) {
+      zero();
+      mainloop<C, IN_DT, COL_MAJOR, MASKED, VEC>(p, m0, n0, 0, kt_n, smem, acc, pass);
+      store_tile<C, OUT_DT, COL_MAJOR, MASKED, PACKED>(p, m0, n0, get, pass);
+    }
+  }
 }
 
-template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
+template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC, bool PACKED = false>
 __global__ __launch_bounds__(CfgFor<IN_DT>::THREADS, 1) void tiled_kernel(Params p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[CfgFor<IN_DT>::SMEM];
-  tiled_cta<IN_DT, OUT_DT, COL_MAJOR, MASKED, VEC>(p, blockIdx.x, smem);
+  tiled_cta<IN_DT, OUT_DT, COL_MAJOR, MASKED, VEC, 0, PACKED>(p, blockIdx.x, smem);
 }
 
 // ---------------------------------------------------------------- Stream-K
@@ -974,6 +1086,21 @@ hipError_t launch_variant(const Params &p, int mode, hipStream_t stream) {
       hipLaunchKernelGGL((tiled_kernel<IN_DT, OUT_DT, CM, MASKED, VEC>), grid, \
                          block, 0, stream, p);                                 \
   } while (0)
+  // Tile-packed C (tiled kernel, column-major orientation only).
+#define WAVE_LAUNCH_PACKED(MASKED, VEC)                                        \
+  hipLaunchKernelGGL((tiled_kernel<IN_DT, OUT_DT, true, MASKED, VEC, true>), grid, block, 0, \
+                     stream, p)
+  if constexpr (CM && !SK) {
+    if (p.pk) {
+      switch (mode) {
+      case 0: WAVE_LAUNCH_PACKED(false, 8); break;
+      case 8: WAVE_LAUNCH_PACKED(true, 8); break;
+      case 4: WAVE_LAUNCH_PACKED(true, 4); break;
+      default: WAVE_LAUNCH_PACKED(true, 1); break;
+      }
+      return hipGetLastError();
+    }
+  }
   switch (mode) {
   case 0: WAVE_LAUNCH(false, 8); break;
   case 8: WAVE_LAUNCH(true, 8); break;
@@ -981,6 +1108,7 @@ hipError_t launch_variant(const Params &p, int mode, hipStream_t stream) {
   default: WAVE_LAUNCH(true, 1); break;
   }
 #undef WAVE_LAUNCH
+#undef WAVE_LAUNCH_PACKED
   return hipGetLastError();
 }
 

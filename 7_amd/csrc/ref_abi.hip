@@ -10,7 +10,10 @@
 //   wmma_f16_matmul_tiled(const T* A, const T* B, C_t* C, int32 trip)
 //     (wave_matmul.py:11415-11427, :6954-6982; runner.cpp:1790-1791).
 //     -DWAVE_ABI_GEMM -DWAVE_ABI_M= -DWAVE_ABI_N= -DWAVE_ABI_K=
-//     -DWAVE_ABI_IN=kF16|kBF16 -DWAVE_ABI_OUT=kF32|kF16|kBF16 -DWAVE_ABI_CM=0|1
+//     -DWAVE_ABI_IN=kF16|kBF16 -DWAVE_ABI_OUT=kF32|kF16|kBF16
+//     -DWAVE_ABI_CM=0|1|2 (row-major, column-major, tile-packed; tile-packed
+//     also takes -DWAVE_ABI_PK_BM= _BN= _WMT= _WNT=, the reference blocking
+//     whose tile order C follows) [-DWAVE_ABI_THREADS=64|128|256|512|1024]
 //   wmma_f16_matmul_tiled(const u8* A, const u8* B, C_t* C, const u8* A_scale,
 //                         const u8* B_scale, int32 trip)
 //     the reference's mxfp4 input type (wave_matmul.py:6965-6975; runner.cpp
@@ -18,8 +21,8 @@
 //     [K/32][M], [K/32][N].  -DWAVE_ABI_MXFP4 -DWAVE_ABI_M= -DWAVE_ABI_N=
 //     -DWAVE_ABI_K= -DWAVE_ABI_OUT=kF32|kF16|kBF16 -DWAVE_ABI_CM=0|1
 //     [-DWAVE_ABI_MXFP4_AITER: B and scales in the AITER layouts
-//     (--mxfp4-input-layout aiter, runner.cpp:1223-1283); dynamic LDS
-//     >= 147456]
+//     (--mxfp4-input-layout aiter, runner.cpp:1223-1283)]
+//     [-DWAVE_ABI_THREADS=512|256]
 //   gfx950_f16_streamk_gemm(const f16* A, const f16* B, f16* C, f32* scratch,
 //                           u32* counters, int32 workers)
 //     (wave_matmul.py:11556-11567; runner.cpp:1811-1816; column-major C,
@@ -34,31 +37,34 @@
 //     (wave_attention.py:1436-1441; runner wave-fa-calibrate-runner.cpp
 //     :346-361).  -DWAVE_ABI_FA32 -DWAVE_ABI_FA32_M= _N= _D=
 //
-// Launch contract (what the reference's runners pass):
+// Launch contract (what the reference's launchers pass):
 //  * wmma_f16_matmul_tiled: any grid (the runner's (M_blocks, N_blocks) for
 //    its tiling); CTAs walk this build's 256x256 tiles in a grid-stride loop.
-//    Block 256 threads and >= 131072 bytes of dynamic LDS (the reference's
-//    gfx950 4-wave profile passes exactly that).  `trip` is accepted and
-//    unused: the K loop length follows from the baked K.
+//    Block WAVE_ABI_THREADS (default 256), i.e. 64 * BM * BN of the
+//    reference's blocking.  LDS is static (the code object's group segment):
+//    the reference's GEMM kernels declare theirs statically and both of its
+//    launchers pass no dynamic LDS (wave-matmul-calibrate.py:901-902; the
+//    mlir-runner gpu.launch_func, wave_matmul.py:6976-6982).  `trip` is
+//    accepted and unused: the K loop length follows from the baked K.
 //  * MXFP4 wmma_f16_matmul_tiled: any grid (grid-stride over the tiles),
 //    block 512 (8 waves, the reference's gfx950-mxfp4-256x256-8wave block)
-//    and >= 139264 bytes of dynamic LDS; M, N % 256 == 0 and K % 128 == 0
-//    at build time; A, B and both scale arrays 16-byte aligned.
-//  * gfx950_f16_streamk_gemm: grid (workers), block 256, >= 131076 bytes of
-//    dynamic LDS; workspace as wave_gemm_streamk_workspace_bytes.
+//    or 256, static LDS; M, N % 256 == 0 and K % 128 == 0 at build time; A,
+//    B and both scale arrays 16-byte aligned.
+//  * gfx950_f16_streamk_gemm: grid (workers), block 256, static LDS;
+//    workspace as wave_gemm_streamk_workspace_bytes.
 //  * flash_attention_bf16_gfx950: grid (S/256, B*H), block 512, >= 102400
-//    bytes of dynamic LDS (the reference's 8-wave profile passes 136192);
-//    built with WAVE_ABI_FA_WAVES=4: block 256, >= 45056 bytes (the
-//    runner's 4-wave default --threads 256 --dynamic-lds 68096).
-//    Non-causal, one KV head per query head, scale 1/sqrt(128).
+//    bytes of dynamic LDS (the reference's 8-wave profile passes 136192 with
+//    hipFuncSetAttribute); built with WAVE_ABI_FA_WAVES=4: block 256,
+//    >= 45056 bytes (the runner's 4-wave default --threads 256
+//    --dynamic-lds 68096).  Non-causal, one KV head per query head, scale
+//    1/sqrt(128).
 //  * flash_attention_f32: grid (1,1,1), any block size up to 1024; LDS is
 //    static.
-// A launch with another block size or grid than the one stated, or with
-// less dynamic LDS than stated, returns without writing anything; so does a
-// GEMM launch whose A/B (16 bytes) or C (4 elements) lack the alignment its
-// load path needs (hipMalloc'd buffers always have it).  The FA runner's
-// default (--threads 256 --dynamic-lds 68096, its 4-wave setting) takes the
-// 4-wave code objects; the 8-wave ones need --threads 512 --dynamic-lds 136192.
+// A launch with a smaller block than the one stated, another grid than the
+// one stated (Stream-K, FA) or less dynamic LDS than stated (FA) returns
+// without writing anything; so does a GEMM launch whose A/B (16 bytes) or C
+// (4 elements) lack the alignment its load path needs (hipMalloc'd buffers
+// always have it).  A larger block the runtime refuses (launch bounds).
 #include "attention_fwd4.hpp"
 #include "attention_kernels.hpp"
 #include "fa_small.hpp"
@@ -86,19 +92,29 @@ namespace {
 } // namespace
 
 #ifdef WAVE_ABI_GEMM
-extern "C" __global__ __launch_bounds__(256, 1) void wmma_f16_matmul_tiled(
+#ifndef WAVE_ABI_THREADS
+#define WAVE_ABI_THREADS 256
+#endif
+// Waves per CTA: the reference's BM * BN (block = 64 * BM * BN threads).
+constexpr int kAbiWaves = WAVE_ABI_THREADS / 64;
+static_assert(WAVE_ABI_THREADS % 64 == 0 && (kAbiWaves == 1 || kAbiWaves == 2 ||
+              kAbiWaves == 4 || kAbiWaves == 8 || kAbiWaves == 16),
+              "block of 64, 128, 256, 512 or 1024 threads");
+using AbiGemmCfg = wave::gemm::CfgFor<WAVE_ABI_IN, kAbiWaves>;
+extern "C" __global__ __launch_bounds__(WAVE_ABI_THREADS, 1) void wmma_f16_matmul_tiled(
     const uint16_t *A, const uint16_t *B, void *C, int trip) {
   using namespace wave::gemm;
-  static_assert(DefaultCfg::THREADS == 256, "tile kernel is built for 4 waves");
-  extern __shared__ __attribute__((aligned(1024))) uint8_t dsmem[];
+  // Static LDS (the code object's group segment): the reference's kernels
+  // declare their LDS statically and its launchers pass no dynamic LDS
+  // (wave-matmul-calibrate.py:901-902; wave_matmul.py:6976-6982).
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[AbiGemmCfg::SMEM];
   (void)trip;
-  if (blockDim.x != 256 || blockDim.y != 1 || blockDim.z != 1 ||
-      dynamic_lds_bytes() < (uint32_t)DefaultCfg::SMEM)
+  if (blockDim.x != WAVE_ABI_THREADS || blockDim.y != 1 || blockDim.z != 1)
     return;
   constexpr int M = WAVE_ABI_M, N = WAVE_ABI_N, K = WAVE_ABI_K;
-  constexpr bool CM = WAVE_ABI_CM != 0;
+  constexpr int CM = WAVE_ABI_CM;  // 0 row-major, 1 column-major, 2 tile-packed
   constexpr int OUT_BYTES = WAVE_ABI_OUT == kF32 ? 4 : 2;
-  static_assert(M > 0 && N > 0 && K > 0, "shape");
+  static_assert(M > 0 && N > 0 && K > 0 && CM >= 0 && CM <= 2, "shape / layout");
   Params p{};
   p.A = A;
   p.B = B;
@@ -110,12 +126,28 @@ extern "C" __global__ __launch_bounds__(256, 1) void wmma_f16_matmul_tiled(
   p.tiles_n = (p.N + kTile - 1) / kTile;
   p.group_m = min(4, p.tiles_m);
   p.ldc = CM ? p.M : p.N;
+#if WAVE_ABI_CM == 2
+  // The reference blocking that fixes the tile order: BM * BN waves of
+  // wave_m_tiles x wave_n_tiles 16x16 tiles per CTA.
+  constexpr int PBM = WAVE_ABI_PK_BM, PBN = WAVE_ABI_PK_BN;
+  constexpr int PWM = WAVE_ABI_PK_WMT, PWN = WAVE_ABI_PK_WNT;
+  static_assert(PBM > 0 && PBN > 0 && PWM > 0 && PWN > 0 && M % (16 * PBM * PWM) == 0 &&
+                N % (16 * PBN * PWN) == 0, "tile-packed blocking must divide M and N");
+  p.pk = 1;
+  p.pk_bm = runtime_int(PBM);
+  p.pk_bn = runtime_int(PBN);
+  p.pk_wmt = runtime_int(PWM);
+  p.pk_wnt = runtime_int(PWN);
+  p.pk_nblocks = runtime_int(N / (16 * PBN * PWN));
+  p.c_vec_ok = ((uintptr_t)C % (4 * OUT_BYTES)) == 0;
+#else
   p.c_vec_ok = (p.ldc % 4 == 0) && (((uintptr_t)C % (4 * OUT_BYTES)) == 0);
+#endif
   // One load path per code object, chosen from the baked shape like the
   // host dispatcher does: the DMA fast path for whole tiles, else the masked
   // path with 16-byte (K % 8 == 0) or 2-byte loads.
-  constexpr bool kFast = M % kTile == 0 && N % kTile == 0 && K % DefaultCfg::BK == 0 &&
-                         (CM ? M : N) % 4 == 0;
+  constexpr bool kFast = M % kTile == 0 && N % kTile == 0 && K % AbiGemmCfg::BK == 0 &&
+                         (CM == 2 || (CM ? M : N) % 4 == 0);
   constexpr int kVec = kFast || K % 8 == 0 ? 8 : 1;
   if (kVec == 8 && !(aligned16(A) && aligned16(B)))
     return;
@@ -124,7 +156,8 @@ extern "C" __global__ __launch_bounds__(256, 1) void wmma_f16_matmul_tiled(
   const int tiles = p.tiles_m * p.tiles_n;
   const int ctas = gridDim.x * gridDim.y;
   for (int raw = blockIdx.y * gridDim.x + blockIdx.x; raw < tiles; raw += ctas)
-    tiled_cta<WAVE_ABI_IN, WAVE_ABI_OUT, CM, !kFast, kVec>(p, raw, dsmem);
+    tiled_cta<WAVE_ABI_IN, WAVE_ABI_OUT, CM != 0, !kFast, kVec, kAbiWaves, CM == 2>(p, raw,
+                                                                                  smem);
 }
 #endif
 
@@ -134,15 +167,19 @@ constexpr int kAbiFp4 = kMXFP4A;  // AITER-preshuffled B and scales
 #else
 constexpr int kAbiFp4 = kMXFP4;
 #endif
-using AbiFp4Cfg = wave::gemm::CfgFor<kAbiFp4>;
+#ifndef WAVE_ABI_THREADS
+#define WAVE_ABI_THREADS 512
+#endif
+static_assert(WAVE_ABI_THREADS == 256 || WAVE_ABI_THREADS == 512,
+              "MXFP4 code objects run 4 or 8 waves");
+using AbiFp4Cfg = wave::gemm::CfgFor<kAbiFp4, WAVE_ABI_THREADS / 64>;
 extern "C" __global__ __launch_bounds__(AbiFp4Cfg::THREADS, 1) void wmma_f16_matmul_tiled(
     const uint8_t *A, const uint8_t *B, void *C, const uint8_t *A_scale, const uint8_t *B_scale,
     int trip) {
   using namespace wave::gemm;
-  extern __shared__ __attribute__((aligned(1024))) uint8_t dsmem[];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[AbiFp4Cfg::SMEM];
   (void)trip;
-  if (blockDim.x != AbiFp4Cfg::THREADS || blockDim.y != 1 || blockDim.z != 1 ||
-      dynamic_lds_bytes() < (uint32_t)AbiFp4Cfg::SMEM)
+  if (blockDim.x != AbiFp4Cfg::THREADS || blockDim.y != 1 || blockDim.z != 1)
     return;
   constexpr int M = WAVE_ABI_M, N = WAVE_ABI_N, K = WAVE_ABI_K;
   static_assert(M > 0 && N > 0 && M % kTile == 0 && N % kTile == 0 && K > 0 && K % 128 == 0,
@@ -171,7 +208,7 @@ extern "C" __global__ __launch_bounds__(AbiFp4Cfg::THREADS, 1) void wmma_f16_mat
   const int tiles = p.tiles_m * p.tiles_n;
   const int ctas = gridDim.x * gridDim.y;
   for (int raw = blockIdx.y * gridDim.x + blockIdx.x; raw < tiles; raw += ctas)
-    tiled_cta<kAbiFp4, WAVE_ABI_OUT, CM, false, 8>(p, raw, dsmem);
+    tiled_cta<kAbiFp4, WAVE_ABI_OUT, CM, false, 8, WAVE_ABI_THREADS / 64>(p, raw, smem);
 }
 #endif
 
@@ -180,9 +217,10 @@ extern "C" __global__ __launch_bounds__(256, 1) void gfx950_f16_streamk_gemm(
     const uint16_t *A, const uint16_t *B, uint16_t *C, float *scratch, uint32_t *counters,
     int workers) {
   using namespace wave::gemm;
-  extern __shared__ __attribute__((aligned(1024))) uint8_t dsmem[];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[DefaultCfg::SMEM];
+  __shared__ int arrival;
   if (blockDim.x != 256 || blockDim.y != 1 || blockDim.z != 1 || workers <= 0 ||
-      (int)gridDim.x != workers || dynamic_lds_bytes() < (uint32_t)DefaultCfg::SMEM + 4)
+      (int)gridDim.x != workers)
     return;
   constexpr int M = WAVE_ABI_SK_M, N = WAVE_ABI_SK_N, K = WAVE_ABI_SK_K;
   static_assert(M > 0 && N > 0 && K > 0, "shape");
@@ -201,7 +239,6 @@ extern "C" __global__ __launch_bounds__(256, 1) void gfx950_f16_streamk_gemm(
   p.scratch = scratch;
   p.counters = counters;
   p.workers = workers;
-  int *arrival = reinterpret_cast<int *>(dsmem + DefaultCfg::SMEM);
   constexpr bool kFast = M % kTile == 0 && N % kTile == 0 && K % DefaultCfg::BK == 0 &&
                          M % 4 == 0;
   constexpr int kVec = kFast || K % 8 == 0 ? 8 : 1;
@@ -209,7 +246,7 @@ extern "C" __global__ __launch_bounds__(256, 1) void gfx950_f16_streamk_gemm(
     return;
   if (kFast && !p.c_vec_ok)
     return;
-  streamk_cta<kF16, kF16, true, !kFast, kVec>(p, blockIdx.x, dsmem, arrival);
+  streamk_cta<kF16, kF16, true, !kFast, kVec>(p, blockIdx.x, smem, &arrival);
 }
 #endif
 

@@ -51,8 +51,9 @@ int check_gemm(const void *A, const void *B, const void *C, int M, int N, int K,
     return fail(WAVE_ERR_INVALID, "gemm: input dtype %d is not f16/bf16", in_dtype);
   if (!is_out_dtype(out_dtype))
     return fail(WAVE_ERR_INVALID, "gemm: output dtype %d is not f32/f16/bf16", out_dtype);
-  if (c_layout != WAVE_ROW_MAJOR && c_layout != WAVE_COL_MAJOR)
-    return fail(WAVE_ERR_INVALID, "gemm: layout %d is not row/column-major", c_layout);
+  if (c_layout != WAVE_ROW_MAJOR && c_layout != WAVE_COL_MAJOR && c_layout != WAVE_TILE_PACKED)
+    return fail(WAVE_ERR_INVALID, "gemm: layout %d is not row-major, column-major or "
+                "tile-packed", c_layout);
   if ((uint64_t)K * 2u * 256u >= (1ull << 32))
     return fail(WAVE_ERR_UNSUPPORTED, "gemm: K=%d exceeds 2^23", K);
   return WAVE_OK;
@@ -152,6 +153,9 @@ void *_mlir_ciface_wave_memref_to_ptr_global_f64(wave_memref_1d *m) {
 
 int wave_gemm_launch(const void *A, const void *B, void *C, int M, int N, int K,
                      int in_dtype, int out_dtype, int c_layout, void *stream) {
+  if (c_layout == WAVE_TILE_PACKED)
+    return wave_gemm_tile_packed_launch(A, B, C, M, N, K, in_dtype, out_dtype, 1, 1, 1, 1,
+                                        stream);
   int st = check_gemm(A, B, C, M, N, K, in_dtype, out_dtype, c_layout);
   if (st != WAVE_OK)
     return st;
@@ -167,6 +171,39 @@ int wave_gemm_launch(const void *A, const void *B, void *C, int M, int N, int K,
   g.col_major = c_layout == WAVE_COL_MAJOR;
   return hip_status(wave::gemm::launch(g, static_cast<hipStream_t>(stream)),
                     "wave_gemm_launch");
+}
+
+int wave_gemm_tile_packed_launch(const void *A, const void *B, void *C, int M, int N, int K,
+                                 int in_dtype, int out_dtype, int bm, int bn, int wave_m_tiles,
+                                 int wave_n_tiles, void *stream) {
+  int st = check_gemm(A, B, C, M, N, K, in_dtype, out_dtype, WAVE_TILE_PACKED);
+  if (st != WAVE_OK)
+    return st;
+  if (bm < 1 || bn < 1 || wave_m_tiles < 1 || wave_n_tiles < 1 || bm > 32 || bn > 32 ||
+      bm * bn > 32)
+    return fail(WAVE_ERR_INVALID, "gemm tile-packed: bm=%d bn=%d wave_m_tiles=%d "
+                "wave_n_tiles=%d must be >= 1 with bm*bn <= 32", bm, bn, wave_m_tiles,
+                wave_n_tiles);
+  const int64_t mb = 16ll * bm * wave_m_tiles, nb = 16ll * bn * wave_n_tiles;
+  if (M % mb != 0 || N % nb != 0)
+    return fail(WAVE_ERR_INVALID, "gemm tile-packed: M=%d N=%d are not multiples of the "
+                "CTA block %lld x %lld", M, N, (long long)mb, (long long)nb);
+  wave::gemm::GemmArgs g;
+  g.A = A;
+  g.B = B;
+  g.C = C;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.in_dtype = in_dtype;
+  g.out_dtype = out_dtype;
+  g.packed = true;
+  g.pk_bm = bm;
+  g.pk_bn = bn;
+  g.pk_wmt = wave_m_tiles;
+  g.pk_wnt = wave_n_tiles;
+  return hip_status(wave::gemm::launch(g, static_cast<hipStream_t>(stream)),
+                    "wave_gemm_tile_packed_launch");
 }
 
 int wave_gemm_mxfp4_launch(const void *A, const void *B, void *C, const void *A_scale,
@@ -198,6 +235,9 @@ int wave_gemm_streamk_launch(const void *A, const void *B, void *C, int M,
   int st = check_gemm(A, B, C, M, N, K, in_dtype, out_dtype, c_layout);
   if (st != WAVE_OK)
     return st;
+  if (c_layout == WAVE_TILE_PACKED)
+    return fail(WAVE_ERR_UNSUPPORTED, "streamk: tile-packed C is not supported (the "
+                "reference's Stream-K ABI stores column-major C)");
   if (!scratch || !counters)
     return fail(WAVE_ERR_INVALID, "streamk: null scratch or counters");
   const int64_t work = (int64_t)wave::gemm::tiles_for(M) *

@@ -26,11 +26,27 @@ def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
-def _need(t: torch.Tensor, name: str) -> None:
+def _need(t: torch.Tensor, name: str, device: torch.device | None = None) -> None:
     if not t.is_cuda:
         raise ValueError(f"{name} must be a device tensor")
     if not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name} is on {t.device}, not {device}")
+
+
+def _out(out: torch.Tensor | None, shape, dtype: torch.dtype, device: torch.device,
+         name: str = "out") -> torch.Tensor:
+    """A caller's output tensor checked for shape, dtype, device and
+    contiguity (the kernels write exactly that many elements through a bare
+    pointer), or a new one."""
+    if out is None:
+        return torch.empty(shape, dtype=dtype, device=device)
+    if tuple(out.shape) != tuple(shape) or out.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype} {tuple(shape)}, got {out.dtype} "
+                         f"{tuple(out.shape)}")
+    _need(out, name, device)
+    return out
 
 
 def gemm(a: torch.Tensor, b: torch.Tensor, *, out_dtype="f16",
@@ -40,24 +56,39 @@ def gemm(a: torch.Tensor, b: torch.Tensor, *, out_dtype="f16",
     layout "row" returns C as [M, N]; "col" returns the column-major buffer
     viewed as [N, M] (element (n, m) = C[m, n]).
     """
+    M, N, K = _gemm_operands(a, b)
+    if layout not in ("row", "col"):
+        raise ValueError("layout must be 'row' or 'col'")
+    odt = _dtype(out_dtype)
+    out = _out(out, (M, N) if layout == "row" else (N, M), odt, a.device)
+    rt.check(rt.lib().wave_gemm_launch(
+        a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, _DT[a.dtype], _DT[odt],
+        rt.ROW_MAJOR if layout == "row" else rt.COL_MAJOR, _stream(a)))
+    return out
+
+
+def _gemm_operands(a: torch.Tensor, b: torch.Tensor) -> tuple[int, int, int]:
     _need(a, "a")
-    _need(b, "b")
+    _need(b, "b", a.device)
     if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[1]:
         raise ValueError("a must be [M, K] and b [N, K]")
     if a.dtype != b.dtype or a.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError("a and b must both be f16 or both bf16")
-    M, K = a.shape
-    N = b.shape[0]
+    return a.shape[0], b.shape[0], a.shape[1]
+
+
+def gemm_tile_packed(a: torch.Tensor, b: torch.Tensor, *, bm: int = 1, bn: int = 1,
+                     wave_m_tiles: int = 1, wave_n_tiles: int = 1, out_dtype="f32",
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """C = A . B^T stored tile-packed (1-D, M*N elements) for the reference
+    blocking (bm, bn, wave_m_tiles, wave_n_tiles): the reference's
+    output_layout "tile-packed" (wave_gemm_tile_packed_launch)."""
+    M, N, K = _gemm_operands(a, b)
     odt = _dtype(out_dtype)
-    shape = (M, N) if layout == "row" else (N, M)
-    if out is None:
-        out = torch.empty(shape, dtype=odt, device=a.device)
-    elif tuple(out.shape) != shape or out.dtype != odt:
-        raise ValueError("out has the wrong shape or dtype")
-    _need(out, "out")
-    rt.check(rt.lib().wave_gemm_launch(
-        a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, _DT[a.dtype], _DT[odt],
-        rt.ROW_MAJOR if layout == "row" else rt.COL_MAJOR, _stream(a)))
+    out = _out(out, (M * N,), odt, a.device)
+    rt.check(rt.lib().wave_gemm_tile_packed_launch(
+        a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, _DT[a.dtype], _DT[odt], bm, bn,
+        wave_m_tiles, wave_n_tiles, _stream(a)))
     return out
 
 
@@ -93,13 +124,12 @@ def gemm_mxfp4(a: torch.Tensor, b: torch.Tensor, a_scale: torch.Tensor,
             raise ValueError("AITER scales must hold M*G8*8 and N*G8*8 bytes")
     elif K % 32 or tuple(a_scale.shape) != (K // 32, M) or tuple(b_scale.shape) != (K // 32, N):
         raise ValueError("scales must be [K/32, M] and [K/32, N]")
+    for t, name in ((b, "b"), (a_scale, "a_scale"), (b_scale, "b_scale")):
+        _need(t, name, a.device)
+    if layout not in ("row", "col"):
+        raise ValueError("layout must be 'row' or 'col'")
     odt = _dtype(out_dtype)
-    shape = (M, N) if layout == "row" else (N, M)
-    if out is None:
-        out = torch.empty(shape, dtype=odt, device=a.device)
-    elif tuple(out.shape) != shape or out.dtype != odt:
-        raise ValueError("out has the wrong shape or dtype")
-    _need(out, "out")
+    out = _out(out, (M, N) if layout == "row" else (N, M), odt, a.device)
     fn = rt.lib().wave_gemm_mxfp4_aiter_launch if aiter else rt.lib().wave_gemm_mxfp4_launch
     rt.check(fn(a.data_ptr(), b.data_ptr(), out.data_ptr(), a_scale.data_ptr(),
                 b_scale.data_ptr(), M, N, K, _DT[odt],
@@ -139,20 +169,22 @@ def gemm_streamk(a: torch.Tensor, b: torch.Tensor, workers: int, *,
                  out_dtype="f16", layout: str = "row",
                  workspace: StreamKWorkspace | None = None,
                  out: torch.Tensor | None = None) -> torch.Tensor:
-    """Stream-K C = A . B^T over `workers` persistent workgroups."""
-    _need(a, "a")
-    _need(b, "b")
-    if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[1]:
-        raise ValueError("a must be [M, K] and b [N, K]")
-    if a.dtype != b.dtype or a.dtype not in (torch.float16, torch.bfloat16):
-        raise ValueError("a and b must both be f16 or both bf16")
-    M, K = a.shape
-    N = b.shape[0]
+    """Stream-K C = A . B^T over `workers` persistent workgroups.
+
+    A caller's workspace must have been made for this (M, N) and at least
+    `workers` workers, on a's device: the kernels index its partial slots
+    and counters through bare pointers."""
+    M, N, K = _gemm_operands(a, b)
+    if layout not in ("row", "col"):
+        raise ValueError("layout must be 'row' or 'col'")
     odt = _dtype(out_dtype)
-    shape = (M, N) if layout == "row" else (N, M)
-    if out is None:
-        out = torch.empty(shape, dtype=odt, device=a.device)
-    _need(out, "out")
+    out = _out(out, (M, N) if layout == "row" else (N, M), odt, a.device)
+    if workspace is not None:
+        if workspace.M != M or workspace.N != N or workspace.workers < workers:
+            raise ValueError(f"workspace is for M={workspace.M} N={workspace.N} "
+                             f"workers={workspace.workers}, not M={M} N={N} workers={workers}")
+        _need(workspace.scratch, "workspace.scratch", a.device)
+        _need(workspace.counters, "workspace.counters", a.device)
     ws = workspace or StreamKWorkspace(M, N, workers, a.device)
     rt.check(rt.lib().wave_gemm_streamk_launch(
         a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, _DT[a.dtype], _DT[odt],
@@ -171,19 +203,8 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     kernel (no online max; wave_fa_fwd_bounded_launch).  waves: 8 (the
     ping-pong kernel) or 4 (the reference's 4-wave configuration;
     wave_fa_fwd_config_launch)."""
-    for t, n in ((q, "q"), (k, "k"), (v, "v")):
-        _need(t, n)
-        if t.dim() != 4:
-            raise ValueError(f"{n} must be [batch, heads, seq, head_dim]")
-    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.float16, torch.bfloat16):
-        raise ValueError("q, k, v must share an f16 or bf16 dtype")
-    B, Hq, S, D = q.shape
-    if k.shape != v.shape or k.shape[0] != B or k.shape[2] != S or k.shape[3] != D:
-        raise ValueError("k and v must be [batch, kv_heads, seq, head_dim]")
-    Hkv = k.shape[1]
-    if out is None:
-        out = torch.empty_like(q)
-    _need(out, "out")
+    B, Hq, Hkv, S, D = _fa_shapes(q, k, v)
+    out = _out(out, q.shape, q.dtype, q.device)
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, Hq, Hkv, S, D,
             _DT[q.dtype], int(causal), float(scale or 0.0))
     if waves != 8:
@@ -199,7 +220,7 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
 
 def _fa_shapes(q, k, v):
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
-        _need(t, n)
+        _need(t, n, q.device)
         if t.dim() != 4:
             raise ValueError(f"{n} must be [batch, heads, seq, head_dim]")
     if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.float16, torch.bfloat16):
@@ -233,10 +254,10 @@ def flash_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: to
     lse (flash_attention_lse); wave_fa_bwd_launch.  seq % 64 == 0."""
     B, Hq, Hkv, S, D = _fa_shapes(q, k, v)
     for t, n in ((o, "o"), (do, "do")):
-        _need(t, n)
+        _need(t, n, q.device)
         if t.shape != q.shape or t.dtype != q.dtype:
             raise ValueError(f"{n} must match q")
-    _need(lse, "lse")
+    _need(lse, "lse", q.device)
     if lse.dtype != torch.float32 or tuple(lse.shape) != (B, Hq, S):
         raise ValueError("lse must be float32 [batch, q_heads, seq]")
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
@@ -253,13 +274,14 @@ def flash_attention_f32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     """The flash_attention_f32 ABI: q [block_m, D] f16 pre-scaled by
     log2(e)/sqrt(D), k/v [seq_n, D] f16 -> O [block_m, D] f32 (exp2 softmax)."""
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
-        _need(t, n)
+        _need(t, n, q.device)
         if t.dim() != 2 or t.dtype != torch.float16:
             raise ValueError(f"{n} must be a 2-D f16 tensor")
     block_m, D = q.shape
     seq_n = k.shape[0]
-    if out is None:
-        out = torch.empty((block_m, D), dtype=torch.float32, device=q.device)
+    if k.shape[1] != D or v.shape != k.shape:
+        raise ValueError("k and v must both be [seq_n, head_dim] with q's head_dim")
+    out = _out(out, (block_m, D), torch.float32, q.device)
     rt.check(rt.lib().wave_fa_f32_launch(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), block_m, seq_n, D,
         _stream(q)))

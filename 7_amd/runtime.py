@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(_HERE, "libwave_runtime.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "wave_runtime.h")
 
 F32, F16, BF16 = 0, 1, 2
-ROW_MAJOR, COL_MAJOR = 0, 1
+ROW_MAJOR, COL_MAJOR, TILE_PACKED = 0, 1, 2
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_WORKSPACE = 0, -1, -2, -3
 
 _P = ctypes.c_void_p
@@ -26,6 +26,8 @@ _SZ = ctypes.c_size_t
 
 _SIGNATURES = {
     "wave_gemm_launch": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "wave_gemm_tile_packed_launch": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I,
+                                          _P]),
     "wave_gemm_mxfp4_launch": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "wave_gemm_mxfp4_aiter_launch": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "wave_gemm_streamk_workspace_bytes": (_I, [_I, _I, _I, ctypes.POINTER(_SZ),

@@ -59,12 +59,28 @@ def read_traffic():
     return None
 
 
-def time_launches(fn, steps, warmup, torch):
+# The GPU lowers its clock while idle and takes a few tens of milliseconds of
+# sustained load to ramp back: with 5 warmup launches (4 ms) the first timed
+# launches of a 0.9 ms kernel ran 10-15 % slower than steady state on the
+# same box (measured in one process: 1206 vs 1330 TFLOP/s for the GEMM, 928
+# vs 1070 for the FA forward; torch vs raw hipMalloc buffers made no
+# difference).  So warmup is `warmup` launches and then at least
+# WARMUP_SECONDS of back-to-back launches.
+WARMUP_SECONDS = 0.5
+
+
+def time_launches(fn, steps, warmup, torch, warm_seconds=WARMUP_SECONDS):
     """Mean ms per launch over `steps` back-to-back launches, timed with HIP
-    events on the current stream (the stream the kernels are launched on)."""
+    events on the current stream (the stream the kernels are launched on),
+    after `warmup` launches and at least `warm_seconds` of untimed load."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < warm_seconds:
+        for _ in range(4):
+            fn()
+        torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -361,6 +377,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_min_seconds": WARMUP_SECONDS,
         "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",

@@ -25,9 +25,12 @@ extern "C" {
 
 /* Element types (f16/bf16 inputs; f32/f16/bf16 GEMM output). */
 enum { WAVE_F32 = 0, WAVE_F16 = 1, WAVE_BF16 = 2 };
-/* GEMM output layouts: C[m*N+n] or C[n*M+m]
- * (runner.cpp:32 OutputLayout::RowMajor / ColumnMajor). */
-enum { WAVE_ROW_MAJOR = 0, WAVE_COL_MAJOR = 1 };
+/* GEMM output layouts: C[m*N+n], C[n*M+m], or tile-packed: C as a
+ * sequence of 16x16 tiles in the reference's CTA / wave / wave-tile order,
+ * each tile in 16x16 MFMA accumulator order (runner.cpp:32
+ * OutputLayout::RowMajor / ColumnMajor / TilePacked; see
+ * wave_gemm_tile_packed_launch). */
+enum { WAVE_ROW_MAJOR = 0, WAVE_COL_MAJOR = 1, WAVE_TILE_PACKED = 2 };
 /* Status codes. */
 enum {
   WAVE_OK = 0,
@@ -66,6 +69,29 @@ void *_mlir_ciface_wave_memref_to_ptr_global_f64(wave_memref_1d *m);
 int wave_gemm_launch(const void *A, const void *B, void *C, int M, int N,
                      int K, int in_dtype, int out_dtype, int c_layout,
                      void *stream);
+/* c_layout WAVE_TILE_PACKED in wave_gemm_launch is the tile-packed C of the
+ * reference's default blocking (BM = BN = 1, one 16x16 tile per wave,
+ * wave_matmul.py:288-300 `_MatmulConfig`): the 16x16 tiles in row-major
+ * order over the (M/16) x (N/16) tile grid.  M, N % 16 == 0. */
+
+/* The same product with C tile-packed for the reference blocking
+ * (bm, bn, wave_m_tiles, wave_n_tiles): the reference's output_layout
+ * "tile-packed" (wave_matmul.py:284, :1279-1347 C pointers, :6351-6405
+ * fragment stores; decoded by the runner's getOutputCoordinate,
+ * runner.cpp:772-834).  Element index of C[m][n], with mt = m/16,
+ * nt = n/16, mi = m%16, nj = n%16, MB = 16*bm*wave_m_tiles,
+ * NB = 16*bn*wave_n_tiles:
+ *   CTA (m/MB, n/NB), row-major over the (M/MB) x (N/NB) grid;
+ *   wave (mt % (bm*wave_m_tiles)) / wave_m_tiles * bn
+ *        + (nt % (bn*wave_n_tiles)) / wave_n_tiles;
+ *   wave tile (mt % wave_m_tiles) * wave_n_tiles + nt % wave_n_tiles;
+ *   offset in the tile (mi/4)*64 + nj*4 + mi%4.
+ * Requires bm, bn, wave_m_tiles, wave_n_tiles >= 1, bm*bn <= 32 (the
+ * reference's wave limit), M % MB == 0 and N % NB == 0. */
+int wave_gemm_tile_packed_launch(const void *A, const void *B, void *C, int M,
+                                 int N, int K, int in_dtype, int out_dtype,
+                                 int bm, int bn, int wave_m_tiles,
+                                 int wave_n_tiles, void *stream);
 
 /* ---- Stream-K GEMM ------------------------------------------------------
  * Same C as wave_gemm_launch, computed by `workers` persistent workgroups

@@ -281,6 +281,41 @@ def fa_reference_heads(head_count: int) -> list[int]:
     return buf[:n].tolist()
 
 
+# ---- Tile-packed C ------------------------------------------------------------
+def tile_packed_coords(m: int, n: int, bm: int, bn: int, wave_m_tiles: int,
+                       wave_n_tiles: int) -> tuple[np.ndarray, np.ndarray]:
+    """(m, n) of every element index of a tile-packed C, decoded as the
+    runner's getOutputCoordinate does for wave64 MFMA accumulators
+    (tools/wave-matmul-calibrate/wave-matmul-calibrate-runner.cpp:772-834):
+    index -> CTA (row-major over the M_blocks x N_blocks grid), wave
+    (m_wave * bn + n_wave), wave tile (i * wave_n_tiles + j), then lane =
+    slot / 4 and register slot % 4, i.e. row (lane / 16) * 4 + register and
+    column lane % 16 of the 16x16 tile."""
+    m_rows, n_cols = 16 * bm * wave_m_tiles, 16 * bn * wave_n_tiles
+    if m % m_rows or n % n_cols:
+        raise ValueError("tile-packed blocking must divide M and N")
+    n_blocks = n // n_cols
+    wave_elems = wave_m_tiles * wave_n_tiles * 256
+    cta_elems = bm * bn * wave_elems
+    idx = np.arange(m * n, dtype=np.int64)
+    cta, cta_rem = idx // cta_elems, idx % cta_elems
+    wg_m, wg_n = cta // n_blocks, cta % n_blocks
+    wave, wave_rem = cta_rem // wave_elems, cta_rem % wave_elems
+    tile, slot = wave_rem // 256, wave_rem % 256
+    m_wave, n_wave = wave // bn, wave % bn
+    lane, reg = slot // 4, slot % 4
+    m_tile = wg_m * (bm * wave_m_tiles) + m_wave * wave_m_tiles + tile // wave_n_tiles
+    n_tile = wg_n * (bn * wave_n_tiles) + n_wave * wave_n_tiles + tile % wave_n_tiles
+    return m_tile * 16 + (lane // 16) * 4 + reg, n_tile * 16 + lane % 16
+
+
+def to_tile_packed(c: np.ndarray, bm: int, bn: int, wave_m_tiles: int,
+                   wave_n_tiles: int) -> np.ndarray:
+    """The row-major [M, N] array c in tile-packed order (1-D)."""
+    mm, nn = tile_packed_coords(c.shape[0], c.shape[1], bm, bn, wave_m_tiles, wave_n_tiles)
+    return np.ascontiguousarray(c)[mm, nn]
+
+
 # ---- Stream-K partition -------------------------------------------------------
 def streamk_worker_interval(total: int, workers: int, worker: int) -> tuple[int, int]:
     b, e = _I64(), _I64()

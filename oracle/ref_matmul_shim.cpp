@@ -65,6 +65,25 @@ void ref_output_coordinate(int wave_size, int wmma, int index, int *m, int *n) {
   *n = c.n;
 }
 
+// getOutputCoordinate of a tile-packed C (runner.cpp:772-834) for the
+// reference blocking (bm, bn, wave_m_tiles, wave_n_tiles) of an m x n output,
+// gfx950 MFMA accumulators (wave64).
+void ref_tile_packed_coordinate(int m, int n, int bm, int bn, int wmt, int wnt,
+                                int index, int *om, int *on) {
+  Args a;
+  a.m = m;
+  a.n = n;
+  a.bm = bm;
+  a.bn = bn;
+  a.waveMTiles = wmt;
+  a.waveNTiles = wnt;
+  a.waveSize = 64;
+  a.accumulatorLayout = AccumulatorLayout::Mfma;
+  OutputCoordinate c = getOutputCoordinate(a, index);
+  *om = c.m;
+  *on = c.n;
+}
+
 // getStreamKWorkspaceSizes + makeLaunchShape for the Stream-K ABI.
 void ref_streamk_workspace(int m, int n, int k, int workers, uint64_t *scratch,
                            uint64_t *counters, int *grid_x, int *block) {

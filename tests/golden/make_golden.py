@@ -131,6 +131,28 @@ def matmul_vectors() -> dict:
         coords[f"{ws}:{wmma}"] = vals
     out["output_coordinates"] = coords
 
+    # Tile-packed C: the runner's getOutputCoordinate over whole blockings
+    # (small ones in full; the 16-wave profile's as a sample plus a digest).
+    L.ref_tile_packed_coordinate.argtypes = [ctypes.c_int] * 7 + [P, P]
+    packed = {}
+    for (m, n, bm, bn, wmt, wnt) in ((32, 64, 1, 2, 2, 1), (64, 96, 2, 1, 2, 3),
+                                     (128, 64, 2, 2, 1, 2), (1024, 512, 4, 4, 4, 4)):
+        mm = ctypes.c_int()
+        nn = ctypes.c_int()
+        coords = np.zeros((m * n, 2), np.int32)
+        for idx in range(m * n):
+            L.ref_tile_packed_coordinate(m, n, bm, bn, wmt, wnt, idx, ctypes.byref(mm),
+                                         ctypes.byref(nn))
+            coords[idx] = (mm.value, nn.value)
+        key = f"{m}x{n}:{bm}:{bn}:{wmt}:{wnt}"
+        if m * n <= 8192:
+            packed[key] = {"coords": coords.tolist()}
+        else:
+            sample = list(range(0, m * n, 4093)) + [m * n - 1]
+            packed[key] = {"sample_index": sample, "sample": coords[sample].tolist(),
+                           "sha256": hashlib.sha256(coords.tobytes()).hexdigest()}
+    out["tile_packed_coordinates"] = packed
+
     ws = {}
     for (m, n, k, w) in ((512, 256, 256, 5), (512, 512, 256, 2), (8192, 8192, 8192, 256),
                          (2048, 2048, 8192, 128)):

@@ -56,13 +56,26 @@ def _gemm(L, **kw):
 
 @pytest.mark.parametrize("kw,status", [
     (dict(A=None), -1), (dict(C=None), -1), (dict(M=0), -1), (dict(N=-3), -1),
-    (dict(K=0), -1), (dict(i=0), -1), (dict(i=7), -1), (dict(o=5), -1), (dict(lay=2), -1),
-    (dict(K=1 << 23), -2),
+    (dict(K=0), -1), (dict(i=0), -1), (dict(i=7), -1), (dict(o=5), -1), (dict(lay=3), -1),
+    (dict(lay=-1), -1), (dict(K=1 << 23), -2),
+    # tile-packed through wave_gemm_launch: the default blocking needs M, N % 16
+    (dict(lay=2, M=24), -1), (dict(lay=2, N=40), -1),
 ])
 def test_gemm_rejects_bad_arguments(wave, kw, status):
     L = wave.runtime.lib()
     assert _gemm(L, **kw) == status
     assert L.wave_last_error()
+
+
+@pytest.mark.parametrize("M,N,blocking", [
+    (32, 64, (0, 2, 2, 1)), (32, 64, (1, 0, 2, 1)), (32, 64, (1, 2, 0, 1)),
+    (32, 64, (1, 2, 2, -1)), (32, 64, (8, 8, 1, 1)),   # bm * bn > 32 waves
+    (48, 64, (1, 2, 2, 1)), (32, 48, (1, 2, 2, 1)),    # CTA block does not divide
+])
+def test_tile_packed_rejects_bad_blocking(wave, M, N, blocking):
+    L = wave.runtime.lib()
+    st = L.wave_gemm_tile_packed_launch(16, 32, 64, M, N, 32, 1, 0, *blocking, None)
+    assert st == -1 and L.wave_last_error()
 
 
 def _mxfp4(L, **kw):
@@ -197,6 +210,20 @@ ABI_SYMBOLS = {
 }
 
 
+# Static LDS (group_segment_fixed_size) per code-object family: the 4-stage
+# ring of two 256 x 32 16-bit tiles (128 KiB), + the Stream-K arrival word,
+# + 2 KiB (MXFP4 scales) or 4 KiB (AITER scale blocks) per stage; the
+# dynamic-LDS FA objects declare none.
+STATIC_LDS = {"gemm_": 131072, "streamk_": 131076, "mxfp4_": 139264, "mxfp4a_": 147456,
+              "fa_bf16_": 0, "fa4_bf16_": 0}
+# VGPR spills measured per code object (hipcc -Rpass-analysis): the ragged
+# 4-wave bf16 object (bounds-checked loads at 512 registers), and a few
+# spills outside the K loop where a 16-wave (128 registers a wave) or 8-wave
+# MXFP4 body sits at its register limit.
+SPILLS_ALLOWED = {"gemm_bf16_bf16_cm_300x200x100": 80, "gemm_f16_f16_cm_1024x512x256_b1024": 12,
+                  "gemm_bf16_bf16_rm_300x200x100_b1024": 4, "mxfp4_f16_cm_4096x4096x8192": 2}
+
+
 def test_code_objects_export_reference_symbols():
     """Every built code object (7_amd/hsaco) is a plain gfx950 ELF whose one
     kernel carries the reference's symbol name and explicit argument list."""
@@ -219,7 +246,14 @@ def test_code_objects_export_reference_symbols():
                                check=True).stdout
         assert "amdgcn-amd-amdhsa--gfx950" in notes, name
         assert f".name:           {symbol}\n" in notes, name
-        assert ".vgpr_spill_count: 0" in notes or "bf16_cm" in name, name
+        spills = int(notes.split(".vgpr_spill_count:")[1].split()[0])
+        assert spills <= SPILLS_ALLOWED.get(name[:-len(".hsaco")], 0), (name, spills)
+        # LDS: the GEMM objects declare their ring statically (the reference's
+        # launchers pass no dynamic LDS); the FA ones take the runner's dynamic
+        # LDS (hipFuncSetAttribute, wave-fa-gfx950-runner.cpp:425-428).
+        lds = int(notes.split(".group_segment_fixed_size:")[1].split()[0])
+        need = next((v for k, v in STATIC_LDS.items() if name.startswith(k)), None)
+        assert lds == need if need is not None else lds > 0, (name, lds)
         # Explicit (non-hidden) kernel arguments end at `explicit` bytes.
         args, cur = [], None
         for line in notes.split(".args:")[1].split(".group_segment_fixed_size")[0].splitlines():

@@ -191,3 +191,69 @@ def test_short_m_bucket_bit_exact(wave, oracle, dev, dt, out_dt, layout, shape):
     M, N, K = shape
     _, _, c, ref = run_gemm(wave, oracle, dev, M, N, K, dt, out_dt, layout, seed=13)
     assert_exact(oracle, c, ref, out_dt)
+
+
+# ---- tile-packed C (wave_gemm_tile_packed_launch) ------------------------------
+@pytest.mark.parametrize("case", [
+    # (M, N, K, in_dt, out_dt, blocking, mode): the reference's own
+    # tile-packed test (wave_matmul_rand_int_runtime.mlir:7-8), ragged shapes
+    # on the bounds-checked path, whole 256x256 tiles on the DMA path, the
+    # 16-wave profile's blocking and a 16-bit output.
+    (32, 64, 32, 2, 0, (1, 2, 2, 1), "rand_int"),
+    (48, 80, 40, 1, 0, (1, 1, 1, 1), "bucket"),
+    (64, 96, 64, 1, 0, (2, 1, 2, 3), "bucket"),
+    (512, 768, 192, 1, 1, (2, 2, 4, 4), "bucket"),
+    (1024, 512, 256, 2, 0, (4, 4, 4, 4), "bucket"),
+    (256, 256, 4100, 2, 2, (2, 2, 2, 2), "bucket"),
+])
+def test_tile_packed_bit_exact(wave, oracle, dev, case):
+    M, N, K, in_dt, out_dt, blocking, mode = case
+    m = oracle.MODE_RAND_INT if mode == "rand_int" else oracle.MODE_RANDOM
+    a = oracle.gemm_inputs(M, K, in_dt, 4, 0, m)
+    b = oracle.gemm_inputs(N, K, in_dt, 4, 1, m)
+    bm, bn, wmt, wnt = blocking
+    c = wave.gemm_tile_packed(to_dev(a, TDT[in_dt], dev), to_dev(b, TDT[in_dt], dev), bm=bm,
+                              bn=bn, wave_m_tiles=wmt, wave_n_tiles=wnt, out_dtype=ODT[out_dt])
+    torch.cuda.synchronize()
+    ref = oracle.to_tile_packed(oracle.gemm_nt(a, b, in_dt), bm, bn, wmt, wnt)
+    assert_exact(oracle, c, ref, out_dt)
+
+
+def test_tile_packed_default_blocking_through_wave_gemm_launch(wave, oracle, dev):
+    """c_layout = WAVE_TILE_PACKED in wave_gemm_launch: the reference's
+    default blocking (bm = bn = 1, one 16x16 tile per wave)."""
+    M, N, K = 80, 48, 96
+    a = oracle.gemm_inputs(M, K, 1, 6, 0)
+    b = oracle.gemm_inputs(N, K, 1, 6, 1)
+    A, B = to_dev(a, torch.float16, dev), to_dev(b, torch.float16, dev)
+    c = torch.full((M * N,), float("nan"), dtype=torch.float32, device=dev)
+    rt = wave.runtime
+    rt.check(rt.lib().wave_gemm_launch(A.data_ptr(), B.data_ptr(), c.data_ptr(), M, N, K, rt.F16,
+                                       rt.F32, rt.TILE_PACKED,
+                                       torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert np.array_equal(c.cpu().numpy(), oracle.to_tile_packed(oracle.gemm_nt(a, b, 1), 1, 1,
+                                                                 1, 1))
+
+
+@pytest.mark.parametrize("M,N,blocking", [(48, 64, (1, 2, 2, 1)),  # 48 % 32
+                                          (32, 48, (1, 2, 2, 1)),  # 48 % 64
+                                          (64, 64, (0, 1, 1, 1)), (64, 64, (8, 8, 1, 1))])
+def test_tile_packed_rejects_bad_blocking(wave, dev, M, N, blocking):
+    a = torch.zeros((M, 32), dtype=torch.float16, device=dev)
+    b = torch.zeros((N, 32), dtype=torch.float16, device=dev)
+    bm, bn, wmt, wnt = blocking
+    with pytest.raises(ValueError):
+        wave.gemm_tile_packed(a, b, bm=bm, bn=bn, wave_m_tiles=wmt, wave_n_tiles=wnt)
+
+
+def test_tile_packed_not_for_streamk(wave, dev):
+    a = torch.zeros((256, 64), dtype=torch.float16, device=dev)
+    rt = wave.runtime
+    ws = wave.StreamKWorkspace(256, 256, 2, dev)
+    c = torch.empty(256 * 256, dtype=torch.float16, device=dev)
+    st = rt.lib().wave_gemm_streamk_launch(a.data_ptr(), a.data_ptr(), c.data_ptr(), 256, 256,
+                                           64, rt.F16, rt.F16, rt.TILE_PACKED,
+                                           ws.scratch.data_ptr(), ws.counters.data_ptr(), 2,
+                                           None)
+    assert st == rt.ERR_UNSUPPORTED

@@ -197,6 +197,45 @@ def test_output_coordinate_goldens(mm):
         assert (m, n) == ((lane // 16) * 4 + r, lane % 16)
 
 
+def test_tile_packed_matches_runner(oracle, mm):
+    """oracle.tile_packed_coords against the runner's own getOutputCoordinate
+    (runner.cpp:772-834, recorded through oracle/_ref) on four blockings,
+    including the reference's tile-packed test (32x64, bm=1 bn=2
+    wave_m_tiles=2, wave_matmul_rand_int_runtime.mlir:7-8) and the 16-wave
+    profile's (bm=bn=4, 4x4 wave tiles)."""
+    import hashlib
+    for key, rec in mm["tile_packed_coordinates"].items():
+        shape, bm, bn, wmt, wnt = key.split(":")
+        m, n = map(int, shape.split("x"))
+        mm_, nn_ = oracle.tile_packed_coords(m, n, int(bm), int(bn), int(wmt), int(wnt))
+        coords = np.stack([mm_, nn_], axis=1).astype(np.int32)
+        if "coords" in rec:
+            assert coords.tolist() == rec["coords"], key
+        else:
+            assert coords[rec["sample_index"]].tolist() == rec["sample"], key
+            assert hashlib.sha256(coords.tobytes()).hexdigest() == rec["sha256"], key
+
+
+def test_tile_packed_is_a_permutation_of_16x16_tiles(oracle):
+    """Properties that fix the layout independently of the runner: every
+    (m, n) appears once; each run of 256 indices is one 16x16 tile; inside a
+    tile the 4 consecutive indices of a lane are 4 consecutive rows of one
+    column (the MFMA 16x16 accumulator registers)."""
+    m, n = 128, 192
+    mm_, nn_ = oracle.tile_packed_coords(m, n, 2, 1, 2, 3)
+    assert len(set(zip(mm_.tolist(), nn_.tolist()))) == m * n
+    assert mm_.min() == 0 and mm_.max() == m - 1 and nn_.max() == n - 1
+    t_m, t_n = (mm_ // 16).reshape(-1, 256), (nn_ // 16).reshape(-1, 256)
+    assert (t_m == t_m[:, :1]).all() and (t_n == t_n[:, :1]).all()
+    q_m, q_n = mm_.reshape(-1, 4), nn_.reshape(-1, 4)
+    assert (np.diff(q_m, axis=1) == 1).all() and (q_n == q_n[:, :1]).all()
+    with pytest.raises(ValueError):
+        oracle.tile_packed_coords(48, 64, 2, 1, 2, 1)  # 48 % 64 != 0
+    c = np.arange(32 * 64, dtype=np.float32).reshape(32, 64)
+    p = oracle.to_tile_packed(c, 1, 2, 2, 1)
+    assert p[:8].tolist() == [0.0, 64.0, 128.0, 192.0, 1.0, 65.0, 129.0, 193.0]
+
+
 # ---- flash attention reference -----------------------------------------------------------
 def test_fa_f32_matches_runner(oracle, fa):
     for key, rec in fa["fa_f32"].items():
