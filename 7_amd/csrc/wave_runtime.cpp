@@ -13,6 +13,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "attention.hpp"
@@ -111,6 +112,44 @@ int gemm_mxfp4(const void *A, const void *B, void *C, const void *A_scale,
   g.out_dtype = out_dtype;
   g.col_major = c_layout == WAVE_COL_MAJOR;
   return hip_status(wave::gemm::launch_mxfp4(g, static_cast<hipStream_t>(stream)), name);
+}
+
+// ---- allocation-free Stream-K workspace ------------------------------------
+// wave_gemm_streamk_noalloc_launch takes its workspace from `scratch`: the
+// partial slots of up to kNoAllocWorkers workers (two fp32 256x256 tiles
+// each, 64 MiB) followed by one uint32 counter per output tile for up to
+// kNoAllocTiles tiles (16 KiB).  Each GPU the library runs on holds its own
+// copy from module load until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it is a stand-in, not a device
+// address): it uses the per-device address from hipGetSymbolAddress.
+constexpr int kNoAllocWorkers = 128;
+constexpr int kNoAllocTiles = 4096;
+constexpr size_t kNoAllocSlotWords = (size_t)kNoAllocWorkers * 2u * 256u * 256u;
+static __device__ __align__(256) uint32_t scratch[kNoAllocSlotWords + kNoAllocTiles];
+
+constexpr int kNoAllocMaxDevices = 256;
+std::mutex g_noalloc_mu;
+void *g_noalloc_base[kNoAllocMaxDevices];  // per device: address of its `scratch`
+
+// This device's `scratch`, looked up once per device with that device
+// current (the first call on it).
+int noalloc_workspace(void **base) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return hip_status(e, "wave_gemm_streamk_noalloc_launch: hipGetDevice");
+  if (dev < 0 || dev >= kNoAllocMaxDevices)
+    return fail(WAVE_ERR_UNSUPPORTED, "wave_gemm_streamk_noalloc_launch: device %d", dev);
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (!g_noalloc_base[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess)
+      return hip_status(e, "wave_gemm_streamk_noalloc_launch: hipGetSymbolAddress(scratch)");
+    g_noalloc_base[dev] = p;
+  }
+  *base = g_noalloc_base[dev];
+  return WAVE_OK;
 }
 
 template <typename T> void *to_global(wave_memref_1d *m) {
@@ -263,6 +302,37 @@ int wave_gemm_streamk_launch(const void *A, const void *B, void *C, int M,
   g.workers = workers;
   return hip_status(wave::gemm::launch(g, static_cast<hipStream_t>(stream)),
                     "wave_gemm_streamk_launch");
+}
+
+int wave_gemm_streamk_noalloc_launch(const void *A, const void *B, void *C, int M, int N,
+                                     int K, int in_dtype, int out_dtype, int c_layout,
+                                     int workers, void *stream) {
+  int st = check_gemm(A, B, C, M, N, K, in_dtype, out_dtype, c_layout);
+  if (st != WAVE_OK)
+    return st;
+  const int64_t tiles = (int64_t)wave::gemm::tiles_for(M) * wave::gemm::tiles_for(N);
+  if (workers <= 0)
+    return fail(WAVE_ERR_INVALID, "streamk noalloc: workers=%d must be positive", workers);
+  if (workers > kNoAllocWorkers || tiles > kNoAllocTiles)
+    return fail(WAVE_ERR_UNSUPPORTED, "streamk noalloc: workers=%d and %lld output tiles "
+                "exceed the static workspace (at most %d workers and %d 256x256 tiles)",
+                workers, (long long)tiles, kNoAllocWorkers, kNoAllocTiles);
+  void *base = nullptr;
+  st = noalloc_workspace(&base);
+  if (st != WAVE_OK)
+    return st;
+  float *slots = static_cast<float *>(base);
+  uint32_t *counters = static_cast<uint32_t *>(base) + kNoAllocSlotWords;
+  // The array keeps the previous call's contents: zero this call's counters
+  // (a fill kernel, so a captured graph holds no memset node).  The partial
+  // slots need no clearing: every slot a launch reads it writes first.
+  st = hip_status(wave::gemm::zero_counters(counters, (size_t)tiles,
+                                            static_cast<hipStream_t>(stream)),
+                  "wave_gemm_streamk_noalloc_launch: counter reset");
+  if (st != WAVE_OK)
+    return st;
+  return wave_gemm_streamk_launch(A, B, C, M, N, K, in_dtype, out_dtype, c_layout, slots,
+                                  counters, workers, stream);
 }
 
 int wave_gemm_streamk_workspace_reset(uint32_t *counters, int M, int N,

@@ -111,6 +111,21 @@ int wave_gemm_streamk_launch(const void *A, const void *B, void *C, int M,
                              int N, int K, int in_dtype, int out_dtype,
                              int c_layout, float *scratch, uint32_t *counters,
                              int workers, void *stream);
+/* Allocation-free Stream-K.  No counterpart in the reference: for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The same product as
+ * wave_gemm_streamk_launch, with the workspace taken from a static device
+ * array of the library (64 MiB of partial slots + 16 KiB of counters, held
+ * on each GPU the library runs on until the process ends).  Limits:
+ * workers <= 128 and ceil(M/256) * ceil(N/256) <= 4096 output tiles;
+ * larger requests return WAVE_ERR_UNSUPPORTED.  Each call first zeroes the
+ * counters it uses with a fill kernel on `stream` and calls no hipMalloc,
+ * hipFree or allocating library routine.  All calls on one GPU share the
+ * array: calls that overlap on one GPU (on different streams) race. */
+int wave_gemm_streamk_noalloc_launch(const void *A, const void *B, void *C,
+                                     int M, int N, int K, int in_dtype,
+                                     int out_dtype, int c_layout, int workers,
+                                     void *stream);
 /* Zero the counters (after a failed or interrupted launch; Stream-K design
  * doc docs/Gfx950StreamKSameKernelReductionDesign.md:98-101). */
 int wave_gemm_streamk_workspace_reset(uint32_t *counters, int M, int N,
