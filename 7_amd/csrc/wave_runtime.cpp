@@ -152,6 +152,39 @@ int noalloc_workspace(void **base) {
   return WAVE_OK;
 }
 
+// Compute units of the current device (cached per device), for the
+// shape-driven dispatch's Stream-K worker count.
+int device_cus(int *cus) {
+  static int cached[kNoAllocMaxDevices];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return hip_status(e, "hipGetDevice");
+  if (dev < 0 || dev >= kNoAllocMaxDevices)
+    return fail(WAVE_ERR_UNSUPPORTED, "device %d", dev);
+  if (cached[dev] == 0) {
+    int n = 0;
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess)
+      return hip_status(e, "hipDeviceGetAttribute(multiProcessorCount)");
+    cached[dev] = n > 0 ? n : 1;
+  }
+  *cus = cached[dev];
+  return WAVE_OK;
+}
+
+// Stream-K workers the shape-driven dispatch uses for (M, N, K), or 0 for
+// the tiled path: fewer 256x256 tiles than CUs, K >= 4096 (64 K units a
+// tile), M > 128 (the short-M kernel's range).
+int auto_workers(int M, int N, int K, int cus) {
+  const int64_t tiles = (int64_t)wave::gemm::tiles_for(M) * wave::gemm::tiles_for(N);
+  if (M <= 128 || K < 4096 || tiles >= cus)
+    return 0;
+  const int64_t w = tiles * 2 < cus ? tiles * 2 : cus;
+  const int64_t work = tiles * wave::gemm::k_iterations(K);
+  return (int)(w < work ? w : work);
+}
+
 template <typename T> void *to_global(wave_memref_1d *m) {
   return static_cast<void *>(static_cast<T *>(m->data) + m->offset);
 }
@@ -329,6 +362,59 @@ int wave_gemm_streamk_noalloc_launch(const void *A, const void *B, void *C, int 
   st = hip_status(wave::gemm::zero_counters(counters, (size_t)tiles,
                                             static_cast<hipStream_t>(stream)),
                   "wave_gemm_streamk_noalloc_launch: counter reset");
+  if (st != WAVE_OK)
+    return st;
+  return wave_gemm_streamk_launch(A, B, C, M, N, K, in_dtype, out_dtype, c_layout, slots,
+                                  counters, workers, stream);
+}
+
+int wave_gemm_auto_workspace_bytes(int M, int N, int K, size_t *bytes) {
+  if (!bytes)
+    return fail(WAVE_ERR_INVALID, "gemm auto: null size output");
+  if (M <= 0 || N <= 0 || K <= 0)
+    return fail(WAVE_ERR_INVALID, "gemm auto: M=%d N=%d K=%d must be positive", M, N, K);
+  int cus = 0;
+  int st = device_cus(&cus);
+  if (st != WAVE_OK)
+    return st;
+  const int workers = auto_workers(M, N, K, cus);
+  *bytes = 0;
+  if (workers > 0) {
+    size_t scratch = 0, counters = 0;
+    st = streamk_sizes(M, N, workers, &scratch, &counters);
+    if (st != WAVE_OK)
+      return st;
+    *bytes = scratch + counters;
+  }
+  return WAVE_OK;
+}
+
+int wave_gemm_auto_launch(const void *A, const void *B, void *C, int M, int N, int K,
+                          int in_dtype, int out_dtype, int c_layout, void *workspace,
+                          size_t workspace_bytes, void *stream) {
+  int st = check_gemm(A, B, C, M, N, K, in_dtype, out_dtype, c_layout);
+  if (st != WAVE_OK)
+    return st;
+  if (c_layout == WAVE_TILE_PACKED)
+    return fail(WAVE_ERR_INVALID, "gemm auto: layout must be row- or column-major");
+  int cus = 0;
+  st = device_cus(&cus);
+  if (st != WAVE_OK)
+    return st;
+  const int workers = auto_workers(M, N, K, cus);
+  size_t scratch = 0, counter_bytes = 0;
+  if (workers > 0) {
+    st = streamk_sizes(M, N, workers, &scratch, &counter_bytes);
+    if (st != WAVE_OK)
+      return st;
+  }
+  if (workers == 0 || !workspace || workspace_bytes < scratch + counter_bytes)
+    return wave_gemm_launch(A, B, C, M, N, K, in_dtype, out_dtype, c_layout, stream);
+  float *slots = static_cast<float *>(workspace);
+  uint32_t *counters = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + scratch);
+  st = hip_status(wave::gemm::zero_counters(counters, counter_bytes / sizeof(uint32_t),
+                                            static_cast<hipStream_t>(stream)),
+                  "wave_gemm_auto_launch: counter reset");
   if (st != WAVE_OK)
     return st;
   return wave_gemm_streamk_launch(A, B, C, M, N, K, in_dtype, out_dtype, c_layout, slots,

@@ -77,6 +77,38 @@ def _gemm_operands(a: torch.Tensor, b: torch.Tensor) -> tuple[int, int, int]:
     return a.shape[0], b.shape[0], a.shape[1]
 
 
+def gemm_auto_workspace_bytes(M: int, N: int, K: int) -> int:
+    n = ctypes.c_size_t()
+    rt.check(rt.lib().wave_gemm_auto_workspace_bytes(M, N, K, ctypes.byref(n)))
+    return n.value
+
+
+def gemm_auto(a: torch.Tensor, b: torch.Tensor, *, out_dtype="f16", layout: str = "row",
+              workspace: torch.Tensor | None = None,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """C = A . B^T through the shape-driven dispatch (wave_gemm_auto_launch):
+    Stream-K when the 256x256 tiles would leave CUs idle, else the tiled
+    kernel.  workspace: a device byte tensor of at least
+    gemm_auto_workspace_bytes(M, N, K) bytes (allocated here when None)."""
+    M, N, K = _gemm_operands(a, b)
+    if layout not in ("row", "col"):
+        raise ValueError("layout must be 'row' or 'col'")
+    odt = _dtype(out_dtype)
+    out = _out(out, (M, N) if layout == "row" else (N, M), odt, a.device)
+    need = gemm_auto_workspace_bytes(M, N, K)
+    if workspace is None and need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=a.device)
+    if workspace is not None:
+        _need(workspace, "workspace", a.device)
+    rt.check(rt.lib().wave_gemm_auto_launch(
+        a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, _DT[a.dtype], _DT[odt],
+        rt.ROW_MAJOR if layout == "row" else rt.COL_MAJOR,
+        workspace.data_ptr() if workspace is not None else None,
+        workspace.numel() * workspace.element_size() if workspace is not None else 0,
+        _stream(a)))
+    return out
+
+
 def gemm_tile_packed(a: torch.Tensor, b: torch.Tensor, *, bm: int = 1, bn: int = 1,
                      wave_m_tiles: int = 1, wave_n_tiles: int = 1, out_dtype="f32",
                      out: torch.Tensor | None = None) -> torch.Tensor:

@@ -34,6 +34,8 @@ _SIGNATURES = {
                                                ctypes.POINTER(_SZ)]),
     "wave_gemm_streamk_launch": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P]),
     "wave_gemm_streamk_noalloc_launch": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "wave_gemm_auto_workspace_bytes": (_I, [_I, _I, _I, ctypes.POINTER(_SZ)]),
+    "wave_gemm_auto_launch": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _SZ, _P]),
     "wave_gemm_streamk_workspace_reset": (_I, [_P, _I, _I, _P]),
     "wave_gemm_streamk_counters_check": (_I, [_P, _I, _I, _P]),
     "wave_fa_fwd_launch": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P]),

@@ -91,29 +91,53 @@ def time_launches(fn, steps, warmup, torch, warm_seconds=WARMUP_SECONDS):
     return start.elapsed_time(stop) / steps
 
 
+def host_cpu():
+    """The host's CPU model and core counts (for the CPU-baseline record)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "logical_cpus": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0))}
+
+
+# Host threads for the CPU baseline: the affinity mask, capped at the CPU
+# share a one-GPU job gets on the GPU boxes (16), whatever nproc shows.
+CPU_THREADS_CAP = 16
+
+
 def cpu_baseline(a_bits, b_bits, M, N, K, budget_s):
-    """Oracle GEMM (C++, fp32 accumulate, all allowed host threads) on a
-    bounded sample of rows of the same 8192^3 problem."""
+    """Oracle GEMM (C++, fp32 accumulate) on a bounded sample of rows of the
+    same 8192^3 problem, on all allowed host threads; the median of three
+    timed runs of about budget_s / 3 seconds each."""
     from oracle import oracle
-    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    threads = max(1, min(len(os.sched_getaffinity(0)), CPU_THREADS_CAP))
     rows, dt = 8, 0.0
-    while True:  # grow the sample until it takes >= 1 s, then scale to budget
+    while True:  # grow the sample until one run takes >= 0.5 s, then scale
         t0 = time.perf_counter()
         oracle.gemm_nt_rows(a_bits, b_bits, 0, rows, oracle.F16, threads=threads)
         dt = time.perf_counter() - t0
-        if dt >= 1.0 or rows >= M:
+        if dt >= 0.5 or rows >= M:
             break
         rows = min(M, rows * 4)
-    target = int(min(M, rows * budget_s / dt))
-    if target > rows:
-        rows = target
+    rows = int(max(1, min(M, rows * (budget_s / 3) / dt)))
+    runs = []
+    for _ in range(3):
         t0 = time.perf_counter()
         oracle.gemm_nt_rows(a_bits, b_bits, 0, rows, oracle.F16, threads=threads)
-        dt = time.perf_counter() - t0
+        runs.append(time.perf_counter() - t0)
+    dt = sorted(runs)[1]
     return {"value": round(2.0 * rows * N * K / dt / 1e12, 6), "unit": "TFLOP/s",
             "cores": threads, "kind": "port",
             "sample": f"rows 0..{rows - 1} of C (={rows}x{N}x{K}) of the 8192^3 f16 GEMM, "
-                      f"{dt:.1f} s, oracle/oracle.cpp gemm_nt_rows"}
+                      f"median of 3 runs ({', '.join(f'{r:.1f}' for r in runs)} s), "
+                      f"oracle/oracle.cpp gemm_nt_rows",
+            "host": host_cpu()}
 
 
 def cpu_reference_path(M, N, K, budget_s):
@@ -191,6 +215,69 @@ def mxfp4_line(wave, torch, dev, steps, warmup):
                 "source": "docs/Gfx950MatmulProfiles.md:57-68"}}
 
 
+def config_lines(wave, torch, dev, steps, warmup):
+    """BASELINE.json configs 3 (ragged / skinny bf16 GEMMs, entries N(0,1)
+    scaled by 1/sqrt(K), bf16 in and out, fp32 accumulate) and 5 (causal GQA
+    flash attention, bf16), each on inputs resident in HBM."""
+    lines = []
+    g = torch.Generator(device=dev).manual_seed(5)
+
+    def operands(M, N, K):
+        a = (torch.randn((M, K), generator=g, device=dev) / math.sqrt(K)).to(torch.bfloat16)
+        b = (torch.randn((N, K), generator=g, device=dev) / math.sqrt(K)).to(torch.bfloat16)
+        return a, b, torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+    for name, (M, N, K) in (("3a", (128, 8192, 8192)), ("3b", (4000, 4096, 4100)),
+                            ("3c", (8192, 1024, 28672))):
+        a, b, c = operands(M, N, K)
+        fl = 2.0 * M * N * K
+        nbytes = 2.0 * (M * K + N * K + M * N)
+        ms = time_launches(lambda: wave.gemm(a, b, out_dtype=torch.bfloat16, out=c), steps,
+                           warmup, torch)
+        tf = fl / (ms * 1e-3) / 1e12
+        line = {"workload": f"gemm_bf16_{M}x{N}x{K}_config{name}", "value": round(tf, 2),
+                "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+                "frac_of_mfma_peak": round(tf / MFMA_PEAK_TFLOPS, 4),
+                "kernel": "wave_gemm_launch"}
+        if name == "3a":  # HBM-bound: algorithmic bytes read and written once
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            line.update({"gbps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                         "algorithmic_bytes": int(nbytes)})
+        if name == "3c":  # fewer 256x256 tiles (128) than CUs: the auto dispatch's Stream-K
+            ws = torch.empty(max(wave.gemm_auto_workspace_bytes(M, N, K), 1), dtype=torch.uint8,
+                             device=dev)
+            ams = time_launches(lambda: wave.gemm_auto(a, b, out_dtype=torch.bfloat16,
+                                                       workspace=ws, out=c), steps, warmup,
+                                torch)
+            atf = fl / (ams * 1e-3) / 1e12
+            line.update({"value": round(atf, 2), "ms_per_step": round(ams, 4),
+                         "frac_of_mfma_peak": round(atf / MFMA_PEAK_TFLOPS, 4),
+                         "kernel": "wave_gemm_auto_launch (Stream-K, min(2*tiles, CUs) workers)",
+                         "tiled_kernel_value": round(tf, 2)})
+        log(f"config {name} gemm bf16 {M}x{N}x{K}: {line['ms_per_step'] * 1e3:.1f} us/launch, "
+            f"{line['value']:.1f} TFLOP/s" + (f", {line['gbps']:.0f} GB/s" if "gbps" in line else ""))
+        lines.append(line)
+        del a, b, c
+
+    B, Hq, Hkv, S, D = 1, 64, 8, 8192, 128
+    q = torch.randn((B, Hq, S, D), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn((B, Hkv, S, D), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((B, Hkv, S, D), generator=g, device=dev).to(torch.bfloat16)
+    o = torch.empty_like(q)
+    ms = time_launches(lambda: wave.flash_attention(q, k, v, causal=True, out=o), steps, warmup,
+                       torch)
+    tf = 2.0 * B * Hq * S * S * D / (ms * 1e-3) / 1e12
+    log(f"config 5 fa fwd causal GQA bf16 B1 Hq64 Hkv8 S8192: {ms * 1e3:.1f} us/launch, "
+        f"{tf:.1f} TFLOP/s (causal FLOPs)")
+    lines.append({"workload": "fa_fwd_bf16_b1_hq64_hkv8_s8192_d128_causal_config5",
+                  "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+                  "frac_of_mfma_peak": round(tf / MFMA_PEAK_TFLOPS, 4),
+                  "flops": "2*B*Hq*S^2*D (the keys a causal row attends to; the reference's "
+                           "4*B*H*S^2*D non-causal count would double it)"})
+    del q, k, v, o
+    return lines
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -201,7 +288,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-ref-compare", action="store_true",
                     help="skip the runs on the reference's published input modes / shapes")
-    ap.add_argument("--workload", choices=["all", "gemm", "fa", "mxfp4", "copy"], default="all",
+    ap.add_argument("--workload", choices=["all", "gemm", "fa", "mxfp4", "copy", "configs"],
+                    default="all",
                     help="gemm / fa / mxfp4: run only that kernel (for profiler passes); copy: "
                          "a 1 GiB device copy used to calibrate rocprofv3 byte counters")
     args = ap.parse_args()
@@ -224,7 +312,7 @@ def main():
         ms = time_launches(lambda: dst.copy_(src), args.steps, args.warmup, torch)
         log(f"copy 1 GiB: {ms:.3f} ms, {2 * 4 * src.numel() / (ms * 1e-3) / 1e9:.0f} GB/s")
         return
-    if args.workload in ("fa", "mxfp4"):
+    if args.workload in ("fa", "mxfp4", "configs"):
         args.no_cpu = True
     if args.workload == "mxfp4":
         m = mxfp4_line(wave, torch, dev, args.steps, args.warmup)
@@ -249,7 +337,7 @@ def main():
         f"({100 * tflops / MFMA_PEAK_TFLOPS:.1f}% of {MFMA_PEAK_TFLOPS})")
 
     secondary = []
-    if args.workload == "gemm":
+    if args.workload in ("gemm", "configs"):
         args.no_fa = True
     if not args.no_fa:
         B, H, S, D = 4, 32, 4096, 128
@@ -285,6 +373,9 @@ def main():
                               "flops": "10*B*H*S^2*D"})
             del do, lse
         del q, k, v, o
+
+    if args.workload in ("all", "configs"):
+        secondary.extend(config_lines(wave, torch, dev, max(10, args.steps // 2), 3))
 
     if args.workload == "all" and not args.no_ref_compare:
         # The same kernels on the input mode / shape of the reference's own

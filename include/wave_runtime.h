@@ -135,6 +135,25 @@ int wave_gemm_streamk_workspace_reset(uint32_t *counters, int M, int N,
 int wave_gemm_streamk_counters_check(const uint32_t *counters, int M, int N,
                                      void *stream);
 
+/* ---- shape-driven GEMM dispatch ------------------------------------------
+ * No kernel symbol of the reference: the reference's harness picks its
+ * tiled or Stream-K kernel per run (tools/wave-matmul-calibrate/
+ * wave-matmul-perf-sweep.py:151-326 kernel matrix).  This entry point picks
+ * for the caller: the tiled kernel (or the short-M kernel for M <= 128), or
+ * Stream-K with min(2 * tiles, CUs) workers when the 256x256 output tiles
+ * alone would leave CUs idle (fewer tiles than CUs) and K >= 4096.  Stream-K
+ * takes its workspace from `workspace` (caller-owned device memory of
+ * wave_gemm_auto_workspace_bytes(M, N, K) bytes, 0 when the shape takes
+ * the tiled path; no initialisation needed, each launch zeroes the counters
+ * it uses with a fill kernel); with a smaller workspace the tiled kernel
+ * runs.  One launch in flight per workspace.  Same C as wave_gemm_launch
+ * (c_layout row- or column-major). */
+int wave_gemm_auto_workspace_bytes(int M, int N, int K, size_t *bytes);
+int wave_gemm_auto_launch(const void *A, const void *B, void *C, int M, int N,
+                          int K, int in_dtype, int out_dtype, int c_layout,
+                          void *workspace, size_t workspace_bytes,
+                          void *stream);
+
 /* ---- MXFP4 scaled GEMM ----------------------------------------------------
  * C[m][n] = sum_k (a[m][k] * 2^(sa[k/32][m] - 127)) * (b[n][k] * 2^(sb[k/32][n] - 127))
  * with fp32 accumulation and one RNE rounding to out_dtype.  A [M][K/2] and

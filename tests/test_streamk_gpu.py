@@ -104,3 +104,28 @@ def test_config3_streamk_bf16(wave, oracle, dev):
     got = c.float().cpu().numpy()
     ref = oracle.gemm_nt_rows(abits, bbits, 0, M, 2)
     assert float(np.abs(got - ref).max()) <= 2e-3 * np.sqrt(K)
+
+
+# ---- shape-driven dispatch (wave_gemm_auto_launch) ------------------------------
+@pytest.mark.parametrize("shape,streamk", [((2048, 512, 8192), True),   # 16 tiles, long K
+                                           ((1000, 300, 4100), True),   # ragged, 8 tiles
+                                           ((4096, 4096, 512), False),  # 256 tiles
+                                           ((128, 1024, 8192), False)])  # short-M kernel
+def test_auto_dispatch_matches_tiled(wave, oracle, dev, shape, streamk):
+    """Bucket inputs make every sum exact, so the auto path (Stream-K or not)
+    equals wave_gemm_launch bit for bit; a too-small workspace falls back to
+    the tiled kernel."""
+    M, N, K = shape
+    need = wave.gemm_auto_workspace_bytes(M, N, K)
+    assert (need > 0) == streamk
+    a = oracle.gemm_inputs(M, K, 2, 5, 0)
+    b = oracle.gemm_inputs(N, K, 2, 5, 1)
+    A, B = to_dev(a, torch.bfloat16, dev), to_dev(b, torch.bfloat16, dev)
+    ref = wave.gemm(A, B, out_dtype=torch.bfloat16)
+    ws = torch.full((max(need, 1),), 0xFF, dtype=torch.uint8, device=dev)  # dirty counters
+    for _ in range(2):
+        got = wave.gemm_auto(A, B, out_dtype=torch.bfloat16, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref)
+    small = torch.empty((max(need // 2, 1),), dtype=torch.uint8, device=dev)
+    assert torch.equal(wave.gemm_auto(A, B, out_dtype=torch.bfloat16, workspace=small), ref)
