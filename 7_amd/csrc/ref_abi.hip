@@ -58,8 +58,9 @@
 //    >= 45056 bytes (the runner's 4-wave default --threads 256
 //    --dynamic-lds 68096).  Non-causal, one KV head per query head, scale
 //    1/sqrt(128).
-//  * flash_attention_f32: grid (1,1,1), any block size up to 1024; LDS is
-//    static.
+//  * flash_attention_f32: grid (1,1,1), any block size up to 1024: whole
+//    waves run the matrix-core path, a block narrower than 64 (the runner's
+//    default --threads 32) the scalar one; LDS is static.
 // A launch with a smaller block than the one stated, another grid than the
 // one stated (Stream-K, FA) or less dynamic LDS than stated (FA) returns
 // without writing anything; so does a GEMM launch whose A/B (16 bytes) or C

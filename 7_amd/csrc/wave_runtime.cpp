@@ -619,8 +619,9 @@ int wave_fa_f32_launch(const void *Q, const void *K, const void *V, float *O,
   if (block_m <= 0 || seq_n <= 0 || head_dim <= 0)
     return fail(WAVE_ERR_INVALID, "fa_f32: block_m=%d seq_n=%d head_dim=%d must be positive",
                 block_m, seq_n, head_dim);
-  if (seq_n > 16384)
-    return fail(WAVE_ERR_UNSUPPORTED, "fa_f32: seq_n=%d exceeds 16384", seq_n);
+  if ((int64_t)block_m * head_dim > INT32_MAX || (int64_t)seq_n * head_dim > INT32_MAX)
+    return fail(WAVE_ERR_INVALID, "fa_f32: block_m=%d seq_n=%d head_dim=%d exceed 2^31 elements",
+                block_m, seq_n, head_dim);
   return hip_status(wave::attention::launch_small(Q, K, V, O, block_m, seq_n, head_dim,
                                                   static_cast<hipStream_t>(stream)),
                     "wave_fa_f32_launch");

@@ -256,7 +256,9 @@ int wave_fa_bwd_launch(const void *Q, const void *K, const void *V, const void *
  * Replaces `flash_attention_f32(Q, K, V, O)` (wave_attention.py:1406-1441;
  * wave-fa-calibrate-runner.cpp:346-361): Q [block_m][head_dim] f16
  * pre-scaled by log2(e)/sqrt(head_dim), K, V [seq_n][head_dim] f16,
- * O [block_m][head_dim] f32 = softmax2(Q K^T) V with exp2.  seq_n <= 16384. */
+ * O [block_m][head_dim] f32 = softmax2(Q K^T) V with exp2; P enters the
+ * P.V product as f16, as in the reference.  Any positive sizes (each of Q
+ * and K below 2^31 elements). */
 int wave_fa_f32_launch(const void *Q, const void *K, const void *V, float *O,
                        int block_m, int seq_n, int head_dim, void *stream);
 

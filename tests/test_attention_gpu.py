@@ -2,8 +2,16 @@
 
 * wave_fa_fwd_launch vs oracle.attention_rows (double-precision softmax,
   the reference runner's computeAttentionRow, wave-fa-gfx950-runner.cpp
-  :247-279, extended with the causal mask and the GQA head map).  Tolerance:
-  BASELINE.json's 2e-2 on O (the reference runner uses 3e-2, :388).
+  :247-279, extended with the causal mask and the GQA head map).  The bar is
+  on the error beyond the output type's own rounding (excess_error):
+  - the reference's bf16 bucket inputs: 1.35e-3 x input scale, the maximum
+    error the reference reports for them
+    (docs/PerfReferences/WaveGfx950FlashAttention.md:39-41);
+  - N(0,1) inputs: 5e-4 for f16, 3e-3 for bf16, where P enters the PV MFMA
+    rounded to bf16 (2^-9 relative) while the row sum keeps fp32;
+  - the fixed-max mode: 1e-3 / 7.5e-3, since its largest P is not the exact
+    1.0 of the adaptive mode and is rounded too.
+  BASELINE.json's own bound (2e-2, the runner's 3e-2 at :388) is far looser.
 * The reference's own inputs (bucket generator x 0.125 / 0.25, bf16,
   runner :194-202), all rows of small problems, the sampled heads/rows of
   large ones (runner :204-232), and --zero-qk (every row = mean of V).
@@ -24,7 +32,9 @@ from conftest import to_bits, to_dev
 
 pytestmark = pytest.mark.gpu
 
-TOL = 2e-2
+REF_TOL = 1.35e-3
+TOL = {1: 5e-4, 2: 3e-3}
+FIXED_TOL = {1: 1e-3, 2: 7.5e-3}
 TDT = {1: torch.float16, 2: torch.bfloat16}
 
 
@@ -45,9 +55,19 @@ def run_fa(wave, oracle, dev, q, k, v, dt, B, Hq, Hkv, S, causal, heads, rows, w
     ref = oracle.attention_rows(q, k, v, dtype=dt, batch=B, q_heads=Hq, kv_heads=Hkv,
                                 seq_q=S, seq_k=S, head_dim=D, causal=causal,
                                 scale=1.0 / math.sqrt(D), heads=hh, rows=rr)
-    err = np.abs(got[hh, rr] - ref)
     assert np.all(np.isfinite(got[hh, rr]))
-    return float(err.max())
+    return excess_error(got[hh, rr], ref, dt)
+
+
+# Half an ulp of the output type, relative: the rounding of the stored O
+# alone (f16 keeps 10 fraction bits, bf16 7).
+HALF_ULP = {1: 2.0 ** -11, 2: 2.0 ** -8}
+
+
+def excess_error(got, ref, dt):
+    """max |got - ref| beyond the output type's own rounding of ref: the
+    error the kernel adds before the final f16/bf16 store."""
+    return float(np.max(np.abs(got - ref) - HALF_ULP[dt] * np.abs(ref)))
 
 
 def normal_bits(n, dt, seed):
@@ -65,7 +85,7 @@ def test_reference_inputs_all_rows(wave, oracle, dev, seq, iscale, waves):
     n = seq * 128
     q, k, v = oracle.fa_gfx950_inputs(n, 0, iscale)
     err = run_fa(wave, oracle, dev, q, k, v, 2, 1, 1, 1, seq, False, [0], range(seq), waves)
-    assert err <= TOL, err
+    assert err <= REF_TOL * iscale, err
 
 
 def test_zero_qk_rows_are_mean_v(wave, oracle, dev):
@@ -75,8 +95,9 @@ def test_zero_qk_rows_are_mean_v(wave, oracle, dev):
     kt = to_dev(k, torch.bfloat16, dev).view(1, 2, 512, 128)
     vt = to_dev(v, torch.bfloat16, dev).view(1, 2, 512, 128)
     o = wave.flash_attention(qt, kt, vt).float().cpu()
-    mean = vt.float().mean(dim=2, keepdim=True).cpu()
-    assert float((o - mean).abs().max()) <= 1e-2
+    mean = vt.float().mean(dim=2, keepdim=True).cpu().expand_as(o)
+    # Every P is exactly 1: only the fp32 sum of V and the bf16 store remain.
+    assert excess_error(o.numpy(), mean.numpy(), 2) <= 1e-4
 
 
 @WAVES
@@ -90,7 +111,7 @@ def test_small_problems_all_rows(wave, oracle, dev, dt, causal, B, Hq, Hkv, S, w
     v = normal_bits(B * Hkv * S * 128, dt, 3)
     err = run_fa(wave, oracle, dev, q, k, v, dt, B, Hq, Hkv, S, causal,
                  range(B * Hq), range(S), waves)
-    assert err <= TOL, err
+    assert err <= TOL[dt], err
 
 
 @WAVES
@@ -103,7 +124,7 @@ def test_config4_f16_b4_h32_s4096(wave, oracle, dev, waves):
     rows = oracle.fa_reference_rows(S) + [1, 255, 256, 1000, 4000]
     err = run_fa(wave, oracle, dev, q, k, v, 1, B, H, H, S, False, heads, sorted(set(rows)),
                  waves)
-    assert err <= TOL, err
+    assert err <= TOL[1], err
 
 
 @WAVES
@@ -116,7 +137,7 @@ def test_config5_causal_gqa_bf16_s8192(wave, oracle, dev, waves):
     heads = [0, 7, 8, 31, 63]
     rows = sorted(set(oracle.fa_reference_rows(S) + [1, 63, 64, 4097, 8191]))
     err = run_fa(wave, oracle, dev, q, k, v, 2, B, Hq, Hkv, S, True, heads, rows, waves)
-    assert err <= TOL, err
+    assert err <= TOL[2], err
 
 
 def test_key_permutation_invariance(wave, dev):
@@ -129,12 +150,16 @@ def test_key_permutation_invariance(wave, dev):
     perm = torch.randperm(2048, generator=g).to(dev)
     o1 = wave.flash_attention(q, k, v).float()
     o2 = wave.flash_attention(q, k[:, :, perm].contiguous(), v[:, :, perm].contiguous()).float()
-    assert float((o1 - o2).abs().max()) <= 5e-3
+    # Each within TOL[1] of the exact result beyond one f16 rounding.
+    diff = (o1 - o2).abs() - 2 * HALF_ULP[1] * o2.abs()
+    assert float(diff.max()) <= 2 * TOL[1]
 
 
 @pytest.mark.parametrize("bm,sn,hd,seed", [(16, 16, 32, 11), (16, 32, 32, 11),
                                            (16, 64, 64, 3), (16, 256, 128, 5),
-                                           (8, 100, 32, 2)])
+                                           (8, 100, 32, 2), (40, 300, 256, 4),
+                                           (16, 20000, 128, 6), (3, 33, 20, 7),
+                                           (64, 1000, 72, 8), (1, 1, 8, 9)])
 def test_flash_attention_f32_abi(wave, oracle, dev, bm, sn, hd, seed):
     q, k, v = oracle.fa_f32_inputs(bm, sn, hd, seed)
     o = wave.flash_attention_f32(to_dev(q, torch.float16, dev), to_dev(k, torch.float16, dev),
@@ -156,7 +181,7 @@ def uniform_bits(n, dt, seed, bound):
 def test_fixed_max_mode(wave, oracle, dev, dt, bound, B, Hq, Hkv, S, causal, waves):
     """qk_max_abs mode (wave_flash_attention.py:63-75, :108-113): inputs
     within the declared bound, every row against the double-precision
-    softmax at 2e-2."""
+    softmax at FIXED_TOL beyond the output rounding."""
     D = 128
     q = uniform_bits(B * Hq * S * D, dt, 21, bound)
     k = uniform_bits(B * Hkv * S * D, dt, 22, bound)
@@ -171,18 +196,21 @@ def test_fixed_max_mode(wave, oracle, dev, dt, bound, B, Hq, Hkv, S, causal, wav
     ref = oracle.attention_rows(q, k, v, dtype=dt, batch=B, q_heads=Hq, kv_heads=Hkv,
                                 seq_q=S, seq_k=S, head_dim=D, causal=causal,
                                 scale=1.0 / math.sqrt(D), heads=hh.ravel(), rows=rr.ravel())
-    assert float(np.abs(got[hh.ravel(), rr.ravel()] - ref).max()) <= TOL
+    assert excess_error(got[hh.ravel(), rr.ravel()], ref, dt) <= FIXED_TOL[dt]
 
 
 def test_fixed_max_reference_inputs(wave, oracle, dev):
     """The reference runner's bf16 inputs (|Q|, |K| <= 0.25) under its
-    qk_max_abs=1 profile agree with the adaptive kernel within 2e-2."""
+    qk_max_abs=1 profile agree with the adaptive kernel: each is within
+    REF_TOL of the exact softmax beyond one bf16 rounding, so the two are
+    within 2 * REF_TOL beyond two."""
     S = 512
     q, k, v = oracle.fa_gfx950_inputs(S * 128, 5, 1)
     qt, kt, vt = (to_dev(x, torch.bfloat16, dev).view(1, 1, S, 128) for x in (q, k, v))
     fixed = wave.flash_attention(qt, kt, vt, qk_max_abs=1.0).float()
     adaptive = wave.flash_attention(qt, kt, vt).float()
-    assert float((fixed - adaptive).abs().max()) <= TOL
+    diff = (fixed - adaptive).abs() - 2 * HALF_ULP[2] * adaptive.abs()
+    assert float(diff.max()) <= 2 * REF_TOL
 
 
 def test_config_launch_rejects_bad_waves_and_bounds(wave, dev):

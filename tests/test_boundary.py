@@ -179,7 +179,7 @@ def test_fa_f32_rejects_bad_arguments(wave):
     L = wave.runtime.lib()
     assert L.wave_fa_f32_launch(None, 32, 48, 64, 16, 16, 32, None) == -1
     assert L.wave_fa_f32_launch(16, 32, 48, 64, 0, 16, 32, None) == -1
-    assert L.wave_fa_f32_launch(16, 32, 48, 64, 16, 20000, 32, None) == -2
+    assert L.wave_fa_f32_launch(16, 32, 48, 64, 16, 1 << 26, 64, None) == -1  # 2^32 elements
 
 
 def test_product_does_not_import_oracle():

@@ -21,7 +21,7 @@ dynamic LDS and bare-pointer arguments), checked against the oracle.
   zero afterwards (runner.cpp:1718-1742).
 * flash_attention_bf16_gfx950(Q, K, V, O): grid (S/256, B*H), block 512,
   dynamic LDS 136192 set with hipFuncSetAttribute (wave-fa-gfx950-runner.cpp
-  :396-428); tolerance 2e-2.
+  :396-428); 1.35e-3 beyond the bf16 rounding of O.
 * flash_attention_f32(Q, K, V, O): grid 1, the runner's --threads
   (wave-fa-calibrate-runner.cpp:346-361); tolerance 3e-3 (:263).
 """
@@ -307,8 +307,9 @@ def test_streamk_runner_launch(co, wave, oracle, dev, workers):
 def test_fa_bf16_runner_launch(co, wave, oracle, dev):
     """B1 H2 S512 bf16 with the reference's bucket inputs (runner :194-202),
     grid (S/256, B*H) = (2, 2), block 512, dynamic LDS 136192: every row
-    within 2e-2 of the double-precision reference, and bit-identical to
-    wave_fa_fwd_launch."""
+    within the reference's 1.35e-3 of the double-precision softmax beyond the
+    bf16 rounding of O (WaveGfx950FlashAttention.md:39-41), and bit-identical
+    to wave_fa_fwd_launch."""
     Bt, H, S, D = 1, 2, 512, 128
     q, k, v = oracle.fa_gfx950_inputs(Bt * H * S * D, 3, 1)
     Q, Kt, V = (to_dev(x, torch.bfloat16, dev).view(Bt, H, S, D) for x in (q, k, v))
@@ -322,7 +323,8 @@ def test_fa_bf16_runner_launch(co, wave, oracle, dev):
     ref = oracle.attention_rows(q, k, v, dtype=2, batch=Bt, q_heads=H, kv_heads=H, seq_q=S,
                                 seq_k=S, head_dim=D, causal=False, scale=1.0 / math.sqrt(D),
                                 heads=hh.ravel(), rows=rr.ravel())
-    assert float(np.abs(got[hh.ravel(), rr.ravel()] - ref).max()) <= 2e-2
+    excess = np.abs(got[hh.ravel(), rr.ravel()] - ref) - 2.0 ** -8 * np.abs(ref)
+    assert float(excess.max()) <= 1.35e-3
     assert torch.equal(O, wave.flash_attention(Q, Kt, V))
 
 
