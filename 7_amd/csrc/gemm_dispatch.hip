@@ -120,13 +120,17 @@ hipError_t launch(const GemmArgs &g, hipStream_t stream) {
   const bool fast = (g.M % kTile == 0) && (g.N % kTile == 0) &&
                     (g.K % DefaultCfg::BK == 0) && aligned_to(g.A, 16) &&
                     aligned_to(g.B, 16) && p.c_vec_ok && !g.force_masked;
+  // Ragged M / N or K off the 32-element stage: the hybrid DMA path for the
+  // tiled kernel (rows every 8 bytes at least, so each 16-byte DMA access is
+  // dword-aligned), unless the caller forces the bounds-checked one.
+  const bool hybrid = !g.force_masked && !g.packed && g.workers == 0;
   int mode = 1;
   if (fast)
     mode = 0;
   else if (g.K % 8 == 0 && aligned_to(g.A, 16) && aligned_to(g.B, 16))
-    mode = 8;
+    mode = hybrid ? kModeHybrid8 : 8;
   else if (g.K % 4 == 0 && aligned_to(g.A, 8) && aligned_to(g.B, 8))
-    mode = 4;
+    mode = hybrid ? kModeHybrid4 : 4;
   const bool sk = g.workers > 0;
   if (g.in_dtype == kF16)
     return launch_in<kF16>(p, g.out_dtype, cm, sk, mode, stream);

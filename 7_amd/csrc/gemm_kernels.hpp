@@ -290,7 +290,14 @@ __device__ __forceinline__ u32x4 load_chunk(const uint16_t *row, int k, int K) {
 
 // Accumulate C-tile (m0, n0) over K steps [kt_begin, kt_end) (in units of
 // C::BK elements) into acc.
-template <class C, int IN_DT, bool COL_MAJOR, bool MASKED, int VEC>
+// HYBRID (with !MASKED, one MFMA slice per stage): the DMA ring for tiles
+// that cross M or N and for K that is not a multiple of BK.  Rows past M / N
+// are fetched from the last valid row instead (their products only reach C
+// rows / columns that are never stored), the stages wholly inside K run the
+// DMA pipeline, and a K remainder is one more stage copied through VGPRs
+// with zero fill past K (VEC elements per access, as the masked path).  Every
+// DMA access is dword-aligned when K is even and A, B are 4-byte aligned.
+template <class C, int IN_DT, bool COL_MAJOR, bool MASKED, int VEC, bool HYBRID = false>
 __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
                                          int kt_begin, int kt_end,
                                          uint8_t *smem,
@@ -464,19 +471,32 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
   };
   auto body = [&](uint32_t stage) { body_h(stage, no_hook); };
 
-  const int nk = kt_end - kt_begin;
-  if (nk <= 0)
+  static_assert(!HYBRID || (!MASKED && C::KS == 1 && !is_fp4(IN_DT)),
+                "the hybrid path is the one-slice 16-bit DMA path");
+  // HYBRID: the DMA pipeline covers the stages wholly inside K.
+  const int kt_last = HYBRID ? min(kt_end, p.K / C::BK) : kt_end;
+  const int nk = kt_last - kt_begin;
+  const bool tail = HYBRID && kt_end > kt_last && kt_last >= kt_begin;
+  if (nk <= 0 && !tail)
     return;
 
   if constexpr (!MASKED) {
     // Global byte offsets of this lane's DMA chunks (same for A and B).
     const uint32_t rowbytes = (uint32_t)p.K * 2u;
     uint32_t goff[C::DMA];
+    // HYBRID: B's offsets differ (rows clamped to N instead of M).
+    uint32_t goff_bh[HYBRID ? C::DMA : 1];
 #pragma unroll
     for (int i = 0; i < C::DMA; ++i) {
       // Lane l of DMA issue i fills physical slot l%8 of super-row R.
       const uint32_t R = (wave * C::DMA + i) * 8 + (lane >> 3), ps = lane & 7;
-      goff[i] = Geo<C>::row_of(R, ps) * rowbytes + (Geo<C>::chunk_of(R, ps) << 4);
+      const uint32_t row = Geo<C>::row_of(R, ps), cb = Geo<C>::chunk_of(R, ps) << 4;
+      if constexpr (HYBRID) {
+        goff[i] = min(row, (uint32_t)(p.M - m0 - 1)) * rowbytes + cb;
+        goff_bh[i] = min(row, (uint32_t)(p.N - n0 - 1)) * rowbytes + cb;
+      } else {
+        goff[i] = row * rowbytes + cb;
+      }
     }
     const char *a_tile =
         reinterpret_cast<const char *>(p.A) + (size_t)m0 * rowbytes;
@@ -515,8 +535,12 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
     // block (wave*DMA + i); a row block spans 16 rows x 2*p.K bytes.
     uint32_t goff_b[C::DMA];
 #pragma unroll
-    for (int i = 0; i < C::DMA; ++i)
-      goff_b[i] = kAiter ? (wave * C::DMA + i) * 32u * (uint32_t)p.K + lane * 16u : goff[i];
+    for (int i = 0; i < C::DMA; ++i) {
+      if constexpr (HYBRID)
+        goff_b[i] = goff_bh[i];
+      else
+        goff_b[i] = kAiter ? (wave * C::DMA + i) * 32u * (uint32_t)p.K + lane * 16u : goff[i];
+    }
     // DMA d of one stage (0 <= d < 2*DMA): A chunks first, then B; MXFP4
     // adds d = 2*DMA (A scales) and 2*DMA + 1 (B scales).
     auto issue_one = [&](uint32_t stage, int kt, int d) {
@@ -564,6 +588,39 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
         if (d * G / D2 == g)
           issue_one(stage, kt, d);
     };
+    // HYBRID K remainder: stage kt_last copied through VGPRs into ring slot
+    // 0 (zero past K, rows past M / N read as zero), then one MFMA step.
+    // Runs after the pipeline's final wait + barrier, so no DMA is in flight
+    // and no wave still reads the ring.
+    auto tail_stage = [&]() {
+      if constexpr (HYBRID) {
+#pragma unroll
+        for (int i = 0; i < C::DMA; ++i) {
+          const uint32_t R = (wave * C::DMA + i) * 8 + (lane >> 3), ps = lane & 7;
+          const int r = (int)Geo<C>::row_of(R, ps);
+          const int kc = kt_last * C::BK + (int)(Geo<C>::chunk_of(R, ps) * 8);
+          const uint16_t *ar = m0 + r < p.M ? p.A + (size_t)(m0 + r) * p.K : nullptr;
+          const uint16_t *br = n0 + r < p.N ? p.B + (size_t)(n0 + r) * p.K : nullptr;
+          const u32x4 va = load_chunk<VEC>(ar, kc, p.K);
+          const u32x4 vb = load_chunk<VEC>(br, kc, p.K);
+          uint8_t *d = smem + (wave * C::DMA + i) * 1024 + lane * 16;
+          *reinterpret_cast<u32x4 *>(d) = va;
+          *reinterpret_cast<u32x4 *>(d + C::OPB) = vb;
+        }
+        lds_barrier();
+        read_frags(f[0], 0, 0);
+        // Asm MFMA hazard: the accumulators' VALU zero fill (K < BK: no
+        // pipeline ran) stays 2+ wait states ahead.
+        asm volatile("s_nop 4" ::: "memory");
+        step(f[0], f[1], false, 0, 0, no_hook, std::integral_constant<int, TP>{});
+        mfma_asm_drain();
+        lds_barrier();  // fragment reads done before the ring is reused
+      }
+    };
+    if (nk <= 0) {
+      tail_stage();
+      return;
+    }
     // Prologue: stages 0 .. NSTAGE-2 in flight, wait for stage 0.
 #pragma unroll
     for (int s = 0; s + 1 < C::NSTAGE; ++s)
@@ -588,7 +645,7 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       const auto rg = std::integral_constant<int, kRg>{};
       auto next = [&](Frag &cur, Frag &nxt) {
         const uint32_t ahead = (stage + C::NSTAGE - 1) % C::NSTAGE;
-        const int kt_ahead = min(kt_begin + i + C::NSTAGE - 1, kt_end - 1);
+        const int kt_ahead = min(kt_begin + i + C::NSTAGE - 1, kt_last - 1);
         vm_wait_barrier<kVm>();
         stage = (stage + 1) % C::NSTAGE;
         step(cur, nxt, true, stage, 0,
@@ -611,6 +668,8 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       }
       mfma_asm_drain();
       vm_wait_barrier();
+      if (tail)
+        tail_stage();
       return;
     }
     read_frags(f[0], 0, 0);
@@ -791,8 +850,10 @@ __device__ __forceinline__ void store_tile(const Params &p, int m0, int n0,
 // of r is set: the 32 lanes of one scattered write (32 lines, one chunk
 // half each) then cover all 64 banks, and the line reads are contiguous.
 // Needs: the mainloop's LDS reads and DMA finished, a whole tile, C 16-byte
-// aligned and ldc * 2 a multiple of 16 bytes.
-template <class C, int OUT_DT, bool COL_MAJOR, typename Get>
+// aligned and ldc * 2 a multiple of 16 bytes.  MASKED: any tile and any C;
+// the line runs are cut at M / N, and a 16-byte piece that is partly outside
+// or not 16-byte aligned in C is written element by element.
+template <class C, int OUT_DT, bool COL_MAJOR, bool MASKED = false, typename Get>
 __device__ __forceinline__ void store_tile_lds(const Params &p, int m0, int n0, uint8_t *smem,
                                                Get get) {
   static_assert(OUT_DT != kF32, "16-bit outputs only");
@@ -824,6 +885,8 @@ __device__ __forceinline__ void store_tile_lds(const Params &p, int m0, int n0, 
   }
   lds_barrier();
   constexpr int PER = 256 * CH / C::THREADS;
+  const int Pext = COL_MAJOR ? p.M : p.N, Qext = COL_MAJOR ? p.N : p.M;
+  const bool vec16 = ((((uintptr_t)p.C | (uintptr_t)p.ldc * 2) & 15) == 0);
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const uint32_t flat = i * C::THREADS + tid;
@@ -832,23 +895,43 @@ __device__ __forceinline__ void store_tile_lds(const Params &p, int m0, int n0, 
     if ((r >> 4) & 1u)
       v = u32x4{v[2], v[3], v[0], v[1]};
     const size_t q = (size_t)(Q0 + (int)r);
-    *reinterpret_cast<u32x4 *>(out + (q * p.ldc + P0) * 2 + c * 16) = v;
+    if constexpr (!MASKED) {
+      *reinterpret_cast<u32x4 *>(out + (q * p.ldc + P0) * 2 + c * 16) = v;
+    } else {
+      const int pc = P0 + 8 * (int)c;
+      if ((int)q < Qext && pc < Pext) {
+        uint16_t *dst = reinterpret_cast<uint16_t *>(p.C) + q * p.ldc + pc;
+        if (vec16 && pc + 8 <= Pext) {
+          *reinterpret_cast<u32x4 *>(dst) = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (pc + e < Pext)
+              dst[e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+        }
+      }
+    }
   }
   // Every wave's line reads are done before LDS is written again (the next
   // tile's DMA ring in a grid-stride caller).
   lds_barrier();
 }
 
-// Store one finished tile: 16-bit output of a whole tile goes through LDS
-// (store_tile_lds) when C allows 16-byte line runs; f32 output, twice the
-// bytes, is bound by HBM writes either way and is stored directly (measured
-// faster), as are ragged tiles.
+// Store one finished tile: 16-bit output goes through LDS (store_tile_lds):
+// whole tiles when C allows 16-byte line runs, ragged tiles always (with
+// bounds checks on the line runs, which also keeps the per-accumulator
+// bounds logic and its registers out of the kernel; not with 16 waves,
+// whose 128 registers a wave it overflows); f32 output, twice the bytes, is
+// bound by HBM writes either way and is stored directly (measured faster).
 // Tile-packed C is stored directly: each wave's 64 lanes already write one
 // contiguous 16x16 tile.
 template <class C, int OUT_DT, bool COL_MAJOR, bool MASKED, bool PACKED = false, typename Get>
 __device__ __forceinline__ void store_out(const Params &p, int m0, int n0, uint8_t *smem,
                                           Get get) {
-  if constexpr (!MASKED && !PACKED && OUT_DT != kF32) {
+  if constexpr (MASKED && !PACKED && OUT_DT != kF32 && C::WAVES < 16) {
+    store_tile_lds<C, OUT_DT, COL_MAJOR, true>(p, m0, n0, smem, get);
+    return;
+  } else if constexpr (!MASKED && !PACKED && OUT_DT != kF32) {
     if ((((uintptr_t)p.C | (uintptr_t)p.ldc * 2) & 15) == 0) {
       store_tile_lds<C, OUT_DT, COL_MAJOR>(p, m0, n0, smem, get);
       return;
@@ -864,11 +947,14 @@ template <int IN_DT, int W = 0>
 using CfgFor = std::conditional_t<IN_DT == kMXFP4, Fp4CfgW<W>,
                                   std::conditional_t<IN_DT == kMXFP4A, Fp4ACfgW<W>, TileCfgW<W>>>;
 
+// HYBRID: every tile on the DMA ring (see mainloop), edge tiles stored with
+// bounds checks.
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC, int W = 0,
-          bool PACKED = false>
+          bool PACKED = false, bool HYBRID = false>
 __device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *smem) {
   // Whole tiles run TileCfg's MFMA shape; ragged tiles the 32x32 one.
   using C = std::conditional_t<MASKED, DefaultCfgW<W>, CfgFor<IN_DT, W>>;
+  static_assert(!HYBRID || (!MASKED && !PACKED), "hybrid: row- or column-major C");
   static_assert(C::SMEM == CfgFor<IN_DT, W>::SMEM && C::THREADS == CfgFor<IN_DT, W>::THREADS,
                 "one LDS size and block size per input type");
   static_assert(!is_fp4(IN_DT) || !MASKED, "MXFP4 takes whole tiles only");
@@ -892,7 +978,14 @@ __device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *sme
     return f32x4{acc[tp][tq][4 * g], acc[tp][tq][4 * g + 1],
                  acc[tp][tq][4 * g + 2], acc[tp][tq][4 * g + 3]};
   };
-  if constexpr (C::PASSES == 1) {
+  if constexpr (HYBRID) {
+    zero();
+    mainloop<C, IN_DT, COL_MAJOR, false, VEC, true>(p, m0, n0, 0, kt_n, smem, acc);
+    if constexpr (OUT_DT != kF32)
+      store_tile_lds<C, OUT_DT, COL_MAJOR, true>(p, m0, n0, smem, get);
+    else
+      store_tile<C, OUT_DT, COL_MAJOR, true>(p, m0, n0, get);
+  } else if constexpr (C::PASSES == 1) {
     zero();
     mainloop<C, IN_DT, COL_MAJOR, MASKED, VEC>(p, m0, n0, 0, kt_n, smem, acc);
     store_out<C, OUT_DT, COL_MAJOR, MASKED, PACKED>(p, m0, n0, smem, get);
@@ -906,10 +999,11 @@ __device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *sme
   }
 }
 
-template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC, bool PACKED = false>
+template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC, bool PACKED = false,
+          bool HYBRID = false>
 __global__ __launch_bounds__(CfgFor<IN_DT>::THREADS, 1) void tiled_kernel(Params p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[CfgFor<IN_DT>::SMEM];
-  tiled_cta<IN_DT, OUT_DT, COL_MAJOR, MASKED, VEC, 0, PACKED>(p, blockIdx.x, smem);
+  tiled_cta<IN_DT, OUT_DT, COL_MAJOR, MASKED, VEC, 0, PACKED, HYBRID>(p, blockIdx.x, smem);
 }
 
 // ---------------------------------------------------------------- Stream-K
@@ -1072,7 +1166,10 @@ __global__ __launch_bounds__(DefaultCfg::THREADS, 1) void streamk_kernel(Params 
 
 // ------------------------------------------------------------- launchers
 // mode: 0 = aligned fast path (LDS DMA), 8/4/1 = masked path with that many
-// elements per global load.
+// elements per global load, kModeHybrid8/4 = hybrid DMA path whose K tail
+// loads 8/4 elements at a time (tiled kernel; Stream-K and tile-packed C
+// run the masked path with the same load width instead).
+constexpr int kModeHybrid8 = 18, kModeHybrid4 = 14;
 template <int IN_DT, int OUT_DT, bool CM, bool SK>
 hipError_t launch_variant(const Params &p, int mode, hipStream_t stream) {
   const dim3 block(DefaultCfg::THREADS);
@@ -1094,17 +1191,29 @@ hipError_t launch_variant(const Params &p, int mode, hipStream_t stream) {
     if (p.pk) {
       switch (mode) {
       case 0: WAVE_LAUNCH_PACKED(false, 8); break;
-      case 8: WAVE_LAUNCH_PACKED(true, 8); break;
-      case 4: WAVE_LAUNCH_PACKED(true, 4); break;
+      case 8: case kModeHybrid8: WAVE_LAUNCH_PACKED(true, 8); break;
+      case 4: case kModeHybrid4: WAVE_LAUNCH_PACKED(true, 4); break;
       default: WAVE_LAUNCH_PACKED(true, 1); break;
       }
       return hipGetLastError();
     }
   }
+  // Hybrid DMA path (tiled kernel only; Stream-K takes the masked one).
+  if constexpr (!SK) {
+    if (mode == kModeHybrid8 || mode == kModeHybrid4) {
+      if (mode == kModeHybrid8)
+        hipLaunchKernelGGL((tiled_kernel<IN_DT, OUT_DT, CM, false, 8, false, true>), grid, block,
+                           0, stream, p);
+      else
+        hipLaunchKernelGGL((tiled_kernel<IN_DT, OUT_DT, CM, false, 4, false, true>), grid, block,
+                           0, stream, p);
+      return hipGetLastError();
+    }
+  }
   switch (mode) {
   case 0: WAVE_LAUNCH(false, 8); break;
-  case 8: WAVE_LAUNCH(true, 8); break;
-  case 4: WAVE_LAUNCH(true, 4); break;
+  case 8: case kModeHybrid8: WAVE_LAUNCH(true, 8); break;
+  case 4: case kModeHybrid4: WAVE_LAUNCH(true, 4); break;
   default: WAVE_LAUNCH(true, 1); break;
   }
 #undef WAVE_LAUNCH

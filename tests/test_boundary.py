@@ -220,7 +220,7 @@ STATIC_LDS = {"gemm_": 131072, "streamk_": 131076, "mxfp4_": 139264, "mxfp4a_": 
 # 4-wave bf16 object (bounds-checked loads at 512 registers), and a few
 # spills outside the K loop where a 16-wave (128 registers a wave) or 8-wave
 # MXFP4 body sits at its register limit.
-SPILLS_ALLOWED = {"gemm_bf16_bf16_cm_300x200x100": 80, "gemm_f16_f16_cm_1024x512x256_b1024": 12,
+SPILLS_ALLOWED = {"gemm_f16_f16_cm_1024x512x256_b1024": 12,
                   "gemm_bf16_bf16_rm_300x200x100_b1024": 4, "mxfp4_f16_cm_4096x4096x8192": 2}
 
 

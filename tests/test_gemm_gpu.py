@@ -69,7 +69,12 @@ def test_integration_64x96x64_seed37(wave, oracle, dev):
                                    (130, 70, 63), (64, 96, 64),
                                    # whole tiles with an odd number of 32-deep
                                    # K stages (1, 3, 5)
-                                   (256, 512, 32), (512, 256, 96), (256, 256, 160)])
+                                   (256, 512, 32), (512, 256, 96), (256, 256, 160),
+                                   # ragged tiles on the DMA ring: K below one
+                                   # stage (tail only), K % 32 = 8 and 4, C
+                                   # lines not 16-byte aligned (N, M = 300, 270)
+                                   (300, 260, 20), (300, 300, 200), (270, 300, 72),
+                                   (1000, 600, 36)])
 def test_bucket_inputs_bit_exact(wave, oracle, dev, in_dt, out_dt, layout, shape):
     M, N, K = shape
     _, _, c, ref = run_gemm(wave, oracle, dev, M, N, K, in_dt, out_dt, layout, seed=9)
