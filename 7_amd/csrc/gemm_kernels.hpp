@@ -1037,9 +1037,10 @@ __device__ __forceinline__ int sk_slot(int total, int workers, int w, int tile,
   return first_whole ? 0 : 1;
 }
 
-// Per-thread scratch layout: element e (0 .. 65536/THREADS - 1) of thread
-// t's share of the 256x256 tile lives at slot_base + e * THREADS + t, so
-// publishing and reducing are fully coalesced and need no coordinate math.
+// Per-thread scratch layout: 16-byte group j (0 .. 65536/THREADS/4 - 1) of
+// thread t's share of the 256x256 tile lives at f32x4 index
+// slot_base/4 + j * THREADS + t, so publishing and reducing are fully
+// coalesced 16-byte accesses and need no coordinate math.
 // Worker `worker` of p.workers.  smem: DefaultCfg::SMEM bytes of
 // 1024-byte-aligned LDS; arrival: one int of LDS.
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
@@ -1049,7 +1050,6 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
   using C = std::conditional_t<MASKED, DefaultCfg, TileCfg>;
   static_assert(C::SMEM == DefaultCfg::SMEM && C::THREADS == DefaultCfg::THREADS,
                 "one LDS size and block size");
-  constexpr int NR = C::NG * 4;  // accumulator registers per MFMA tile
   // XCD-aware worker numbering, as for tiled CTAs: the dispatcher places
   // workgroup i on XCD i % 8, so renumbering makes the workers of one XCD
   // consecutive; their work units, and so their tiles, are then adjacent and
@@ -1111,15 +1111,19 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
     mainloop<C, IN_DT, COL_MAJOR, MASKED, VEC>(
         p, tm * kTile, tn * kTile, kb * kStepsPerUnit,
         min(ke * kStepsPerUnit, ksteps), smem, acc);
-    // Publish this worker's fp32 partial.
-    float *mine = p.scratch + ((size_t)worker * 2 + slot) * kTileElems;
+    // Publish this worker's fp32 partial: 16-byte group g of MFMA tile
+    // (tp, tq) of thread t at f32x4 index ((tp*TQ + tq)*NG + g)*NT + t, so
+    // every store and load instruction covers 4 KiB contiguously.
+    f32x4 *mine = reinterpret_cast<f32x4 *>(p.scratch + ((size_t)worker * 2 + slot) * kTileElems);
 #pragma unroll
     for (int tp = 0; tp < TP; ++tp)
 #pragma unroll
       for (int tq = 0; tq < TQ; ++tq)
 #pragma unroll
-        for (int r = 0; r < NR; ++r)
-          mine[((tp * TQ + tq) * NR + r) * NT + threadIdx.x] = acc[tp][tq][r];
+        for (int g = 0; g < C::NG; ++g)
+          mine[((tp * TQ + tq) * C::NG + g) * NT + threadIdx.x] =
+              f32x4{acc[tp][tq][4 * g], acc[tp][tq][4 * g + 1], acc[tp][tq][4 * g + 2],
+                    acc[tp][tq][4 * g + 3]};
     ++slot;
     const int first_owner = sk_owner(total, p.workers, tile * iters);
     const int last_owner = sk_owner(total, p.workers, (tile + 1) * iters - 1);
@@ -1132,24 +1136,53 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
     __syncthreads();
     if (*arrival != parts - 1)
       continue;
-    // Last arriver: reduce all contributors' partials in worker order (a
-    // fixed order, so the result does not depend on arrival order).
+    // Last arriver: reduce all contributors' partials (its own included,
+    // reloaded) in worker order, a fixed order, so the result does not
+    // depend on arrival order: s = ((0 + p_first) + p_second) + ....
     __threadfence();  // acquire the other workers' partials
-    store_tile<C, OUT_DT, COL_MAJOR, MASKED>(
-        p, tm * kTile, tn * kTile, [&](int tp, int tq, int g) {
-          f32x4 s = {0.f, 0.f, 0.f, 0.f};
-          for (int c = first_owner; c <= last_owner; ++c) {
-            const int cs = sk_slot(total, p.workers, c, tile, iters);
-            const float *part =
-                p.scratch + ((size_t)c * 2 + cs) * kTileElems;
+    auto part_of = [&](int c) {
+      return reinterpret_cast<const f32x4 *>(
+          p.scratch + ((size_t)c * 2 + sk_slot(total, p.workers, c, tile, iters)) * kTileElems);
+    };
+    auto at = [&](int tp, int tq, int g) {
+      return (size_t)((tp * TQ + tq) * C::NG + g) * NT + threadIdx.x;
+    };
+    if (parts == 2) {
+      // The partial groups of kBatch MFMA tiles of a row are loaded from
+      // both slots at the first of them, before that batch's stores (which
+      // the compiler cannot move loads across), so 2*kBatch*NG = 16 loads
+      // are in flight at once.  A contributor loop inside the callback
+      // waited out one memory round trip per group: ~140 us a tile.
+      // Stored directly: the LDS-staged epilogue costs VGPR spills here.
+      constexpr int kBatch = 8 / C::NG < TP ? 8 / C::NG : TP;
+      static_assert(TP % kBatch == 0, "whole batches per row");
+      const f32x4 *pa = part_of(first_owner), *pb = part_of(first_owner + 1);
+      f32x4 ra[kBatch][C::NG], rb[kBatch][C::NG];
+      store_tile<C, OUT_DT, COL_MAJOR, MASKED>(
+          p, tm * kTile, tn * kTile, [&](int tp, int tq, int g) {
+            if (g == 0 && tp % kBatch == 0) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              s[e] += __builtin_nontemporal_load(
-                  part + ((tp * TQ + tq) * NR + 4 * g + e) * NT +
-                  threadIdx.x);
-          }
-          return s;
-        });
+              for (int j = 0; j < kBatch; ++j)
+#pragma unroll
+                for (int h = 0; h < C::NG; ++h) {
+                  ra[j][h] = __builtin_nontemporal_load(pa + at(tp + j, tq, h));
+                  rb[j][h] = __builtin_nontemporal_load(pb + at(tp + j, tq, h));
+                }
+            }
+            f32x4 s = {0.f, 0.f, 0.f, 0.f};
+            s += ra[tp % kBatch][g];
+            s += rb[tp % kBatch][g];
+            return s;
+          });
+    } else {
+      store_tile<C, OUT_DT, COL_MAJOR, MASKED>(
+          p, tm * kTile, tn * kTile, [&](int tp, int tq, int g) {
+            f32x4 s = {0.f, 0.f, 0.f, 0.f};
+            for (int c = first_owner; c <= last_owner; ++c)
+              s += __builtin_nontemporal_load(part_of(c) + at(tp, tq, g));
+            return s;
+          });
+    }
     __syncthreads();
     if (threadIdx.x == 0)
       __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELEASE,
