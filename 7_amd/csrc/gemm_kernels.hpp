@@ -1128,8 +1128,14 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
     const int first_owner = sk_owner(total, p.workers, tile * iters);
     const int last_owner = sk_owner(total, p.workers, (tile + 1) * iters - 1);
     const int parts = last_owner - first_owner + 1;
-    __threadfence();  // release the partial at device scope
-    __syncthreads();
+    // Every wave waits for its partial stores (vmcnt(0): acknowledged by
+    // L2) before the barrier; thread 0's agent-scope acq_rel ticket then
+    // writes the XCD's L2 back, which releases all of them at once.  The
+    // last arriver's waves each invalidate with an agent-scope acquire
+    // before reading the others' partials.  So one wave per worker does the
+    // L2-wide write-back (a __threadfence in every wave did it four times,
+    // plus an invalidate each, before and after the ticket).
+    vm_wait_barrier();
     if (threadIdx.x == 0)
       *arrival = __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_ACQ_REL,
                                         __HIP_MEMORY_SCOPE_AGENT);
@@ -1139,7 +1145,7 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
     // Last arriver: reduce all contributors' partials (its own included,
     // reloaded) in worker order, a fixed order, so the result does not
     // depend on arrival order: s = ((0 + p_first) + p_second) + ....
-    __threadfence();  // acquire the other workers' partials
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     auto part_of = [&](int c) {
       return reinterpret_cast<const f32x4 *>(
           p.scratch + ((size_t)c * 2 + sk_slot(total, p.workers, c, tile, iters)) * kTileElems);
@@ -1183,9 +1189,11 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
             return s;
           });
     }
+    // Counter back to zero for the next launch (ordered after this one by
+    // the kernel boundary, so no release is needed).
     __syncthreads();
     if (threadIdx.x == 0)
-      __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELEASE,
+      __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
   }
 }
