@@ -110,6 +110,7 @@ def test_config3_streamk_bf16(wave, oracle, dev):
 @pytest.mark.parametrize("shape,streamk", [((2048, 512, 8192), True),   # 16 tiles, long K
                                            ((1000, 300, 4100), True),   # ragged, 8 tiles
                                            ((4096, 4096, 512), False),  # 256 tiles
+                                           ((4096, 2048, 4096), False),  # 128 tiles, K 4096
                                            ((128, 1024, 8192), False)])  # short-M kernel
 def test_auto_dispatch_matches_tiled(wave, oracle, dev, shape, streamk):
     """Bucket inputs make every sum exact, so the auto path (Stream-K or not)
