@@ -117,8 +117,12 @@ hipError_t launch(const GemmArgs &g, hipStream_t stream) {
   p.scratch = static_cast<float *>(g.scratch);
   p.counters = static_cast<uint32_t *>(g.counters);
   p.workers = g.workers;
+  // Whole tiles take the DMA path when K is a whole number of stages of the
+  // kernel that runs: 64 for the tiled kernel, 32 for Stream-K.
+  const bool sk = g.workers > 0;
+  const int stage_k = sk ? HybridCfgW<>::BK : TileCfg::BK;
   const bool fast = (g.M % kTile == 0) && (g.N % kTile == 0) &&
-                    (g.K % DefaultCfg::BK == 0) && aligned_to(g.A, 16) &&
+                    (g.K % stage_k == 0) && aligned_to(g.A, 16) &&
                     aligned_to(g.B, 16) && p.c_vec_ok && !g.force_masked;
   // Ragged M / N or K off the 32-element stage: the hybrid DMA path for the
   // tiled kernel (rows every 8 bytes at least, so each 16-byte DMA access is
@@ -131,7 +135,6 @@ hipError_t launch(const GemmArgs &g, hipStream_t stream) {
     mode = hybrid ? kModeHybrid8 : 8;
   else if (g.K % 4 == 0 && aligned_to(g.A, 8) && aligned_to(g.B, 8))
     mode = hybrid ? kModeHybrid4 : 4;
-  const bool sk = g.workers > 0;
   if (g.in_dtype == kF16)
     return launch_in<kF16>(p, g.out_dtype, cm, sk, mode, stream);
   return launch_in<kBF16>(p, g.out_dtype, cm, sk, mode, stream);

@@ -121,10 +121,24 @@ using DefaultCfg = DefaultCfgW<>;
 #ifndef WAVE_GEMM_MF8
 #define WAVE_GEMM_MF8 32
 #endif
-template <int W = 0>
-using TileCfgW = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE, W == 0 ? WAVE_GEMM_WAVES : W, 0,
-                     W >= 16 ? 32 : W == 8 ? WAVE_GEMM_MF8 : WAVE_GEMM_MF>;
+// 4-wave whole tiles take 64-deep stages in two buffers (one barrier per
+// stage, whole-line DMA): 8192^3 f16 1321-1331 -> 1382-1391 TFLOP/s against
+// 32-deep stages in four, one box, two runs.  Other wave counts keep the
+// 32-deep ring.
+#ifndef WAVE_GEMM_TILE_BK
+#define WAVE_GEMM_TILE_BK 64
+#endif
+template <int W = 0, int WV = (W == 0 ? WAVE_GEMM_WAVES : W)>
+using TileCfgW = Cfg<WV == 4 ? WAVE_GEMM_TILE_BK : WAVE_GEMM_BK,
+                     WV == 4 && WAVE_GEMM_TILE_BK == 64 ? 2 : WAVE_GEMM_NSTAGE, WV, 0,
+                     WV >= 16 ? 32 : WV == 8 ? WAVE_GEMM_MF8 : WAVE_GEMM_MF>;
 using TileCfg = TileCfgW<>;
+// The hybrid path (ragged tiles and K on the DMA ring) and Stream-K (whose
+// kernel inlines the main loop twice; the 64-deep loop there spills) keep
+// 32-deep stages.
+template <int W = 0>
+using HybridCfgW = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE, W == 0 ? WAVE_GEMM_WAVES : W, 0,
+                       WAVE_GEMM_MF>;
 // MXFP4: the same ring with K counted in 16-bit units (one 64-byte row
 // chunk = 128 fp4 values per stage, one MFMA 32x32x64 per 32-byte slice)
 // and 2 KiB of scales per stage: four 32-value groups x (256 A + 256 B)
@@ -672,6 +686,47 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
         tail_stage();
       return;
     }
+    if constexpr (C::KS == 2 && C::NSTAGE == 2 && MF == 16 && !is_fp4(IN_DT)) {
+      // 64-deep stages in two LDS buffers (the geometry of hipBLASLt's
+      // kernel for this shape): every DMA instruction fetches 8 whole
+      // 128-byte row segments (a 32-deep stage gives 16 half ones, and the
+      // DMA then measured to stall the MFMA stream more).
+      // Stage k sits in buffer k & 1 and is multiplied as two slices: the
+      // even step (slice (k, 0) from registers, reading slice (k, 1)) needs
+      // no barrier, since nothing it reads is new; the barrier before the
+      // odd step waits for stage k+1 (vmcnt(0)) and for every wave's reads
+      // of buffer k & 1, so the odd step (slice (k, 1), reading (k+1, 0))
+      // refills that buffer with stage k+2, two DMA issues after each of
+      // its groups.  Cover for a stage's DMA: the rest of an odd step plus
+      // an even step; one barrier per 64-deep stage.  Past the end the DMA
+      // re-fetches the last stage into the free buffer.
+      static_assert(!HYBRID, "the hybrid path keeps 32-deep stages");
+      constexpr int D2 = kDmaPerStage;
+      // Two issues after each of the odd step's groups: spread over 4 or 2
+      // groups they measured 1.1 and 4.6 % slower (the DMA backs up).
+      auto issue_spread = [&](uint32_t buf, int k, int tp) {
+#pragma unroll
+        for (int d = 0; d < D2; ++d)
+          if (d * TP / D2 == tp)
+            issue_one(buf, kt_begin + min(k, nk - 1), d);
+      };
+      issue(0, kt_begin);
+      issue(1, kt_begin + min(1, nk - 1));
+      vm_wait_barrier<D2>();  // stage 0 has landed
+      read_frags(f[0], 0, 0);
+      asm volatile("s_nop 4" ::: "memory");  // VALU zero fill -> asm MFMA
+      const auto rg = std::integral_constant<int, TP>{};
+      for (int k = 0; k < nk; ++k) {
+        const uint32_t buf = (uint32_t)(k & 1);
+        step(f[0], f[1], true, buf, 1, no_hook, rg);
+        vm_wait_barrier<0>();
+        step(f[1], f[0], k + 1 < nk, buf ^ 1u, 0,
+             [&](int tp) { issue_spread(buf, k + 2, tp); }, rg);
+      }
+      mfma_asm_drain();
+      vm_wait_barrier();
+      return;
+    }
     read_frags(f[0], 0, 0);
     if constexpr (MF == 16)  // asm MFMAs: the one-slice path's hazard rules
       asm volatile("s_nop 4" ::: "memory");
@@ -953,7 +1008,8 @@ template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC, int W = 0
           bool PACKED = false, bool HYBRID = false>
 __device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *smem) {
   // Whole tiles run TileCfg's MFMA shape; ragged tiles the 32x32 one.
-  using C = std::conditional_t<MASKED, DefaultCfgW<W>, CfgFor<IN_DT, W>>;
+  using C = std::conditional_t<MASKED, DefaultCfgW<W>,
+                               std::conditional_t<HYBRID, HybridCfgW<W>, CfgFor<IN_DT, W>>>;
   static_assert(!HYBRID || (!MASKED && !PACKED), "hybrid: row- or column-major C");
   static_assert(C::SMEM == CfgFor<IN_DT, W>::SMEM && C::THREADS == CfgFor<IN_DT, W>::THREADS,
                 "one LDS size and block size per input type");
@@ -1046,8 +1102,9 @@ __device__ __forceinline__ int sk_slot(int total, int workers, int w, int tile,
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
 __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t *smem,
                                             int *arrival) {
-  // Whole-tile ranges run TileCfg's MFMA shape; ragged tiles the 32x32 one.
-  using C = std::conditional_t<MASKED, DefaultCfg, TileCfg>;
+  // Whole-tile ranges run the 16x16 MFMA shape (32-deep stages); ragged
+  // tiles the 32x32 one.
+  using C = std::conditional_t<MASKED, DefaultCfg, HybridCfgW<>>;
   static_assert(C::SMEM == DefaultCfg::SMEM && C::THREADS == DefaultCfg::THREADS,
                 "one LDS size and block size");
   // XCD-aware worker numbering, as for tiled CTAs: the dispatcher places

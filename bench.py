@@ -188,6 +188,42 @@ def rand_int_operand(rows, k, stream, torch):
     return torch.from_numpy(v.reshape(rows, k)).to(torch.float16)
 
 
+def vendor_lines(torch, dev, a, b, steps):
+    """The vendor libraries on the same box and inputs, for scale: hipBLASLt
+    (torch.matmul, C = A . B^T, f16) on the headline GEMM and PyTorch's SDPA
+    flash backend (forced, so nothing falls back to batched matmuls) on
+    config 4.  Not this build's code; reported beside it."""
+    lines = []
+    c = torch.empty((a.shape[0], b.shape[0]), dtype=torch.float16, device=dev)
+    ms = time_launches(lambda: torch.matmul(a, b.t(), out=c), steps, 3, torch)
+    tf = 2.0 * a.shape[0] * b.shape[0] * a.shape[1] / (ms * 1e-3) / 1e12
+    log(f"vendor: torch.matmul (hipBLASLt) f16 8192^3: {ms * 1e3:.1f} us/launch, {tf:.1f} TFLOP/s")
+    lines.append({"workload": "vendor_hipblaslt_gemm_f16_8192x8192x8192", "value": round(tf, 2),
+                  "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+                  "frac_of_mfma_peak": round(tf / MFMA_PEAK_TFLOPS, 4),
+                  "kernel": "torch.matmul(A, B.t()), same inputs as the headline"})
+    del c
+    B, H, S, D = 4, 32, 4096, 128
+    g = torch.Generator(device=dev).manual_seed(11)
+    q, k, v = (torch.randn((B, H, S, D), generator=g, device=dev).to(torch.float16)
+               for _ in range(3))
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+            ms = time_launches(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v),
+                               10, 3, torch)
+        tf = 4.0 * B * H * S * S * D / (ms * 1e-3) / 1e12
+        log(f"vendor: torch SDPA flash f16 B4 H32 S4096 D128: {ms * 1e3:.1f} us/launch, "
+            f"{tf:.1f} TFLOP/s")
+        lines.append({"workload": "vendor_torch_sdpa_flash_f16_b4_h32_s4096_d128",
+                      "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+                      "frac_of_mfma_peak": round(tf / MFMA_PEAK_TFLOPS, 4)})
+    except (RuntimeError, ImportError) as e:
+        log(f"vendor: torch SDPA flash unavailable ({type(e).__name__})")
+    del q, k, v
+    return lines
+
+
 def mxfp4_line(wave, torch, dev, steps, warmup):
     """MXFP4 scaled GEMM at the reference's MXFP4 profile shape (4096 x 4096
     x 32768, f16 column-major C): random e2m1 codes (every nibble uniform
@@ -449,6 +485,7 @@ def main():
                               "source": "docs/PerfReferences/WaveGfx950FlashAttention.md:67"}})
         del q, k, v, o
         secondary.append(mxfp4_line(wave, torch, dev, 20, 3))
+        secondary.extend(vendor_lines(torch, dev, a, b, max(10, args.steps // 2)))
 
     cpu = None
     ref_cpu = None
