@@ -702,13 +702,12 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       // re-fetches the last stage into the free buffer.
       static_assert(!HYBRID, "the hybrid path keeps 32-deep stages");
       constexpr int D2 = kDmaPerStage;
-      // Two issues after each of the odd step's groups: spread over 4 or 2
-      // groups they measured 1.1 and 4.6 % slower (the DMA backs up).
+      // Stage k+2's 16 DMA issues go two after each of the odd step's groups.
+      // Spread over 4 or 2 groups they measured 1 and 5 % slower (the DMA
+      // backs up); moving 4 or 8 of them into the even step k+1, 5-7 %
+      // slower (the even step's groups then wait on LDS).
       auto issue_spread = [&](uint32_t buf, int k, int tp) {
-#pragma unroll
-        for (int d = 0; d < D2; ++d)
-          if (d * TP / D2 == tp)
-            issue_one(buf, kt_begin + min(k, nk - 1), d);
+        for (int d = 0; d < D2; ++d) if (d * TP / D2 == tp) issue_one(buf, kt_begin + min(k, nk - 1), d);
       };
       issue(0, kt_begin);
       issue(1, kt_begin + min(1, nk - 1));
@@ -716,12 +715,14 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       read_frags(f[0], 0, 0);
       asm volatile("s_nop 4" ::: "memory");  // VALU zero fill -> asm MFMA
       const auto rg = std::integral_constant<int, TP>{};
+      // The odd step always reads the next stage's first slice: after the
+      // last stage those reads land, unused, in registers no MFMA reads (from
+      // the other buffer, in bounds), and no read sits behind a branch.
       for (int k = 0; k < nk; ++k) {
         const uint32_t buf = (uint32_t)(k & 1);
         step(f[0], f[1], true, buf, 1, no_hook, rg);
         vm_wait_barrier<0>();
-        step(f[1], f[0], k + 1 < nk, buf ^ 1u, 0,
-             [&](int tp) { issue_spread(buf, k + 2, tp); }, rg);
+        step(f[1], f[0], true, buf ^ 1u, 0, [&](int tp) { issue_spread(buf, k + 2, tp); }, rg);
       }
       mfma_asm_drain();
       vm_wait_barrier();
