@@ -124,8 +124,8 @@ hipError_t launch(const GemmArgs &g, hipStream_t stream) {
   const bool fast = (g.M % kTile == 0) && (g.N % kTile == 0) &&
                     (g.K % stage_k == 0) && aligned_to(g.A, 16) &&
                     aligned_to(g.B, 16) && p.c_vec_ok && !g.force_masked;
-  // Ragged M / N or K off the 32-element stage: the hybrid DMA path for the
-  // tiled kernel (rows every 8 bytes at least, so each 16-byte DMA access is
+  // Ragged M / N or K off the stage: the hybrid DMA path for the tiled
+  // kernel (rows every 8 bytes at least, so each 16-byte DMA access is
   // dword-aligned), unless the caller forces the bounds-checked one.
   const bool hybrid = !g.force_masked && !g.packed && g.workers == 0;
   int mode = 1;

@@ -133,12 +133,17 @@ using TileCfgW = Cfg<WV == 4 ? WAVE_GEMM_TILE_BK : WAVE_GEMM_BK,
                      WV == 4 && WAVE_GEMM_TILE_BK == 64 ? 2 : WAVE_GEMM_NSTAGE, WV, 0,
                      WV >= 16 ? 32 : WV == 8 ? WAVE_GEMM_MF8 : WAVE_GEMM_MF>;
 using TileCfg = TileCfgW<>;
-// The hybrid path (ragged tiles and K on the DMA ring) and Stream-K (whose
-// kernel inlines the main loop twice; the 64-deep loop there spills) keep
-// 32-deep stages.
+// Stream-K (whose kernel inlines the main loop twice; the 64-deep loop there
+// spills) keeps 32-deep stages, and so does the hybrid path (ragged tiles
+// and K on the DMA ring) of other wave counts.
 template <int W = 0>
 using HybridCfgW = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE, W == 0 ? WAVE_GEMM_WAVES : W, 0,
                        WAVE_GEMM_MF>;
+// The tiled kernel's hybrid path: the 64-deep two-buffer ring where whole
+// tiles run it (4 waves), else HybridCfgW.
+template <int W = 0, int WV = (W == 0 ? WAVE_GEMM_WAVES : W)>
+using HybridTileCfgW =
+    std::conditional_t<WV == 4 && WAVE_GEMM_TILE_BK == 64, TileCfgW<W>, HybridCfgW<W>>;
 // MXFP4: the same ring with K counted in 16-bit units (one 64-byte row
 // chunk = 128 fp4 values per stage, one MFMA 32x32x64 per 32-byte slice)
 // and 2 KiB of scales per stage: four 32-value groups x (256 A + 256 B)
@@ -304,7 +309,8 @@ __device__ __forceinline__ u32x4 load_chunk(const uint16_t *row, int k, int K) {
 
 // Accumulate C-tile (m0, n0) over K steps [kt_begin, kt_end) (in units of
 // C::BK elements) into acc.
-// HYBRID (with !MASKED, one MFMA slice per stage): the DMA ring for tiles
+// HYBRID (with !MASKED; one MFMA slice per stage, or the 64-deep two-buffer
+// ring): the DMA ring for tiles
 // that cross M or N and for K that is not a multiple of BK.  Rows past M / N
 // are fetched from the last valid row instead (their products only reach C
 // rows / columns that are never stored), the stages wholly inside K run the
@@ -485,8 +491,9 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
   };
   auto body = [&](uint32_t stage) { body_h(stage, no_hook); };
 
-  static_assert(!HYBRID || (!MASKED && C::KS == 1 && !is_fp4(IN_DT)),
-                "the hybrid path is the one-slice 16-bit DMA path");
+  constexpr bool kTwoBuf = C::KS == 2 && C::NSTAGE == 2 && MF == 16 && !is_fp4(IN_DT);
+  static_assert(!HYBRID || (!MASKED && (C::KS == 1 || kTwoBuf) && !is_fp4(IN_DT)),
+                "the hybrid path is the one-slice or the 64-deep 16-bit DMA path");
   // HYBRID: the DMA pipeline covers the stages wholly inside K.
   const int kt_last = HYBRID ? min(kt_end, p.K / C::BK) : kt_end;
   const int nk = kt_last - kt_begin;
@@ -603,9 +610,9 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
           issue_one(stage, kt, d);
     };
     // HYBRID K remainder: stage kt_last copied through VGPRs into ring slot
-    // 0 (zero past K, rows past M / N read as zero), then one MFMA step.
-    // Runs after the pipeline's final wait + barrier, so no DMA is in flight
-    // and no wave still reads the ring.
+    // 0 (zero past K, rows past M / N read as zero), then its MFMA steps (one
+    // per slice).  Runs after the pipeline's final wait + barrier, so no DMA
+    // is in flight and no wave still reads the ring.
     auto tail_stage = [&]() {
       if constexpr (HYBRID) {
 #pragma unroll
@@ -626,7 +633,12 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
         // Asm MFMA hazard: the accumulators' VALU zero fill (K < BK: no
         // pipeline ran) stays 2+ wait states ahead.
         asm volatile("s_nop 4" ::: "memory");
-        step(f[0], f[1], false, 0, 0, no_hook, std::integral_constant<int, TP>{});
+        if constexpr (C::KS == 2) {
+          step(f[0], f[1], true, 0, 1, no_hook, std::integral_constant<int, TP>{});
+          step(f[1], f[0], false, 0, 0, no_hook, std::integral_constant<int, TP>{});
+        } else {
+          step(f[0], f[1], false, 0, 0, no_hook, std::integral_constant<int, TP>{});
+        }
         mfma_asm_drain();
         lds_barrier();  // fragment reads done before the ring is reused
       }
@@ -686,7 +698,7 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
         tail_stage();
       return;
     }
-    if constexpr (C::KS == 2 && C::NSTAGE == 2 && MF == 16 && !is_fp4(IN_DT)) {
+    if constexpr (kTwoBuf) {
       // 64-deep stages in two LDS buffers (the geometry of hipBLASLt's
       // kernel for this shape): every DMA instruction fetches 8 whole
       // 128-byte row segments (a 32-deep stage gives 16 half ones, and the
@@ -700,7 +712,6 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       // its groups.  Cover for a stage's DMA: the rest of an odd step plus
       // an even step; one barrier per 64-deep stage.  Past the end the DMA
       // re-fetches the last stage into the free buffer.
-      static_assert(!HYBRID, "the hybrid path keeps 32-deep stages");
       constexpr int D2 = kDmaPerStage;
       // Stage k+2's 16 DMA issues go two after each of the odd step's groups.
       // Spread over 4 or 2 groups they measured 1 and 5 % slower (the DMA
@@ -726,6 +737,8 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       }
       mfma_asm_drain();
       vm_wait_barrier();
+      if (tail)
+        tail_stage();
       return;
     }
     read_frags(f[0], 0, 0);
@@ -1010,7 +1023,7 @@ template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC, int W = 0
 __device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *smem) {
   // Whole tiles run TileCfg's MFMA shape; ragged tiles the 32x32 one.
   using C = std::conditional_t<MASKED, DefaultCfgW<W>,
-                               std::conditional_t<HYBRID, HybridCfgW<W>, CfgFor<IN_DT, W>>>;
+                               std::conditional_t<HYBRID, HybridTileCfgW<W>, CfgFor<IN_DT, W>>>;
   static_assert(!HYBRID || (!MASKED && !PACKED), "hybrid: row- or column-major C");
   static_assert(C::SMEM == CfgFor<IN_DT, W>::SMEM && C::THREADS == CfgFor<IN_DT, W>::THREADS,
                 "one LDS size and block size per input type");
