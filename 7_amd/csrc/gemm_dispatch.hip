@@ -117,10 +117,10 @@ hipError_t launch(const GemmArgs &g, hipStream_t stream) {
   p.scratch = static_cast<float *>(g.scratch);
   p.counters = static_cast<uint32_t *>(g.counters);
   p.workers = g.workers;
-  // Whole tiles take the DMA path when K is a whole number of stages of the
-  // kernel that runs: 64 for the tiled kernel, 32 for Stream-K.
+  // Whole tiles take the DMA path when K is a whole number of 64-deep stages
+  // (the tiled and the Stream-K kernel).
   const bool sk = g.workers > 0;
-  const int stage_k = sk ? HybridCfgW<>::BK : TileCfg::BK;
+  const int stage_k = TileCfg::BK;
   const bool fast = (g.M % kTile == 0) && (g.N % kTile == 0) &&
                     (g.K % stage_k == 0) && aligned_to(g.A, 16) &&
                     aligned_to(g.B, 16) && p.c_vec_ok && !g.force_masked;

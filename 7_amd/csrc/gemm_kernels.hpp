@@ -133,14 +133,13 @@ using TileCfgW = Cfg<WV == 4 ? WAVE_GEMM_TILE_BK : WAVE_GEMM_BK,
                      WV == 4 && WAVE_GEMM_TILE_BK == 64 ? 2 : WAVE_GEMM_NSTAGE, WV, 0,
                      WV >= 16 ? 32 : WV == 8 ? WAVE_GEMM_MF8 : WAVE_GEMM_MF>;
 using TileCfg = TileCfgW<>;
-// Stream-K (whose kernel inlines the main loop twice; the 64-deep loop there
-// spills) keeps 32-deep stages, and so does the hybrid path (ragged tiles
-// and K on the DMA ring) of other wave counts.
+// 32-deep stages for the hybrid path (ragged tiles and K on the DMA ring) of
+// wave counts other than 4.
 template <int W = 0>
 using HybridCfgW = Cfg<WAVE_GEMM_BK, WAVE_GEMM_NSTAGE, W == 0 ? WAVE_GEMM_WAVES : W, 0,
                        WAVE_GEMM_MF>;
-// The tiled kernel's hybrid path: the 64-deep two-buffer ring where whole
-// tiles run it (4 waves), else HybridCfgW.
+// The hybrid path and Stream-K's whole-tile ranges: the 64-deep two-buffer
+// ring where whole tiles run it (4 waves), else HybridCfgW.
 template <int W = 0, int WV = (W == 0 ? WAVE_GEMM_WAVES : W)>
 using HybridTileCfgW =
     std::conditional_t<WV == 4 && WAVE_GEMM_TILE_BK == 64, TileCfgW<W>, HybridCfgW<W>>;
@@ -1116,9 +1115,9 @@ __device__ __forceinline__ int sk_slot(int total, int workers, int w, int tile,
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
 __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t *smem,
                                             int *arrival) {
-  // Whole-tile ranges run the 16x16 MFMA shape (32-deep stages); ragged
+  // Whole-tile ranges run the 16x16 MFMA shape (64-deep stages); ragged
   // tiles the 32x32 one.
-  using C = std::conditional_t<MASKED, DefaultCfg, HybridCfgW<>>;
+  using C = std::conditional_t<MASKED, DefaultCfg, HybridTileCfgW<>>;
   static_assert(C::SMEM == DefaultCfg::SMEM && C::THREADS == DefaultCfg::THREADS,
                 "one LDS size and block size");
   // XCD-aware worker numbering, as for tiled CTAs: the dispatcher places

@@ -240,7 +240,7 @@ extern "C" __global__ __launch_bounds__(256, 1) void gfx950_f16_streamk_gemm(
   p.scratch = scratch;
   p.counters = counters;
   p.workers = workers;
-  constexpr bool kFast = M % kTile == 0 && N % kTile == 0 && K % DefaultCfg::BK == 0 &&
+  constexpr bool kFast = M % kTile == 0 && N % kTile == 0 && K % HybridTileCfgW<>::BK == 0 &&
                          M % 4 == 0;
   constexpr int kVec = kFast || K % 8 == 0 ? 8 : 1;
   if (kVec == 8 && !(aligned16(A) && aligned16(B)))

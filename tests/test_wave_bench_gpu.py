@@ -44,7 +44,8 @@ def test_gemm_modes(sweep, mode, extra, shape):
     us, cycles, check = sweep.parse(out)
     assert check == "passed" and us > 0 and cycles > 0
     tf = float(re.search(r"^tflops:\s+([0-9.]+)$", out, re.M).group(1))
-    assert tf == pytest.approx(2.0 * M * N * K / us * 1e-6, rel=1e-3)
+    # tflops is printed with 3 decimals (half a digit: 5e-4 absolute).
+    assert tf == pytest.approx(2.0 * M * N * K / us * 1e-6, rel=1e-3, abs=5e-4)
     assert f"input_mode: {mode}" in out
     if "--streamk-workers" in extra:
         assert "gfx950_f16_streamk_gemm" in out
