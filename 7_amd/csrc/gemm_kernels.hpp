@@ -463,8 +463,16 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
           acc[tp][tq] = mfma32x32x16<IN_DT>(cur.p[tp], cur.q[tq], acc[tp][tq]);
         else
           mfma16x16x32_acc<IN_DT>(acc[tp][tq], cur.p[tp], cur.q[tq]);
+        // A two-argument hook also runs after the group's middle MFMA.
+        if constexpr (std::is_invocable_v<decltype(hook), int, int>) {
+          if (tq == TQ / 2 - 1)
+            hook(tp, 0);
+        }
       }
-      hook(tp);
+      if constexpr (std::is_invocable_v<decltype(hook), int, int>)
+        hook(tp, 1);
+      else
+        hook(tp);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -707,18 +715,19 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       // no barrier, since nothing it reads is new; the barrier before the
       // odd step waits for stage k+1 (vmcnt(0)) and for every wave's reads
       // of buffer k & 1, so the odd step (slice (k, 1), reading (k+1, 0))
-      // refills that buffer with stage k+2, two DMA issues after each of
-      // its groups.  Cover for a stage's DMA: the rest of an odd step plus
+      // refills that buffer with stage k+2, two DMA issues in each of its
+      // groups.  Cover for a stage's DMA: the rest of an odd step plus
       // an even step; one barrier per 64-deep stage.  Past the end the DMA
       // re-fetches the last stage into the free buffer.
       constexpr int D2 = kDmaPerStage;
-      // Stage k+2's 16 DMA issues go two after each of the odd step's groups.
-      // Spread over 4 or 2 groups they measured 1 and 5 % slower (the DMA
-      // backs up); moving 4 or 8 of them into the even step k+1, 5-7 %
-      // slower (the even step's groups then wait on LDS).
-      auto issue_spread = [&](uint32_t buf, int k, int tp) {
-        for (int d = 0; d < D2; ++d) if (d * TP / D2 == tp) issue_one(buf, kt_begin + min(k, nk - 1), d);
-      };
+      // Stage k+2's 16 DMA issues go two into each of the odd step's groups,
+      // one after its middle MFMA and one after its last: each issue stalls
+      // the wave's MFMA stream, and back to back after the group (the
+      // previous placement) measured 3.3 % more cycles a stage.  Spread over
+      // 4 or 2 groups they measured 1 and 5 % slower (the DMA backs up);
+      // moving 4 or 8 of them into the even step k+1, 5-7 % slower (the even
+      // step's groups then wait on LDS).
+      static_assert(D2 == 2 * TP, "one DMA issue per half group");
       issue(0, kt_begin);
       issue(1, kt_begin + min(1, nk - 1));
       vm_wait_barrier<D2>();  // stage 0 has landed
@@ -732,7 +741,9 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
         const uint32_t buf = (uint32_t)(k & 1);
         step(f[0], f[1], true, buf, 1, no_hook, rg);
         vm_wait_barrier<0>();
-        step(f[1], f[0], true, buf ^ 1u, 0, [&](int tp) { issue_spread(buf, k + 2, tp); }, rg);
+        step(f[1], f[0], true, buf ^ 1u, 0,
+             [&](int tp, int sub) { issue_one(buf, kt_begin + min(k + 2, nk - 1), 2 * tp + sub); },
+             rg);
       }
       mfma_asm_drain();
       vm_wait_barrier();
