@@ -441,19 +441,35 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
   // keeps the compiler from regrouping them, so DMA and LDS traffic stay
   // spread through the MFMA stream.
   // RG: the reads are spread over the first RG groups only.
+  // The 64-deep two-buffer path spreads each group's LDS reads and DMA
+  // issues between its MFMAs (reads before the 1st and 3rd, DMA after the
+  // 4th and 6th): a timing copy measured 2580 cycles a stage against 2700
+  // with the reads together before the group and the two issues after its
+  // 4th and 8th MFMAs (2815 with both issues after the 8th); the other
+  // placements tried (reads before the 1st and 5th, issues after 2nd/6th,
+  // 3rd/7th, 4th/8th) fell in between.
+  constexpr bool kSpread = C::KS == 2 && C::NSTAGE == 2 && MF == 16 && !is_fp4(IN_DT) && TQ == 8;
   auto step = [&](const Frag &cur, Frag &nxt, bool read, uint32_t nstage,
                   int nkk, auto hook, auto rg_tag) {
     constexpr int RG = decltype(rg_tag)::value;
     static_assert(RG >= 1 && RG <= TP, "every read group is one of the step's TP groups");
 #pragma unroll
     for (int tp = 0; tp < TP; ++tp) {
+      // kSpread: the group's later reads go after its second MFMA.
+      const int j0 = tp * NREAD / RG, j2 = (tp + 1) * NREAD / RG;
+      const int j1 = kSpread ? (j0 + j2) / 2 : j2;
       if (read && tp < RG) {
 #pragma unroll
-        for (int j = tp * NREAD / RG; j < (tp + 1) * NREAD / RG; ++j)
+        for (int j = j0; j < j1; ++j)
           read_one(nxt, nstage, nkk, j);
       }
 #pragma unroll
       for (int tq = 0; tq < TQ; ++tq) {
+        if (kSpread && read && tp < RG && tq == 2) {
+#pragma unroll
+          for (int j = j1; j < j2; ++j)
+            read_one(nxt, nstage, nkk, j);
+        }
         if constexpr (is_fp4(IN_DT) && MF == 32)
           acc[tp][tq] = mfma_fp4_32x32x64(cur.p[tp], cur.q[tq], acc[tp][tq], cur.sp[tp],
                                           cur.sq[tq]);
@@ -463,15 +479,15 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
           acc[tp][tq] = mfma32x32x16<IN_DT>(cur.p[tp], cur.q[tq], acc[tp][tq]);
         else
           mfma16x16x32_acc<IN_DT>(acc[tp][tq], cur.p[tp], cur.q[tq]);
-        // A two-argument hook also runs after the group's middle MFMA.
+        // A two-argument hook (two DMA issues) runs after the group's 4th
+        // and 6th MFMAs.
         if constexpr (std::is_invocable_v<decltype(hook), int, int>) {
-          if (tq == TQ / 2 - 1)
-            hook(tp, 0);
+          static_assert(TQ == 8, "issue positions within an 8-MFMA group");
+          if (tq == 3 || tq == 5)
+            hook(tp, tq == 5 ? 1 : 0);
         }
       }
-      if constexpr (std::is_invocable_v<decltype(hook), int, int>)
-        hook(tp, 1);
-      else
+      if constexpr (!std::is_invocable_v<decltype(hook), int, int>)
         hook(tp);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -721,12 +737,10 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       // re-fetches the last stage into the free buffer.
       constexpr int D2 = kDmaPerStage;
       // Stage k+2's 16 DMA issues go two into each of the odd step's groups,
-      // one after its middle MFMA and one after its last: each issue stalls
-      // the wave's MFMA stream, and back to back after the group (the
-      // previous placement) measured 3.3 % more cycles a stage.  Spread over
-      // 4 or 2 groups they measured 1 and 5 % slower (the DMA backs up);
-      // moving 4 or 8 of them into the even step k+1, 5-7 % slower (the even
-      // step's groups then wait on LDS).
+      // between its MFMAs (see kSpread): each issue stalls the wave's MFMA
+      // stream.  Spread over 4 or 2 groups they measured 1 and 5 % slower
+      // (the DMA backs up); moving 4 or 8 of them into the even step k+1,
+      // 5-7 % slower (the even step's groups then wait on LDS).
       static_assert(D2 == 2 * TP, "one DMA issue per half group");
       issue(0, kt_begin);
       issue(1, kt_begin + min(1, nk - 1));
