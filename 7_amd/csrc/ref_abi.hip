@@ -55,7 +55,7 @@
 //  * flash_attention_bf16_gfx950: grid (S/256, B*H), block 512, >= 102400
 //    bytes of dynamic LDS (the reference's 8-wave profile passes 136192 with
 //    hipFuncSetAttribute); built with WAVE_ABI_FA_WAVES=4: block 256,
-//    >= 45056 bytes (the runner's 4-wave default --threads 256
+//    >= 67584 bytes (the runner's 4-wave default --threads 256
 //    --dynamic-lds 68096).  Non-causal, one KV head per query head, scale
 //    1/sqrt(128).
 //  * flash_attention_f32: grid (1,1,1), any block size up to 1024: whole
