@@ -68,8 +68,11 @@ def test_workspace_reuse_many_launches(wave, oracle, dev):
 
 @pytest.mark.parametrize("in_dt", [1, 2])
 @pytest.mark.parametrize("out_dt", [torch.float32, torch.float16, torch.bfloat16])
+# (512, 512, 1056): whole tiles with K off the 64-deep stage, so Stream-K
+# runs its bounds-checked path and the tiled kernel its hybrid one.
 @pytest.mark.parametrize("shape,workers", [((128, 1024, 2048), 40), ((300, 520, 700), 9),
-                                           ((257, 255, 4100), 13), ((1024, 1024, 1024), 64)])
+                                           ((257, 255, 4100), 13), ((1024, 1024, 1024), 64),
+                                           ((512, 512, 1056), 7)])
 def test_ragged_streamk_matches_tiled(wave, oracle, dev, in_dt, out_dt, shape, workers):
     M, N, K = shape
     a, b, da, db = inputs(oracle, dev, M, N, K, in_dt, seed=11)
