@@ -67,9 +67,11 @@ def test_integration_64x96x64_seed37(wave, oracle, dev):
 @pytest.mark.parametrize("shape", [(256, 256, 64), (512, 768, 192), (32, 32, 64),
                                    (300, 200, 100), (1, 1, 1), (257, 513, 4100),
                                    (130, 70, 63), (64, 96, 64),
-                                   # whole tiles with an odd number of 32-deep
-                                   # K stages (1, 3, 5)
+                                   # whole tiles, K off the 64-deep stage (the
+                                   # hybrid path's 32-element tail after 0, 1, 2
+                                   # stages), and 2 and 5 whole 64-deep stages
                                    (256, 512, 32), (512, 256, 96), (256, 256, 160),
+                                   (256, 256, 128), (512, 512, 320),
                                    # ragged tiles on the DMA ring: K below one
                                    # stage (tail only), K % 32 = 8 and 4, C
                                    # lines not 16-byte aligned (N, M = 300, 270)
