@@ -158,6 +158,10 @@ using HybridTileCfgW =
 template <int W = 0>
 using Fp4CfgW = Cfg<32, 4, W == 0 ? WAVE_FP4_WAVES : W, 4 * 512, WAVE_FP4_MF>;
 using Fp4Cfg = Fp4CfgW<>;
+// Canonical MXFP4 with K a multiple of 256 values: 64-deep stages (256
+// values, 128 bytes a row, 4 KiB of scales) in two buffers, the same LDS.
+template <int W = 0>
+using Fp4Cfg64W = Cfg<64, 2, W == 0 ? WAVE_FP4_WAVES : W, 8 * 512, WAVE_FP4_MF>;
 // MXFP4 with AITER-preshuffled B and scales: the scale area holds whole
 // 256-byte AITER scale blocks (32 rows x 8 groups), 8 for A and 8 for B.
 template <int W = 0>
@@ -566,7 +570,7 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
     // AITER: 16 jobs, (A if j < 8, else B) x the 256-byte scale block of
     // rows 32*(j%8) .. +31 that holds the stage's groups.
     static_assert(!kAiter || C::NSTAGE % 2 == 0, "AITER scale half follows stage parity");
-    constexpr int SJ = IN_DT == kMXFP4 ? 8 / C::WAVES : kAiter ? 16 / C::WAVES : 0;
+    constexpr int SJ = IN_DT == kMXFP4 ? (C::BK / 4) / C::WAVES : kAiter ? 16 / C::WAVES : 0;
     uint32_t lds_sc[SJ > 0 ? SJ : 1], g_sc[SJ > 0 ? SJ : 1];
     // AITER scale blocks per 32-row block: ceil(groups / 8), groups = K/32
     // (p.K counts 16-bit units, 4 fp4 values each).
@@ -608,7 +612,7 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       } else if constexpr (IN_DT == kMXFP4) {
         const int s = d - 2 * C::DMA;
         const bool is_b = ((wave * SJ + s) & 1) != 0;
-        const uint32_t g0 = (uint32_t)kt * 4u * (uint32_t)(is_b ? p.N : p.M);
+        const uint32_t g0 = (uint32_t)kt * (C::BK / 8u) * (uint32_t)(is_b ? p.N : p.M);
         dma4(lds_sc[s] + stage * C::STAGE, is_b ? (const void *)p.b_scale : p.a_scale,
              g_sc[s] + g0);
       } else if constexpr (kAiter) {
@@ -775,6 +779,43 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
       vm_wait_barrier();
       if (tail)
         tail_stage();
+      return;
+    }
+    if constexpr (C::KS == 4 && C::NSTAGE == 2 && IN_DT == kMXFP4) {
+      // MXFP4, 64-deep stages in two buffers: stage k (buffer k & 1) is
+      // four 32x32x64 slices.  Steps 0-2 multiply slices 0-2 and read
+      // slices 1-3; the barrier before step 3 waits for stage k+1 and for
+      // every wave's reads of buffer k & 1, so step 3 (slice 3, reading
+      // stage k+1's slice 0) refills that buffer with the first half of
+      // stage k+2's DMA issues and step 0 of stage k+1 with the rest: three
+      // to four steps of cover, against one to two on the 32-deep ring.
+      // Past the end the DMA re-fetches the last stage; the last step's
+      // reads of that copy land in registers no MFMA reads.
+      constexpr int D2 = kDmaPerStage, DH = D2 / 2;
+      auto issue_part = [&](uint32_t buf, int k, int first, int count, int tp) {
+#pragma unroll
+        for (int d = 0; d < count; ++d)
+          if (d * TP / count == tp)
+            issue_one(buf, kt_begin + min(k, nk - 1), first + d);
+      };
+      issue(0, kt_begin);
+#pragma unroll
+      for (int d = 0; d < DH; ++d)
+        issue_one(1, kt_begin + min(1, nk - 1), d);
+      vm_wait_barrier<DH>();  // stage 0 has landed
+      read_frags(f[0], 0, 0);
+      const auto rg = std::integral_constant<int, TP>{};
+      for (int k = 0; k < nk; ++k) {
+        const uint32_t buf = (uint32_t)(k & 1);
+        step(f[0], f[1], true, buf, 1,
+             [&](int tp) { issue_part(buf ^ 1u, k + 1, DH, D2 - DH, tp); }, rg);
+        step(f[1], f[0], true, buf, 2, no_hook, rg);
+        step(f[0], f[1], true, buf, 3, no_hook, rg);
+        vm_wait_barrier<0>();
+        step(f[1], f[0], true, buf ^ 1u, 0, [&](int tp) { issue_part(buf, k + 2, 0, DH, tp); },
+             rg);
+      }
+      vm_wait_barrier();
       return;
     }
     read_frags(f[0], 0, 0);
@@ -1054,12 +1095,16 @@ using CfgFor = std::conditional_t<IN_DT == kMXFP4, Fp4CfgW<W>,
 
 // HYBRID: every tile on the DMA ring (see mainloop), edge tiles stored with
 // bounds checks.
+// DEEP (canonical MXFP4, K a multiple of 256 values): 64-deep stages.
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC, int W = 0,
-          bool PACKED = false, bool HYBRID = false>
+          bool PACKED = false, bool HYBRID = false, bool DEEP = false>
 __device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *smem) {
+  static_assert(!DEEP || IN_DT == kMXFP4, "64-deep MXFP4 stages: canonical layout");
   // Whole tiles run TileCfg's MFMA shape; ragged tiles the 32x32 one.
-  using C = std::conditional_t<MASKED, DefaultCfgW<W>,
-                               std::conditional_t<HYBRID, HybridTileCfgW<W>, CfgFor<IN_DT, W>>>;
+  using C = std::conditional_t<
+      MASKED, DefaultCfgW<W>,
+      std::conditional_t<HYBRID, HybridTileCfgW<W>,
+                         std::conditional_t<DEEP, Fp4Cfg64W<W>, CfgFor<IN_DT, W>>>>;
   static_assert(!HYBRID || (!MASKED && !PACKED), "hybrid: row- or column-major C");
   static_assert(C::SMEM == CfgFor<IN_DT, W>::SMEM && C::THREADS == CfgFor<IN_DT, W>::THREADS,
                 "one LDS size and block size per input type");
@@ -1106,10 +1151,10 @@ __device__ __forceinline__ void tiled_cta(const Params &p, int raw, uint8_t *sme
 }
 
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC, bool PACKED = false,
-          bool HYBRID = false>
+          bool HYBRID = false, bool DEEP = false>
 __global__ __launch_bounds__(CfgFor<IN_DT>::THREADS, 1) void tiled_kernel(Params p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[CfgFor<IN_DT>::SMEM];
-  tiled_cta<IN_DT, OUT_DT, COL_MAJOR, MASKED, VEC, 0, PACKED, HYBRID>(p, blockIdx.x, smem);
+  tiled_cta<IN_DT, OUT_DT, COL_MAJOR, MASKED, VEC, 0, PACKED, HYBRID, DEEP>(p, blockIdx.x, smem);
 }
 
 // ---------------------------------------------------------------- Stream-K

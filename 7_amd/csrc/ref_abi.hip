@@ -208,8 +208,11 @@ extern "C" __global__ __launch_bounds__(AbiFp4Cfg::THREADS, 1) void wmma_f16_mat
   p.c_vec_ok = 1;
   const int tiles = p.tiles_m * p.tiles_n;
   const int ctas = gridDim.x * gridDim.y;
+  // Canonical layout with K a multiple of 256: the 64-deep stages.
+  constexpr bool kDeep = kAbiFp4 == kMXFP4 && K % 256 == 0;
   for (int raw = blockIdx.y * gridDim.x + blockIdx.x; raw < tiles; raw += ctas)
-    tiled_cta<kAbiFp4, WAVE_ABI_OUT, CM, false, 8, WAVE_ABI_THREADS / 64>(p, raw, smem);
+    tiled_cta<kAbiFp4, WAVE_ABI_OUT, CM, false, 8, WAVE_ABI_THREADS / 64, false, false, kDeep>(
+        p, raw, smem);
 }
 #endif
 
