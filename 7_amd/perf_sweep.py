@@ -15,7 +15,7 @@ Each run is one ``7_amd/wave-bench`` process with ``--check``; its
 ``median_per_launch_us:``, ``hw_cycles_wallclock:`` and ``output_check:``
 lines are parsed with the reference's patterns (:659-679).
 
-    python 7_amd/perf_sweep.py --csv gpurun_out/sweep.csv [--kernels f16,fa]
+    python 7_amd/perf_sweep.py --csv sweep.csv [--kernels f16,fa]
         [--m 4096 --n 4096 --k 512,8192] [--input-mode rand-int] [--iters N]
 """
 

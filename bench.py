@@ -331,7 +331,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(see DESIGN.md for how the GEMM and attention would shard)", file=sys.stderr)
+              "(the GEMM and attention would shard by output tiles and by heads, "
+              "one process per GPU)", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -415,8 +416,9 @@ def main():
 
     if args.workload == "all" and not args.no_ref_compare:
         # The same kernels on the input mode / shape of the reference's own
-        # published figures: not the headline
-        # metric, which uses uniform inputs.
+        # published figures (docs/PerfReferences/WaveGfx950F16Gemm4Wave.md:29-31,
+        # docs/PerfReferences/WaveGfx950FlashAttention.md:5-21, MI350X): not the
+        # headline metric, which uses uniform inputs.
         ra = rand_int_operand(M, K, 0, torch).to(dev)
         rb = rand_int_operand(N, K, 1, torch).to(dev)
         r_ms = time_launches(lambda: wave.gemm(ra, rb, out_dtype=torch.float16, out=c),
