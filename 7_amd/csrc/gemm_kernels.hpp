@@ -1041,8 +1041,16 @@ __device__ __forceinline__ void store_tile_lds(const Params &p, int m0, int n0, 
     if ((r >> 4) & 1u)
       v = u32x4{v[2], v[3], v[0], v[1]};
     const size_t q = (size_t)(Q0 + (int)r);
+    // Whole tiles store non-temporally: C is not read again by this launch.
+    // With plain stores one round of tiles leaves its C lines (32 MiB for 256
+    // f16 tiles) dirty in L2, and their write-back slows the next round's K
+    // loop (wave-bench, same box: 8192^3 f16 1479-1482 -> 1510-1514 TFLOP/s,
+    // rand_int inputs 1701 -> 1863-1875, 16384x8192x4096 1403 -> 1447-1451,
+    // MXFP4 4096^2 x 32768 +1-2 %).  The bounds-checked branch (the hybrid
+    // path's ragged tiles) keeps plain stores: config 3b measured 1.3 %
+    // slower with non-temporal ones.
     if constexpr (!MASKED) {
-      *reinterpret_cast<u32x4 *>(out + (q * p.ldc + P0) * 2 + c * 16) = v;
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(out + (q * p.ldc + P0) * 2 + c * 16));
     } else {
       const int pc = P0 + 8 * (int)c;
       if ((int)q < Qext && pc < Pext) {
