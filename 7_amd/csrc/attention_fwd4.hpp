@@ -345,16 +345,31 @@ __device__ __forceinline__ void fwd4_cta(const Params &p, int raw, uint8_t *smem
     const float inv = total > 0.f ? 1.0f / total : 0.f;
     if (p.lse != nullptr && half == 0 && my_q < p.seq_q)
       p.lse[(size_t)bh * p.seq_q + my_q] = (m + __builtin_log2f(total)) * kLn2;
-    if (my_q < p.seq_q) {
-      uint16_t *orow = Oh + (size_t)my_q * kD + 4 * half;
+    // Staged through this wave's own K DMA rows of the two ring tiles (4 KiB
+    // each, row r in tile r / 16; no wave reads K after the last barrier) so
+    // that each store writes 4 whole 256-byte rows, as in fwd_pp_cta.
+    {
+      const uint32_t r = lane & 31;
+      const uint32_t wb = lds0 + wave * 4096;
+      const uint32_t wrow = wb + (r >> 4) * kKBytes + (r & 15) * 256 + half * 8;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const u32x2 w = {pack2<DT>(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv),
                            pack2<DT>(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv)};
-          *reinterpret_cast<u32x2 *>(orow + 32 * dt + 8 * g) = w;
+          const uint32_t c = (uint32_t)(4 * dt + g);
+          lds_store8(wrow + ((c ^ (r & 15)) << 4), w);
         }
+      const uint32_t c = lane & 15;
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const uint32_t rr = it * 4 + (lane >> 4);
+        const u32x4 v =
+            lds_load16(wb + (rr >> 4) * kKBytes + (rr & 15) * 256 + ((c ^ (rr & 15)) << 4));
+        if (qw + (int)rr < p.seq_q)
+          __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(Oh + (size_t)(qw + rr) * kD + 8 * c));
+      }
     }
     // The next pass refills both rings: every wave's reads of this pass are
     // done first.

@@ -134,11 +134,13 @@ __device__ __forceinline__ float dot2_ones(uint32_t pk, float acc) {
                                            __builtin_bit_cast(b2, kOnePair<DT>), acc, false);
 }
 
-// 16-byte LDS load / 4-byte LDS store at a 32-bit LDS byte address.
+// 16-byte LDS load / 4- and 8-byte LDS stores at a 32-bit LDS byte address.
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 typedef __attribute__((address_space(3))) uint32_t lds_u32;
+typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
 __device__ __forceinline__ u32x4 lds_load16(uint32_t a) { return *(lds_u32x4 *)(uintptr_t)a; }
 __device__ __forceinline__ void lds_store4(uint32_t a, uint32_t v) { *(lds_u32 *)(uintptr_t)a = v; }
+__device__ __forceinline__ void lds_store8(uint32_t a, u32x2 v) { *(lds_u32x2 *)(uintptr_t)a = v; }
 // Hide v's value from constant folding, so that base + constant address
 // expressions keep the constant in the instruction's 16-bit offset field.
 __device__ __forceinline__ uint32_t opaque(uint32_t v) {
@@ -494,16 +496,33 @@ __device__ __forceinline__ void fwd_pp_cta(const Params &p, int raw, uint8_t *sm
   // sum_k 2^(c*s_k) = total * 2^m, so ln sum_k e^(scale*s_k) = (m + log2 total) ln 2.
   if (p.lse != nullptr && half == 0 && my_q < p.seq_q)
     p.lse[(size_t)bh * p.seq_q + my_q] = (m + __builtin_log2f(total)) * kLn2;
-  if (my_q < p.seq_q) {
-    uint16_t *orow = Oh + (size_t)my_q * kD + 4 * half;
+  // The wave's 32 rows go through LDS so that each store writes 4 whole
+  // 256-byte rows (1 KiB) instead of 8-byte pieces of 32 rows.  Staging
+  // area: this wave's own K DMA rows of the four ring tiles (2 KiB each,
+  // row r in tile r / 8): after its vmcnt(0) nothing else writes them, and
+  // no wave reads K after its last G.  16-byte chunk c of row r sits at
+  // c ^ (r & 15).
+  {
+    const uint32_t r = lane & 31;
+    const uint32_t wb = lds0 + wave * 2048;
+    const uint32_t wrow = wb + (r >> 3) * kKBytes + (r & 7) * 256 + half * 8;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const u32x2 w = {pack2<DT>(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv),
                          pack2<DT>(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv)};
-        *reinterpret_cast<u32x2 *>(orow + 32 * dt + 8 * g) = w;
+        const uint32_t c = (uint32_t)(4 * dt + g);
+        lds_store8(wrow + ((c ^ (r & 15)) << 4), w);
       }
+    const uint32_t c = lane & 15;
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const uint32_t rr = it * 4 + (lane >> 4);
+      const u32x4 v = lds_load16(wb + (rr >> 3) * kKBytes + (rr & 7) * 256 + ((c ^ (rr & 15)) << 4));
+      if (qw + (int)rr < p.seq_q)
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(Oh + (size_t)(qw + rr) * kD + 8 * c));
+    }
   }
 }
 
