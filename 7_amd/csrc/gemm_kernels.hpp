@@ -310,6 +310,19 @@ __device__ __forceinline__ u32x4 load_chunk(const uint16_t *row, int k, int K) {
   return v;
 }
 
+// The hybrid path's K remainder: K % 4 == 0 and rows 8-byte aligned, so each
+// 8-element chunk (k % 8 == 0) is whole, half (4 elements) or past K.  Both
+// 8-byte halves are loaded from in-bounds addresses (column 0 for a half past
+// K) and zeroed by a select: no branch, so the loads issue back to back
+// under one wait (the branchy load_chunk waited out one round trip per
+// load: config 3b spent 20-25 us on its 4-element tail).
+__device__ __forceinline__ u32x4 load_chunk_k4(const uint16_t *row, int k, int K) {
+  const bool v0 = k + 4 <= K, v1 = k + 8 <= K;
+  const u32x2 lo = *reinterpret_cast<const u32x2 *>(row + (v0 ? k : 0));
+  const u32x2 hi = *reinterpret_cast<const u32x2 *>(row + (v1 ? k + 4 : 0));
+  return u32x4{v0 ? lo.x : 0u, v0 ? lo.y : 0u, v1 ? hi.x : 0u, v1 ? hi.y : 0u};
+}
+
 // Accumulate C-tile (m0, n0) over K steps [kt_begin, kt_end) (in units of
 // C::BK elements) into acc.
 // HYBRID (with !MASKED; one MFMA slice per stage, or the 64-deep two-buffer
@@ -648,9 +661,10 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
           issue_one(stage, kt, d);
     };
     // HYBRID K remainder: stage kt_last copied through VGPRs into ring slot
-    // 0 (zero past K, rows past M / N read as zero), then its MFMA steps (one
-    // per slice).  Runs after the pipeline's final wait + barrier, so no DMA
-    // is in flight and no wave still reads the ring.
+    // 0 (zero past K; rows past M / N clamped to the last valid row, as the
+    // DMA clamps them), then its MFMA steps (one per slice).  Runs after the
+    // pipeline's final wait + barrier, so no DMA is in flight and no wave
+    // still reads the ring.
     auto tail_stage = [&]() {
       if constexpr (HYBRID) {
 #pragma unroll
@@ -658,10 +672,10 @@ __device__ __forceinline__ void mainloop(const Params &p, int m0, int n0,
           const uint32_t R = (wave * C::DMA + i) * 8 + (lane >> 3), ps = lane & 7;
           const int r = (int)Geo<C>::row_of(R, ps);
           const int kc = kt_last * C::BK + (int)(Geo<C>::chunk_of(R, ps) * 8);
-          const uint16_t *ar = m0 + r < p.M ? p.A + (size_t)(m0 + r) * p.K : nullptr;
-          const uint16_t *br = n0 + r < p.N ? p.B + (size_t)(n0 + r) * p.K : nullptr;
-          const u32x4 va = load_chunk<VEC>(ar, kc, p.K);
-          const u32x4 vb = load_chunk<VEC>(br, kc, p.K);
+          const uint16_t *ar = p.A + (size_t)min(m0 + r, p.M - 1) * p.K;
+          const uint16_t *br = p.B + (size_t)min(n0 + r, p.N - 1) * p.K;
+          const u32x4 va = load_chunk_k4(ar, kc, p.K);
+          const u32x4 vb = load_chunk_k4(br, kc, p.K);
           uint8_t *d = smem + (wave * C::DMA + i) * 1024 + lane * 16;
           *reinterpret_cast<u32x4 *>(d) = va;
           *reinterpret_cast<u32x4 *>(d + C::OPB) = vb;
