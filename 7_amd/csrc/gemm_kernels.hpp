@@ -1327,7 +1327,53 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
     auto at = [&](int tp, int tq, int g) {
       return (size_t)((tp * TQ + tq) * C::NG + g) * NT + threadIdx.x;
     };
-    if (parts == 2) {
+    if (parts >= 2) {
+      if (parts > 2) {
+        // More than two contributors: fold all but the last, in worker
+        // order from +0, into the first one's slot (read before it is
+        // overwritten, by the same thread, at the same index; no worker
+        // writes that slot again in this launch).  The pass below then adds
+        // the last one to (+0 + fold), which equals the fold exactly (a sum
+        // begun at +0 is never -0), so the result is the serial
+        // ((0 + p_first) + p_second) + ... bit for bit.  kFold groups of
+        // two contributors are in flight per round trip; accumulating
+        // inside the store callback instead spilled 96-141 VGPRs.
+        constexpr int kGroups = TP * TQ * C::NG, kFold = 8;
+        static_assert(kGroups % kFold == 0, "whole fold batches");
+        f32x4 *dst = reinterpret_cast<f32x4 *>(
+            p.scratch + ((size_t)first_owner * 2 +
+                         sk_slot(total, p.workers, first_owner, tile, iters)) * kTileElems);
+        for (int q0 = 0; q0 < kGroups; q0 += kFold) {
+          f32x4 r[kFold];
+#pragma unroll
+          for (int j = 0; j < kFold; ++j)
+            r[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+          int c = first_owner;
+          for (; c + 1 < last_owner; c += 2) {
+            const f32x4 *x = part_of(c), *y = part_of(c + 1);
+            f32x4 a[kFold], b[kFold];
+#pragma unroll
+            for (int j = 0; j < kFold; ++j) {
+              a[j] = __builtin_nontemporal_load(x + (size_t)(q0 + j) * NT + threadIdx.x);
+              b[j] = __builtin_nontemporal_load(y + (size_t)(q0 + j) * NT + threadIdx.x);
+            }
+#pragma unroll
+            for (int j = 0; j < kFold; ++j) {
+              r[j] += a[j];
+              r[j] += b[j];
+            }
+          }
+          if (c < last_owner) {
+            const f32x4 *x = part_of(c);
+#pragma unroll
+            for (int j = 0; j < kFold; ++j)
+              r[j] += __builtin_nontemporal_load(x + (size_t)(q0 + j) * NT + threadIdx.x);
+          }
+#pragma unroll
+          for (int j = 0; j < kFold; ++j)
+            dst[(size_t)(q0 + j) * NT + threadIdx.x] = r[j];
+        }
+      }
       // The partial groups of kBatch MFMA tiles of a row are loaded from
       // both slots at the first of them, before that batch's stores (which
       // the compiler cannot move loads across), so 2*kBatch*NG = 16 loads
@@ -1336,7 +1382,7 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
       // Stored directly: the LDS-staged epilogue costs VGPR spills here.
       constexpr int kBatch = 8 / C::NG < TP ? 8 / C::NG : TP;
       static_assert(TP % kBatch == 0, "whole batches per row");
-      const f32x4 *pa = part_of(first_owner), *pb = part_of(first_owner + 1);
+      const f32x4 *pa = part_of(first_owner), *pb = part_of(last_owner);
       f32x4 ra[kBatch][C::NG], rb[kBatch][C::NG];
       store_tile<C, OUT_DT, COL_MAJOR, MASKED>(
           p, tm * kTile, tn * kTile, [&](int tp, int tq, int g) {
