@@ -124,10 +124,10 @@ hipError_t launch(const GemmArgs &g, hipStream_t stream) {
   const bool fast = (g.M % kTile == 0) && (g.N % kTile == 0) &&
                     (g.K % stage_k == 0) && aligned_to(g.A, 16) &&
                     aligned_to(g.B, 16) && p.c_vec_ok && !g.force_masked;
-  // Ragged M / N or K off the stage: the hybrid DMA path for the tiled
-  // kernel (rows every 8 bytes at least, so each 16-byte DMA access is
-  // dword-aligned), unless the caller forces the bounds-checked one.
-  const bool hybrid = !g.force_masked && !g.packed && g.workers == 0;
+  // Ragged M / N or K off the stage: the hybrid DMA path (rows every 8
+  // bytes at least, so each 16-byte DMA access is dword-aligned), unless
+  // the caller forces the bounds-checked one or C is tile-packed.
+  const bool hybrid = !g.force_masked && !g.packed;
   int mode = 1;
   if (fast)
     mode = 0;

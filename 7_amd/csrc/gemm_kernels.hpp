@@ -1215,13 +1215,17 @@ __device__ __forceinline__ int sk_slot(int total, int workers, int w, int tile,
 // slot_base/4 + j * THREADS + t, so publishing and reducing are fully
 // coalesced 16-byte accesses and need no coordinate math.
 // Worker `worker` of p.workers.  smem: DefaultCfg::SMEM bytes of
-// 1024-byte-aligned LDS; arrival: one int of LDS.
-template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
+// 1024-byte-aligned LDS; arrival: one int of LDS.  HYBRID (with !MASKED):
+// ragged M / N or K off the stage on the DMA ring, as for the tiled kernel,
+// with bounds-checked stores.
+template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC, bool HYBRID = false>
 __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t *smem,
                                             int *arrival) {
   // Whole-tile ranges run the 16x16 MFMA shape (64-deep stages); ragged
   // tiles the 32x32 one.
   using C = std::conditional_t<MASKED, DefaultCfg, HybridTileCfgW<>>;
+  static_assert(!(HYBRID && MASKED), "hybrid runs the DMA mainloop");
+  constexpr bool SM = MASKED || HYBRID;  // bounds-checked stores
   static_assert(C::SMEM == DefaultCfg::SMEM && C::THREADS == DefaultCfg::THREADS,
                 "one LDS size and block size");
   // XCD-aware worker numbering, as for tiled CTAs: the dispatcher places
@@ -1248,43 +1252,32 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
       for (int j = 0; j < TQ; ++j)
         acc[i][j] = typename C::Acc{};
   };
-  auto whole_tile = [&](int tile) {
-    int tm, tn;
-    tile_coords(tile, p.tiles_m, p.tiles_n, p.group_m, false, tm, tn);
-    zero();
-    mainloop<C, IN_DT, COL_MAJOR, MASKED, VEC>(p, tm * kTile, tn * kTile, 0,
-                                               ksteps, smem, acc);
-    store_out<C, OUT_DT, COL_MAJOR, MASKED>(
-        p, tm * kTile, tn * kTile, smem, [&](int tp, int tq, int g) {
-          return f32x4{acc[tp][tq][4 * g], acc[tp][tq][4 * g + 1],
-                       acc[tp][tq][4 * g + 2], acc[tp][tq][4 * g + 3]};
-        });
+  auto get = [&](int tp, int tq, int g) {
+    return f32x4{acc[tp][tq][4 * g], acc[tp][tq][4 * g + 1], acc[tp][tq][4 * g + 2],
+                 acc[tp][tq][4 * g + 3]};
   };
-
-  if (aligned) {
-    // Every worker owns whole tiles: visit worker, worker + P, ... so the
-    // tiles in flight at any moment are adjacent (no partials, no atomics).
-    for (int tile = worker; tile < tiles; tile += p.workers)
-      whole_tile(tile);
-    return;
-  }
-
-  const int first_tile = iv.begin / iters;
-  const int last_tile = (iv.end - 1) / iters;
+  // Aligned: every worker owns whole tiles and visits worker, worker + P,
+  // ... so the tiles in flight at any moment are adjacent (no partials, no
+  // atomics).  Split: the tiles of the worker's interval, in order.  Both
+  // share one mainloop call site, so its code is inlined once (two copies
+  // of the hybrid ring spilled 79 VGPRs).
+  const int tile_lo = aligned ? worker : iv.begin / iters;
+  const int tile_hi = aligned ? tiles - 1 : (iv.end - 1) / iters;
+  const int tile_step = aligned ? p.workers : 1;
   int slot = 0;
-  for (int tile = first_tile; tile <= last_tile; ++tile) {
-    const int kb = max(iv.begin, tile * iters) - tile * iters;
-    const int ke = min(iv.end, (tile + 1) * iters) - tile * iters;
-    if (kb == 0 && ke == iters) {
-      whole_tile(tile);
-      continue;
-    }
+  for (int tile = tile_lo; tile <= tile_hi; tile += tile_step) {
+    const int kb = aligned ? 0 : max(iv.begin, tile * iters) - tile * iters;
+    const int ke = aligned ? iters : min(iv.end, (tile + 1) * iters) - tile * iters;
     int tm, tn;
     tile_coords(tile, p.tiles_m, p.tiles_n, p.group_m, false, tm, tn);
     zero();
-    mainloop<C, IN_DT, COL_MAJOR, MASKED, VEC>(
+    mainloop<C, IN_DT, COL_MAJOR, MASKED, VEC, HYBRID>(
         p, tm * kTile, tn * kTile, kb * kStepsPerUnit,
         min(ke * kStepsPerUnit, ksteps), smem, acc);
+    if (kb == 0 && ke == iters) {
+      store_out<C, OUT_DT, COL_MAJOR, SM>(p, tm * kTile, tn * kTile, smem, get);
+      continue;
+    }
     // Publish this worker's fp32 partial: 16-byte group g of MFMA tile
     // (tp, tq) of thread t at f32x4 index ((tp*TQ + tq)*NG + g)*NT + t, so
     // every store and load instruction covers 4 KiB contiguously.
@@ -1384,7 +1377,7 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
       static_assert(TP % kBatch == 0, "whole batches per row");
       const f32x4 *pa = part_of(first_owner), *pb = part_of(last_owner);
       f32x4 ra[kBatch][C::NG], rb[kBatch][C::NG];
-      store_tile<C, OUT_DT, COL_MAJOR, MASKED>(
+      store_tile<C, OUT_DT, COL_MAJOR, SM>(
           p, tm * kTile, tn * kTile, [&](int tp, int tq, int g) {
             if (g == 0 && tp % kBatch == 0) {
 #pragma unroll
@@ -1401,7 +1394,7 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
             return s;
           });
     } else {
-      store_tile<C, OUT_DT, COL_MAJOR, MASKED>(
+      store_tile<C, OUT_DT, COL_MAJOR, SM>(
           p, tm * kTile, tn * kTile, [&](int tp, int tq, int g) {
             f32x4 s = {0.f, 0.f, 0.f, 0.f};
             for (int c = first_owner; c <= last_owner; ++c)
@@ -1418,18 +1411,18 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
   }
 }
 
-template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC>
+template <int IN_DT, int OUT_DT, bool COL_MAJOR, bool MASKED, int VEC, bool HYBRID = false>
 __global__ __launch_bounds__(DefaultCfg::THREADS, 1) void streamk_kernel(Params p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[DefaultCfg::SMEM];
   __shared__ int arrival;
-  streamk_cta<IN_DT, OUT_DT, COL_MAJOR, MASKED, VEC>(p, blockIdx.x, smem, &arrival);
+  streamk_cta<IN_DT, OUT_DT, COL_MAJOR, MASKED, VEC, HYBRID>(p, blockIdx.x, smem, &arrival);
 }
 
 // ------------------------------------------------------------- launchers
 // mode: 0 = aligned fast path (LDS DMA), 8/4/1 = masked path with that many
 // elements per global load, kModeHybrid8/4 = hybrid DMA path whose K tail
-// loads 8/4 elements at a time (tiled kernel; Stream-K and tile-packed C
-// run the masked path with the same load width instead).
+// loads 8/4 elements at a time (tile-packed C runs the masked path with the
+// same load width instead).
 constexpr int kModeHybrid8 = 18, kModeHybrid4 = 14;
 template <int IN_DT, int OUT_DT, bool CM, bool SK>
 hipError_t launch_variant(const Params &p, int mode, hipStream_t stream) {
@@ -1459,17 +1452,24 @@ hipError_t launch_variant(const Params &p, int mode, hipStream_t stream) {
       return hipGetLastError();
     }
   }
-  // Hybrid DMA path (tiled kernel only; Stream-K takes the masked one).
-  if constexpr (!SK) {
-    if (mode == kModeHybrid8 || mode == kModeHybrid4) {
+  // Hybrid DMA path.
+  if (mode == kModeHybrid8 || mode == kModeHybrid4) {
+    if constexpr (SK) {
+      if (mode == kModeHybrid8)
+        hipLaunchKernelGGL((streamk_kernel<IN_DT, OUT_DT, CM, false, 8, true>), grid, block, 0,
+                           stream, p);
+      else
+        hipLaunchKernelGGL((streamk_kernel<IN_DT, OUT_DT, CM, false, 4, true>), grid, block, 0,
+                           stream, p);
+    } else {
       if (mode == kModeHybrid8)
         hipLaunchKernelGGL((tiled_kernel<IN_DT, OUT_DT, CM, false, 8, false, true>), grid, block,
                            0, stream, p);
       else
         hipLaunchKernelGGL((tiled_kernel<IN_DT, OUT_DT, CM, false, 4, false, true>), grid, block,
                            0, stream, p);
-      return hipGetLastError();
     }
+    return hipGetLastError();
   }
   switch (mode) {
   case 0: WAVE_LAUNCH(false, 8); break;
