@@ -186,7 +186,20 @@ int auto_workers(int M, int N, int K, int cus) {
   // workers than CUs from K = 4096 (2048^2 x 4096: 423 against 507).
   if (tiles * 2 >= cus && K < 8192)
     return 0;
-  const int64_t w = tiles * 2 < cus ? tiles * 2 : cus;
+  int64_t w = tiles * 2 < cus ? tiles * 2 : cus;
+  // Fewer than CUs / 2 tiles: one worker per 2048 of K a tile, at least
+  // two a tile, at most CUs / 2 (bf16, one box, microseconds at 2 * tiles
+  // against this: 1024^2 x 16384 150 -> 101, 1024^2 x 32768 272 -> 136,
+  // 2048 x 1024 x 16384 153 -> 125; over nine shapes with 16 to 64 tiles
+  // at most 5 % off the best of 32 to 256 workers: 2048^2 x 16384 166
+  // against 158 at 256).
+  if (tiles * 4 <= cus) {
+    const int64_t by_k = tiles * (K / 2048);
+    const int64_t cap = cus / 2;
+    const int64_t want = by_k < cap ? by_k : cap;
+    if (want > w)
+      w = want;
+  }
   const int64_t work = tiles * wave::gemm::k_iterations(K);
   return (int)(w < work ? w : work);
 }

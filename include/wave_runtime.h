@@ -142,7 +142,8 @@ int wave_gemm_streamk_counters_check(const uint32_t *counters, int M, int N,
  * for the caller: the tiled kernel (or the short-M kernel for M <= 128), or
  * Stream-K with min(2 * tiles, CUs) workers when the 256x256 output tiles
  * alone would leave CUs idle (fewer tiles than CUs) and K >= 4096 (K >= 8192
- * once 2 * tiles reaches the CU count).  Stream-K
+ * once 2 * tiles reaches the CU count); with at most CUs / 4 tiles,
+ * max(2 * tiles, min(tiles * (K / 2048), CUs / 2)) workers.  Stream-K
  * takes its workspace from `workspace` (caller-owned device memory of
  * wave_gemm_auto_workspace_bytes(M, N, K) bytes, 0 when the shape takes
  * the tiled path; no initialisation needed, each launch zeroes the counters
