@@ -1367,32 +1367,65 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
             dst[(size_t)(q0 + j) * NT + threadIdx.x] = r[j];
         }
       }
-      // The partial groups of kBatch MFMA tiles of a row are loaded from
-      // both slots at the first of them, before that batch's stores (which
-      // the compiler cannot move loads across), so 2*kBatch*NG = 16 loads
-      // are in flight at once.  A contributor loop inside the callback
-      // waited out one memory round trip per group: ~140 us a tile.
-      // Stored directly: the LDS-staged epilogue costs VGPR spills here.
+      // s = (0 + X) + Y with X the first slot (p_first, or the fold) and Y
+      // the last contributor's partial.  The last arriver still holds its
+      // own partial in its accumulators, so one of the two comes from
+      // registers when it is the first contributor of two (X) or the last
+      // one (Y); only a middle contributor of three or more reads both
+      // slots.  (Reading the accumulators after the MFMAs: the publish's
+      // reads of them above already covered the asm MFMA hazard.)
+      // A batch of partial groups (KB MFMA tiles of a row, over TB rows) is
+      // loaded at the first of them, before that batch's stores (which the
+      // compiler cannot move loads across), so 16 loads are in flight at
+      // once: kBatch tiles from both slots, or twice as many from one.  A
+      // contributor loop inside the callback waited out one memory round
+      // trip per group: ~140 us a tile.  Stored directly: the LDS-staged
+      // epilogue costs VGPR spills here.
       constexpr int kBatch = 8 / C::NG < TP ? 8 / C::NG : TP;
       static_assert(TP % kBatch == 0, "whole batches per row");
       const f32x4 *pa = part_of(first_owner), *pb = part_of(last_owner);
-      f32x4 ra[kBatch][C::NG], rb[kBatch][C::NG];
-      store_tile<C, OUT_DT, COL_MAJOR, SM>(
-          p, tm * kTile, tn * kTile, [&](int tp, int tq, int g) {
-            if (g == 0 && tp % kBatch == 0) {
+      auto reduce = [&](auto role) {
+        // R: 0 both slots, 1 X from registers, 2 Y from registers.
+        constexpr int R = decltype(role)::value;
+        constexpr int KB = R == 0 ? kBatch : (2 * kBatch <= TP ? 2 * kBatch : TP);
+        constexpr int TB = (R != 0 && KB == kBatch) ? 2 : 1;  // then KB == TP
+        static_assert(TP % KB == 0 && TQ % TB == 0 && (TB == 1 || KB == TP), "batches");
+        f32x4 rx[TB][KB][C::NG], ry[TB][KB][C::NG];
+        store_tile<C, OUT_DT, COL_MAJOR, SM>(
+            p, tm * kTile, tn * kTile, [&](int tp, int tq, int g) {
+              if (g == 0 && tp % KB == 0 && tq % TB == 0) {
 #pragma unroll
-              for (int j = 0; j < kBatch; ++j)
+                for (int u = 0; u < TB; ++u)
 #pragma unroll
-                for (int h = 0; h < C::NG; ++h) {
-                  ra[j][h] = __builtin_nontemporal_load(pa + at(tp + j, tq, h));
-                  rb[j][h] = __builtin_nontemporal_load(pb + at(tp + j, tq, h));
-                }
-            }
-            f32x4 s = {0.f, 0.f, 0.f, 0.f};
-            s += ra[tp % kBatch][g];
-            s += rb[tp % kBatch][g];
-            return s;
-          });
+                  for (int j = 0; j < KB; ++j)
+#pragma unroll
+                    for (int h = 0; h < C::NG; ++h) {
+                      if constexpr (R != 1)
+                        rx[u][j][h] = __builtin_nontemporal_load(pa + at(tp + j, tq + u, h));
+                      if constexpr (R != 2)
+                        ry[u][j][h] = __builtin_nontemporal_load(pb + at(tp + j, tq + u, h));
+                    }
+              }
+              f32x4 s = {0.f, 0.f, 0.f, 0.f};
+              if constexpr (R == 1)
+                s += get(tp, tq, g);
+              else
+                s += rx[tq % TB][tp % KB][g];
+              if constexpr (R == 2)
+                s += get(tp, tq, g);
+              else
+                s += ry[tq % TB][tp % KB][g];
+              return s;
+            });
+      };
+      // (The VGPR-staged 32x32 path keeps reading both slots: three
+      // variants there spill 211 VGPRs.)
+      if (!MASKED && worker == last_owner)
+        reduce(std::integral_constant<int, MASKED ? 0 : 2>{});
+      else if (!MASKED && parts == 2)
+        reduce(std::integral_constant<int, MASKED ? 0 : 1>{});
+      else
+        reduce(std::integral_constant<int, 0>{});
     } else {
       store_tile<C, OUT_DT, COL_MAJOR, SM>(
           p, tm * kTile, tn * kTile, [&](int tp, int tq, int g) {
