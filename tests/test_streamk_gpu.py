@@ -112,6 +112,9 @@ def test_config3_streamk_bf16(wave, oracle, dev):
 # ---- shape-driven dispatch (wave_gemm_auto_launch) ------------------------------
 @pytest.mark.parametrize("shape,streamk", [((2048, 512, 8192), True),   # 16 tiles, long K
                                            ((1000, 300, 4100), True),   # ragged, 8 tiles
+                                           # ragged, K off the stage, 16 tiles:
+                                           # 128 workers, 8-9 contributors a tile
+                                           ((1000, 1000, 16400), True),
                                            ((4096, 4096, 512), False),  # 256 tiles
                                            ((4096, 2048, 4096), False),  # 128 tiles, K 4096
                                            ((128, 1024, 8192), False)])  # short-M kernel
@@ -133,3 +136,32 @@ def test_auto_dispatch_matches_tiled(wave, oracle, dev, shape, streamk):
         assert torch.equal(got, ref)
     small = torch.empty((max(need // 2, 1),), dtype=torch.uint8, device=dev)
     assert torch.equal(wave.gemm_auto(A, B, out_dtype=torch.bfloat16, workspace=small), ref)
+
+
+@pytest.mark.parametrize("shape,workers", [((1024, 1024, 8192), 64),    # 4 contributors
+                                           ((1000, 1000, 8200), 128),   # ragged, 8-9
+                                           ((512, 512, 4096), 12),      # 5-6
+                                           ((2048, 2048, 8192), 128)])  # 2
+def test_float_inputs_same_bits_every_launch(wave, dev, shape, workers):
+    """Inexact (normal-distributed) inputs with fp32 C: the reduction sums
+    the contributors in worker order whichever of them arrives last (and
+    takes its own partial from registers or from its slot), so every launch
+    gives the same bits; the result is an fp32-accumulated product of the
+    bf16 inputs (float64 check on a row sample)."""
+    M, N, K = shape
+    g = torch.Generator(device="cpu").manual_seed(17)
+    a = torch.randn((M, K), generator=g).to(torch.bfloat16)
+    b = torch.randn((N, K), generator=g).to(torch.bfloat16)
+    A, B = a.to(dev), b.to(dev)
+    ws = wave.StreamKWorkspace(M, N, workers, dev)
+    first = wave.gemm_streamk(A, B, workers, out_dtype=torch.float32, workspace=ws)
+    out = torch.empty_like(first)
+    for _ in range(20):
+        wave.gemm_streamk(A, B, workers, out_dtype=torch.float32, workspace=ws, out=out)
+        torch.cuda.synchronize()
+        assert torch.equal(out, first)
+    assert ws.nonzero_counters() == 0
+    rows = torch.arange(0, M, 97)
+    ref = a[rows].double() @ b.double().t()
+    err = (first[rows].cpu().double() - ref).abs().max().item()
+    assert err <= 1e-5 * K ** 0.5 * 4, err
