@@ -180,11 +180,18 @@ int auto_workers(int M, int N, int K, int cus) {
   const int64_t tiles = (int64_t)wave::gemm::tiles_for(M) * wave::gemm::tiles_for(N);
   if (M <= 128 || K < 4096 || tiles >= cus)
     return 0;
-  // With 2 * tiles >= CUs every CU runs a worker; the split then pays off
+  // With 2 * tiles = CUs every CU runs a worker; the split then pays off
   // from K = 8192 (measured, bf16: 4096x2048x4096 tiled 750 against
   // Stream-K 720 TFLOP/s, 8192x1024x8192 826 against 932); with fewer
   // workers than CUs from K = 4096 (2048^2 x 4096: 423 against 507).
   if (tiles * 2 >= cus && K < 8192)
+    return 0;
+  // Between CUs / 2 and CUs tiles the split leaves workers with uneven,
+  // tile-straddling shares, which measured slower than one round of whole
+  // tiles (bf16, microseconds, tiled against 256 workers: 3072^2 x 8192
+  // 153 / 227, 4096 x 3072 x 8192 166 / 198); exactly CUs / 2 tiles split
+  // into even halves (4096 x 2048 x 8192 148 / 130).
+  if (tiles * 2 > cus)
     return 0;
   int64_t w = tiles * 2 < cus ? tiles * 2 : cus;
   // Fewer than CUs / 2 tiles: one worker per 2048 of K a tile, at least

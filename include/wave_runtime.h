@@ -140,9 +140,9 @@ int wave_gemm_streamk_counters_check(const uint32_t *counters, int M, int N,
  * tiled or Stream-K kernel per run (tools/wave-matmul-calibrate/
  * wave-matmul-perf-sweep.py:151-326 kernel matrix).  This entry point picks
  * for the caller: the tiled kernel (or the short-M kernel for M <= 128), or
- * Stream-K with min(2 * tiles, CUs) workers when the 256x256 output tiles
- * alone would leave CUs idle (fewer tiles than CUs) and K >= 4096 (K >= 8192
- * once 2 * tiles reaches the CU count); with at most CUs / 4 tiles,
+ * Stream-K with 2 * tiles workers when the 256x256 output tiles would leave
+ * at least half the CUs idle (tiles <= CUs / 2) and K >= 4096 (K >= 8192
+ * at exactly CUs / 2 tiles); with at most CUs / 4 tiles,
  * max(2 * tiles, min(tiles * (K / 2048), CUs / 2)) workers.  Stream-K
  * takes its workspace from `workspace` (caller-owned device memory of
  * wave_gemm_auto_workspace_bytes(M, N, K) bytes, 0 when the shape takes

@@ -116,6 +116,7 @@ def test_config3_streamk_bf16(wave, oracle, dev):
                                            # 128 workers, 8-9 contributors a tile
                                            ((1000, 1000, 16400), True),
                                            ((4096, 4096, 512), False),  # 256 tiles
+                                           ((3072, 3072, 8192), False),  # 144 tiles: uneven split
                                            ((4096, 2048, 4096), False),  # 128 tiles, K 4096
                                            ((128, 1024, 8192), False)])  # short-M kernel
 def test_auto_dispatch_matches_tiled(wave, oracle, dev, shape, streamk):
