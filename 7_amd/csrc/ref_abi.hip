@@ -66,12 +66,23 @@
 // without writing anything; so does a GEMM launch whose A/B (16 bytes) or C
 // (4 elements) lack the alignment its load path needs (hipMalloc'd buffers
 // always have it).  A larger block the runtime refuses (launch bounds).
+#include "../../include/wave_kernel_abi.h"
 #include "attention_fwd4.hpp"
 #include "attention_kernels.hpp"
 #include "fa_small.hpp"
 #include "gemm_kernels.hpp"
 
 using namespace wave;
+
+// The published launch contract (include/wave_kernel_abi.h) is the LDS these
+// kernels declare: the GEMM rings are static, the FA kernels check their
+// dynamic LDS against these sizes.
+static_assert(wave::gemm::TileCfg::SMEM == WAVE_ABI_MATMUL_STATIC_LDS, "GEMM ring");
+static_assert(wave::gemm::Fp4Cfg::SMEM == WAVE_ABI_MXFP4_STATIC_LDS, "MXFP4 ring");
+static_assert(wave::gemm::Fp4ACfg::SMEM == WAVE_ABI_MXFP4_AITER_STATIC_LDS, "AITER ring");
+static_assert(wave::gemm::DefaultCfg::SMEM + 4 == WAVE_ABI_STREAMK_STATIC_LDS, "Stream-K ring");
+static_assert(wave::attention::kPPSmem == WAVE_ABI_FA_MIN_DYNAMIC_LDS, "8-wave FA LDS");
+static_assert(wave::attention::kF4Smem == WAVE_ABI_FA4_MIN_DYNAMIC_LDS, "4-wave FA LDS");
 
 namespace {
 [[maybe_unused]] __device__ __forceinline__ bool aligned16(const void *p) {

@@ -270,10 +270,9 @@ def test_code_objects_export_reference_symbols():
         assert end == explicit, (name, end)
 
 
-def test_kernel_abi_header_matches_code_objects(tmp_path):
-    """include/wave_kernel_abi.h's argument blocks end where the code
-    objects' explicit kernel arguments end (the kernarg layout the runners
-    fill through hipModuleLaunchKernel)."""
+def _header_macros(tmp_path):
+    """The values include/wave_kernel_abi.h states, printed by a C program
+    compiled against it: argument-block ends, symbols, blocks and LDS."""
     import os
     import shutil
     import subprocess
@@ -286,16 +285,94 @@ def test_kernel_abi_header_matches_code_objects(tmp_path):
         '#include <stddef.h>\n#include <stdio.h>\n#include "wave_kernel_abi.h"\n'
         "#define END(T, f) (unsigned)(offsetof(T, f) + sizeof(((T *)0)->f))\n"
         "int main(void) {\n"
-        '  printf("matmul %s %u\\n", WAVE_ABI_MATMUL_SYMBOL, END(wave_abi_matmul_args, trip));\n'
-        '  printf("mxfp4 %s %u\\n", WAVE_ABI_MXFP4_SYMBOL, END(wave_abi_mxfp4_args, trip));\n'
-        '  printf("streamk %s %u\\n", WAVE_ABI_STREAMK_SYMBOL, END(wave_abi_streamk_args, workers));\n'
-        '  printf("fa %s %u\\n", WAVE_ABI_FA_SYMBOL, END(wave_abi_fa_args, O));\n'
-        '  printf("fa32 %s %u\\n", WAVE_ABI_FA32_SYMBOL, END(wave_abi_fa32_args, O));\n'
+        '  printf("end matmul %s %u\\n", WAVE_ABI_MATMUL_SYMBOL, END(wave_abi_matmul_args, trip));\n'
+        '  printf("end mxfp4 %s %u\\n", WAVE_ABI_MXFP4_SYMBOL, END(wave_abi_mxfp4_args, trip));\n'
+        '  printf("end streamk %s %u\\n", WAVE_ABI_STREAMK_SYMBOL, END(wave_abi_streamk_args, workers));\n'
+        '  printf("end fa %s %u\\n", WAVE_ABI_FA_SYMBOL, END(wave_abi_fa_args, O));\n'
+        '  printf("end fa32 %s %u\\n", WAVE_ABI_FA32_SYMBOL, END(wave_abi_fa32_args, O));\n'
+        '  printf("val LDS_LIMIT %d\\n", WAVE_ABI_LDS_LIMIT);\n'
+        '  printf("val MATMUL_BLOCK %d\\n", WAVE_ABI_MATMUL_BLOCK);\n'
+        '  printf("val MATMUL_STATIC_LDS %d\\n", WAVE_ABI_MATMUL_STATIC_LDS);\n'
+        '  printf("val MATMUL_DYNAMIC_LDS %d\\n", WAVE_ABI_MATMUL_DYNAMIC_LDS);\n'
+        '  printf("val MXFP4_BLOCK %d\\n", WAVE_ABI_MXFP4_BLOCK);\n'
+        '  printf("val MXFP4_STATIC_LDS %d\\n", WAVE_ABI_MXFP4_STATIC_LDS);\n'
+        '  printf("val MXFP4_AITER_STATIC_LDS %d\\n", WAVE_ABI_MXFP4_AITER_STATIC_LDS);\n'
+        '  printf("val MXFP4_DYNAMIC_LDS %d\\n", WAVE_ABI_MXFP4_DYNAMIC_LDS);\n'
+        '  printf("val STREAMK_BLOCK %d\\n", WAVE_ABI_STREAMK_BLOCK);\n'
+        '  printf("val STREAMK_STATIC_LDS %d\\n", WAVE_ABI_STREAMK_STATIC_LDS);\n'
+        '  printf("val STREAMK_DYNAMIC_LDS %d\\n", WAVE_ABI_STREAMK_DYNAMIC_LDS);\n'
+        '  printf("val FA_BLOCK %d\\n", WAVE_ABI_FA_BLOCK);\n'
+        '  printf("val FA_STATIC_LDS %d\\n", WAVE_ABI_FA_STATIC_LDS);\n'
+        '  printf("val FA_MIN_DYNAMIC_LDS %d\\n", WAVE_ABI_FA_MIN_DYNAMIC_LDS);\n'
+        '  printf("val FA4_BLOCK %d\\n", WAVE_ABI_FA4_BLOCK);\n'
+        '  printf("val FA4_MIN_DYNAMIC_LDS %d\\n", WAVE_ABI_FA4_MIN_DYNAMIC_LDS);\n'
+        '  printf("val FA32_MAX_BLOCK %d\\n", WAVE_ABI_FA32_MAX_BLOCK);\n'
+        '  printf("val FA32_STATIC_LDS_256 %d\\n", WAVE_ABI_FA32_STATIC_LDS(256));\n'
         "  return 0;\n}\n")
     exe = tmp_path / "abi"
     subprocess.run([gcc, "-std=c99", "-Wall", "-Werror", "-I", os.path.join(root, "include"),
                     str(src), "-o", str(exe)], check=True)
-    rows = [line.split() for line in subprocess.run(
-        [str(exe)], capture_output=True, text=True, check=True).stdout.splitlines()]
-    got = {block: (sym, int(end)) for block, sym, end in rows}
-    assert got == {block: (sym, end) for sym, end, block in ABI_SYMBOLS.values()}
+    ends, vals = {}, {}
+    for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                               check=True).stdout.splitlines():
+        f = line.split()
+        if f[0] == "end":
+            ends[f[1]] = (f[2], int(f[3]))
+        else:
+            vals[f[1]] = int(f[2])
+    return ends, vals
+
+
+def test_kernel_abi_header_matches_code_objects(tmp_path):
+    """include/wave_kernel_abi.h states what the code objects implement:
+    * its argument blocks end where the objects' explicit kernel arguments
+      end (the kernarg layout the runners fill through hipModuleLaunchKernel);
+    * each object's static LDS (.group_segment_fixed_size) and block
+      (.max_flat_workgroup_size) are the header's *_STATIC_LDS and *_BLOCK
+      for its family (a WAVE_ABI_THREADS build: the _b<threads> suffix);
+    * the GEMM-family objects leave no room for the round-1 contract's 128
+      KiB of dynamic LDS: static LDS + the stated dynamic LDS fits the CU,
+      static + 128 KiB does not (so a caller must pass 0, as the reference's
+      launchers do, wave-matmul-calibrate.py:901-902)."""
+    import glob
+    import os
+    import re
+    import shutil
+    import subprocess
+    ends, v = _header_macros(tmp_path)
+    assert ends == {block: (sym, end) for sym, end, block in ABI_SYMBOLS.values()}
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    objs = sorted(glob.glob(os.path.join(root, "7_amd", "hsaco", "*.hsaco")))
+    assert objs, "code objects are built by make -C 7_amd/csrc (hsacos)"
+    readelf = shutil.which("llvm-readelf") or "/opt/rocm/llvm/bin/llvm-readelf"
+    if not os.path.exists(readelf):
+        pytest.skip("llvm-readelf not available")
+    # family prefix -> (static LDS, default block, dynamic LDS the launch passes)
+    family = {
+        "gemm_": (v["MATMUL_STATIC_LDS"], v["MATMUL_BLOCK"], v["MATMUL_DYNAMIC_LDS"]),
+        "mxfp4a_": (v["MXFP4_AITER_STATIC_LDS"], v["MXFP4_BLOCK"], v["MXFP4_DYNAMIC_LDS"]),
+        "mxfp4_": (v["MXFP4_STATIC_LDS"], v["MXFP4_BLOCK"], v["MXFP4_DYNAMIC_LDS"]),
+        "streamk_": (v["STREAMK_STATIC_LDS"], v["STREAMK_BLOCK"], v["STREAMK_DYNAMIC_LDS"]),
+        "fa4_bf16_": (v["FA_STATIC_LDS"], v["FA4_BLOCK"], v["FA4_MIN_DYNAMIC_LDS"]),
+        "fa_bf16_": (v["FA_STATIC_LDS"], v["FA_BLOCK"], v["FA_MIN_DYNAMIC_LDS"]),
+        "fa32_m16_n256_": (v["FA32_STATIC_LDS_256"], v["FA32_MAX_BLOCK"], 0),
+    }
+    seen = set()
+    for path in objs:
+        name = os.path.basename(path)[:-len(".hsaco")]
+        prefix = next(k for k in family if name.startswith(k))
+        static, block, dynamic = family[prefix]
+        m = re.search(r"_b(\d+)$", name)
+        if m:
+            block = int(m.group(1))
+        notes = subprocess.run([readelf, "--notes", path], capture_output=True, text=True,
+                               check=True).stdout
+        lds = int(notes.split(".group_segment_fixed_size:")[1].split()[0])
+        flat = int(notes.split(".max_flat_workgroup_size:")[1].split()[0])
+        assert lds == static, (name, lds, static)
+        assert flat == block, (name, flat, block)
+        assert lds + dynamic <= v["LDS_LIMIT"], name
+        if not prefix.startswith("fa"):
+            assert lds + 131072 > v["LDS_LIMIT"], name
+        seen.add(prefix)
+    assert seen == set(family), seen
