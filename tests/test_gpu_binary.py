@@ -70,6 +70,67 @@ def test_attach_rewrites_stub_or_appends(gb):
         gb.attach("func.func @f() { return }", data)
 
 
+# A host module with the shape of the reference's mlir-runner flow
+# (wave_matmul.py:11496-11514: the memref externals, `gpu.module @kernels`
+# holding the kernel, then the host main whose gpu.launch_func names
+# @kernels::@wmma_f16_matmul_tiled), written here by hand: nested regions,
+# a kernel attribute dictionary, strings holding braces and `->` types.
+HOST_MODULE = """module attributes {gpu.container_module} {
+  func.func private @_mlir_ciface_wave_memref_to_ptr_global_f16(memref<?xf16>) -> !llvm.ptr
+  gpu.module @kernels [#rocdl.target<chip = "gfx950">] attributes {wave.note = "{not a brace}"} {
+    gpu.func @wmma_f16_matmul_tiled(%a: !llvm.ptr, %b: !llvm.ptr, %c: !llvm.ptr, %trip: i32)
+        kernel attributes {gpu.known_block_size = array<i32: 256, 1, 1>} {
+      %c0 = arith.constant 0 : index
+      %c1 = arith.constant 1 : index
+      scf.for %i = %c0 to %c1 step %c1 {
+        %m = affine.apply affine_map<(d0) -> (d0 * 2)>(%i)
+        // a comment with a } brace
+      }
+      gpu.return
+    }
+  }
+  func.func @main() {
+    %c1 = arith.constant 1 : index
+    %c256 = arith.constant 256 : index
+    gpu.launch_func @kernels::@wmma_f16_matmul_tiled blocks in (%c1, %c1, %c1) threads in (%c256, %c1, %c1)
+    return
+  }
+}
+"""
+
+
+def test_attach_replaces_the_kernels_module(gb):
+    """The compile pass's replace-and-erase (WaveCompileKernels.cpp:117-123):
+    the gpu.module @kernels goes, a gpu.binary @kernels takes its place,
+    and everything else, the launch included, is unchanged."""
+    data = open(CONFIG1, "rb").read()
+    out = gb.attach(HOST_MODULE, data)
+    assert "gpu.module" not in out and "gpu.func" not in out
+    assert len(re.findall(r"@kernels\b(?!::)", out)) == 1
+    assert out.count("gpu.binary @kernels") == 1
+    start = HOST_MODULE.index("  gpu.module")
+    end = HOST_MODULE.index("  func.func @main")
+    assert out.startswith(HOST_MODULE[:start] + "  gpu.binary @kernels [")
+    assert out.endswith("]\n" + HOST_MODULE[end:])
+    assert "gpu.launch_func @kernels::@wmma_f16_matmul_tiled blocks in" in out
+    m = re.search(r'bin = "(.*?)">\]', out, flags=re.S)
+    assert unescape(m.group(1)) == data
+
+
+def test_attach_rejects_a_duplicate_symbol_and_unbalanced_modules(gb):
+    both = HOST_MODULE.replace("  func.func @main", '  gpu.binary @kernels [#gpu.object<'
+                               '#rocdl.target<chip = "gfx950">, bin = "">]\n  func.func @main')
+    with pytest.raises(ValueError):
+        gb.attach(both, b"\x7fELF")
+    cut = HOST_MODULE[:HOST_MODULE.index("      gpu.return")]
+    with pytest.raises(ValueError):
+        gb.attach(cut, b"\x7fELF")
+    # Another module name is left alone (the symbol is matched whole).
+    other = HOST_MODULE.replace("gpu.module @kernels", "gpu.module @kernels_v2")
+    out = gb.attach(other, b"\x7fELF")
+    assert "gpu.module @kernels_v2" in out and out.count("gpu.binary @kernels [") == 1
+
+
 def test_cli_prints_op(gb, capsys):
     assert gb.main([CONFIG1]) == 0
     assert capsys.readouterr().out.startswith("gpu.binary @kernels [#gpu.object<")
