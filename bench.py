@@ -10,7 +10,7 @@ peak.  Beside it: the flash-attention forward of configs[3] (B4 H32 S4096
 D128 f16, non-causal; FLOPs 4*B*H*S^2*D as the reference counts them,
 wave-fa-gfx950-runner.cpp:465-467) and the CPU baseline -- the oracle's
 multithreaded C++ GEMM timed on a bounded sample of output rows of the same
-workload on this host's cores.
+workload (the whole problem when it fits the CPU budget) on this host's cores.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-fa]
                     [--no-ref-compare]
@@ -112,31 +112,50 @@ CPU_THREADS_CAP = 16
 
 
 def cpu_baseline(a_bits, b_bits, M, N, K, budget_s):
-    """Oracle GEMM (C++, fp32 accumulate) on a bounded sample of rows of the
-    same 8192^3 problem, on all allowed host threads; the median of three
-    timed runs of about budget_s / 3 seconds each."""
+    """Oracle GEMM (C++, fp32 accumulate, the reference's float arithmetic)
+    on this host's allowed threads: the whole M x N x K problem when three
+    runs of it fit in budget_s, else a sample of whole 32-row blocks (one
+    block per thread and more) of the same problem.  A run = widening and
+    transposing B once (oracle gemm_prepare_bt) + the rows; for a sample the
+    preparation is charged per row (its time x rows / M), as it is shared by
+    all M rows of the whole problem.  Median of three runs."""
     from oracle import oracle
     threads = max(1, min(len(os.sched_getaffinity(0)), CPU_THREADS_CAP))
-    rows, dt = 8, 0.0
-    while True:  # grow the sample until one run takes >= 0.5 s, then scale
-        t0 = time.perf_counter()
-        oracle.gemm_nt_rows(a_bits, b_bits, 0, rows, oracle.F16, threads=threads)
-        dt = time.perf_counter() - t0
-        if dt >= 0.5 or rows >= M:
-            break
-        rows = min(M, rows * 4)
-    rows = int(max(1, min(M, rows * (budget_s / 3) / dt)))
+    t0 = time.perf_counter()
+    bt = oracle.gemm_prepare_bt(b_bits, oracle.F16, threads=threads)
+    t_prep = time.perf_counter() - t0
+    unit = 32 * threads  # one 32-row block per thread
+    out = np.zeros((M, N), dtype=np.float32)  # touched once, reused by every run
+    t0 = time.perf_counter()
+    oracle.gemm_nt_rows_bt(a_bits, bt, 0, unit, oracle.F16, threads=threads, out=out[:unit])
+    per_row = (time.perf_counter() - t0) / unit
+    whole = t_prep + per_row * M
     runs = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        oracle.gemm_nt_rows(a_bits, b_bits, 0, rows, oracle.F16, threads=threads)
-        runs.append(time.perf_counter() - t0)
+    if 3 * whole <= budget_s:
+        rows = M
+        for _ in range(3):
+            t0 = time.perf_counter()
+            bt = oracle.gemm_prepare_bt(b_bits, oracle.F16, threads=threads)
+            oracle.gemm_nt_rows_bt(a_bits, bt, 0, M, oracle.F16, threads=threads, out=out)
+            runs.append(time.perf_counter() - t0)
+        sample = f"the whole {M}x{N}x{K} f16 GEMM (B prepared inside each run)"
+    else:
+        rows = int((budget_s / 3 - t_prep) / per_row) // unit * unit
+        rows = max(unit, min(M, rows))
+        for _ in range(3):
+            t0 = time.perf_counter()
+            oracle.gemm_nt_rows_bt(a_bits, bt, 0, rows, oracle.F16, threads=threads,
+                                   out=out[:rows])
+            runs.append(time.perf_counter() - t0 + t_prep * rows / M)
+        sample = (f"rows 0..{rows - 1} of C (={rows}x{N}x{K}) of the {M}x{N}x{K} f16 GEMM, "
+                  f"B preparation ({t_prep:.2f} s) charged per row")
     dt = sorted(runs)[1]
+    del out, bt
     return {"value": round(2.0 * rows * N * K / dt / 1e12, 6), "unit": "TFLOP/s",
             "cores": threads, "kind": "port",
-            "sample": f"rows 0..{rows - 1} of C (={rows}x{N}x{K}) of the 8192^3 f16 GEMM, "
-                      f"median of 3 runs ({', '.join(f'{r:.1f}' for r in runs)} s), "
-                      f"oracle/oracle.cpp gemm_nt_rows",
+            "sample": f"{sample}, median of 3 runs ({', '.join(f'{r:.2f}' for r in runs)} s), "
+                      f"oracle/oracle.cpp gemm_prepare_bt + gemm_nt_rows_bt; probe-estimated "
+                      f"whole problem {whole:.1f} s",
             "host": host_cpu()}
 
 
@@ -321,7 +340,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fa", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--cpu-budget", type=float, default=24.0)
     ap.add_argument("--no-ref-compare", action="store_true",
                     help="skip the runs on the reference's published input modes / shapes")
     ap.add_argument("--workload", choices=["all", "gemm", "fa", "mxfp4", "copy", "configs"],

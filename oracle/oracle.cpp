@@ -299,13 +299,44 @@ float oracle_gemm_element(const uint16_t *a, const uint16_t *b, int k,
 
 namespace {
 
+// 8 floats in one AVX register (GCC vector extension); element-wise
+// arithmetic, so each lane is its own C element.
+typedef float f8 __attribute__((vector_size(32)));
+
+// acc[r][0..15] += a[r][i] * bt[i][0..15] for i in [kb, ke), 4 rows x 16
+// columns held in registers: every element is the same float multiply then
+// add, in ascending i, as the scalar loop (this file is built with
+// -ffp-contract=off, so nothing is fused).
+inline void microKernel4x16(const float *const a[4], const float *bt, size_t ldb, int kb,
+                            int ke, float *acc, int ldacc) {
+  f8 c[4][2];
+  for (int r = 0; r < 4; ++r)
+    for (int h = 0; h < 2; ++h)
+      std::memcpy(&c[r][h], acc + r * ldacc + 8 * h, sizeof(f8));
+  for (int i = kb; i < ke; ++i) {
+    f8 b0, b1;
+    std::memcpy(&b0, bt + i * ldb, sizeof(f8));
+    std::memcpy(&b1, bt + i * ldb + 8, sizeof(f8));
+    for (int r = 0; r < 4; ++r) {
+      const float av = a[r][i];
+      c[r][0] += av * b0;
+      c[r][1] += av * b1;
+    }
+  }
+  for (int r = 0; r < 4; ++r)
+    for (int h = 0; h < 2; ++h)
+      std::memcpy(acc + r * ldacc + 8 * h, &c[r][h], sizeof(f8));
+}
+
 // Rows [m0, m1) of C = A * B^T from decoded operands: `arow(r, dst)` writes
 // row r of A (K floats) and bt is B^T [K][N].  Each C element is the
 // runner's float accumulation in ascending k (runner.cpp:1586-1597), blocked
-// over (n, k) so every element is still summed strictly in k order.
+// over (n, k) so every element is still summed strictly in k order.  Whole
+// 4 x 16 blocks run the register micro-kernel, edges the scalar loop (the
+// same arithmetic per element).
 template <typename ARow>
-void gemmFloatRows(ARow arowOf, const std::vector<float> &bt, float *c, int m0,
-                   int m1, int n, int k, int threads) {
+void gemmFloatRows(ARow arowOf, const float *bt, float *c, int m0,
+                   int m1, int n, int k, int threads, int c_row0 = 0) {
   constexpr int NB = 128, KB = 256, MB = 32;
   int mBlocks = (m1 - m0 + MB - 1) / MB;
   parallelFor(0, mBlocks, threads, [&](int mb) {
@@ -320,19 +351,38 @@ void gemmFloatRows(ARow arowOf, const std::vector<float> &bt, float *c, int m0,
       std::fill(acc.begin(), acc.end(), 0.0f);
       for (int kb = 0; kb < k; kb += KB) {
         int ke = std::min(kb + KB, k);
-        for (int r = rb; r < re; ++r) {
+        int r = rb;
+        for (; r + 4 <= re; r += 4) {
+          const float *a4[4];
+          for (int q = 0; q < 4; ++q)
+            a4[q] = arow.data() + static_cast<size_t>(r + q - rb) * k;
+          int j = 0;
+          for (; j + 16 <= nw; j += 16)
+            microKernel4x16(a4, bt + nb + j, static_cast<size_t>(n), kb, ke,
+                            acc.data() + static_cast<size_t>(r - rb) * NB + j, NB);
+          for (int q = 0; q < 4; ++q) {
+            float *accr = acc.data() + static_cast<size_t>(r + q - rb) * NB;
+            for (int i = kb; i < ke; ++i) {
+              const float av = a4[q][i];
+              const float *btr = bt + static_cast<size_t>(i) * n + nb;
+              for (int jj = j; jj < nw; ++jj)
+                accr[jj] += av * btr[jj];
+            }
+          }
+        }
+        for (; r < re; ++r) {
           float *accr = acc.data() + static_cast<size_t>(r - rb) * NB;
           const float *ar = arow.data() + static_cast<size_t>(r - rb) * k;
           for (int i = kb; i < ke; ++i) {
             float av = ar[i];
-            const float *btr = bt.data() + static_cast<size_t>(i) * n + nb;
+            const float *btr = bt + static_cast<size_t>(i) * n + nb;
             for (int j = 0; j < nw; ++j)
               accr[j] += av * btr[j];
           }
         }
       }
       for (int r = rb; r < re; ++r)
-        std::memcpy(c + static_cast<size_t>(r) * n + nb,
+        std::memcpy(c + static_cast<size_t>(r - c_row0) * n + nb,
                     acc.data() + static_cast<size_t>(r - rb) * NB,
                     sizeof(float) * nw);
     }
@@ -343,23 +393,38 @@ void gemmFloatRows(ARow arowOf, const std::vector<float> &bt, float *c, int m0,
 
 extern "C" {
 
-// Rows [m0, m1) of C = A * B^T with A [M x K] and B [N x K] row-major (f16 or
-// bf16).  This is also the multithreaded CPU baseline that bench.py times.
-void oracle_gemm_nt_rows(const uint16_t *a, const uint16_t *b, float *c,
-                         int m0, int m1, int n, int k, int dtype, int threads) {
-  // B^T as float, [K][N], shared by all threads.
-  std::vector<float> bt(static_cast<size_t>(k) * n);
+// B [N x K] (f16 or bf16) widened and transposed to B^T [K][N] floats, the
+// operand layout gemmFloatRows streams.
+void oracle_gemm_prepare_bt(const uint16_t *b, float *bt, int n, int k, int dtype,
+                            int threads) {
   parallelFor(0, n, threads, [&](int col) {
     for (int i = 0; i < k; ++i)
-      bt[static_cast<size_t>(i) * n + col] =
-          toFloat(b[static_cast<size_t>(col) * k + i], dtype);
+      bt[static_cast<size_t>(i) * n + col] = toFloat(b[static_cast<size_t>(col) * k + i], dtype);
   });
+}
+
+// Rows [m0, m1) of C = A * B^T from A [M x K] (f16 or bf16) and a prepared
+// B^T (oracle_gemm_prepare_bt), into c [m1 - m0][N] (row r at c + (r - m0) *
+// N).  bench.py times this (and the preparation, apportioned per row) as the
+// multithreaded CPU baseline.
+void oracle_gemm_nt_rows_bt(const uint16_t *a, const float *bt, float *c, int m0, int m1,
+                            int n, int k, int dtype, int threads) {
   gemmFloatRows(
       [&](int r, float *dst) {
         for (int i = 0; i < k; ++i)
           dst[i] = toFloat(a[static_cast<size_t>(r) * k + i], dtype);
       },
-      bt, c, m0, m1, n, k, threads);
+      bt, c, m0, m1, n, k, threads, m0);
+}
+
+// Rows [m0, m1) of C = A * B^T with A [M x K] and B [N x K] row-major (f16 or
+// bf16).
+void oracle_gemm_nt_rows(const uint16_t *a, const uint16_t *b, float *c,
+                         int m0, int m1, int n, int k, int dtype, int threads) {
+  std::vector<float> bt(static_cast<size_t>(k) * n);
+  oracle_gemm_prepare_bt(b, bt.data(), n, k, dtype, threads);
+  oracle_gemm_nt_rows_bt(a, bt.data(), c + static_cast<size_t>(m0) * n, m0, m1, n, k, dtype,
+                         threads);
 }
 
 void oracle_gemm_nt(const uint16_t *a, const uint16_t *b, float *c, int m,
@@ -711,7 +776,7 @@ void oracle_gemm_mxfp4_rows(const uint8_t *a, const uint8_t *b,
         for (int i = 0; i < k; ++i)
           dst[i] = mxfp4Scaled(a, sa, m, k, r, i);
       },
-      bt, c, m0, m1, n, k, threads);
+      bt.data(), c, m0, m1, n, k, threads);
 }
 
 // AITER B layout (runner.cpp:1223-1246; wave_matmul.py:891-910): byte

@@ -55,6 +55,10 @@ void oracle_gemm_nt(const uint16_t *a, const uint16_t *b, float *c, int m,
                     int n, int k, int dtype, int threads);
 void oracle_gemm_nt_rows(const uint16_t *a, const uint16_t *b, float *c,
                          int m0, int m1, int n, int k, int dtype, int threads);
+void oracle_gemm_prepare_bt(const uint16_t *b, float *bt, int n, int k, int dtype,
+                            int threads);
+void oracle_gemm_nt_rows_bt(const uint16_t *a, const float *bt, float *c, int m0, int m1,
+                            int n, int k, int dtype, int threads);
 float oracle_gemm_element(const uint16_t *a, const uint16_t *b, int k,
                           int dtype, int64_t row, int64_t col);
 void oracle_round_output(const float *in, void *out, size_t n, int out_dtype);

@@ -54,6 +54,8 @@ def lib() -> ctypes.CDLL:
             "oracle_gemm_inputs": (None, [_P, _I, _I, _I, _I, _I, _I]),
             "oracle_gemm_nt": (None, [_P, _P, _P, _I, _I, _I, _I, _I]),
             "oracle_gemm_nt_rows": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _I]),
+            "oracle_gemm_prepare_bt": (None, [_P, _P, _I, _I, _I, _I]),
+            "oracle_gemm_nt_rows_bt": (None, [_P, _P, _P, _I, _I, _I, _I, _I, _I]),
             "oracle_gemm_element": (ctypes.c_float, [_P, _P, _I, _I, _I64, _I64]),
             "oracle_round_output": (None, [_P, _P, _SZ, _I]),
             "oracle_mxfp4_code_value": (ctypes.c_float, [_I]),
@@ -148,6 +150,32 @@ def gemm_nt_rows(a: np.ndarray, b: np.ndarray, m0: int, m1: int, dtype: int = F1
     lib().oracle_gemm_nt_rows(_ptr(a), _ptr(b), _ptr(c), m0, m1, n, k, dtype,
                               threads or hardware_threads())
     return c[m0:m1]
+
+
+def gemm_prepare_bt(b: np.ndarray, dtype: int = F16, threads: int | None = None) -> np.ndarray:
+    """B [N x K] (16-bit bits) widened to float and transposed, [K][N]: the
+    operand gemm_nt_rows_bt takes."""
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    n, k = b.shape
+    bt = np.empty((k, n), dtype=np.float32)
+    lib().oracle_gemm_prepare_bt(_ptr(b), _ptr(bt), n, k, dtype, threads or hardware_threads())
+    return bt
+
+
+def gemm_nt_rows_bt(a: np.ndarray, bt: np.ndarray, m0: int, m1: int, dtype: int = F16,
+                    threads: int | None = None, out: np.ndarray | None = None) -> np.ndarray:
+    """Rows [m0, m1) of A . B^T from a prepared B^T (gemm_prepare_bt); same
+    arithmetic as gemm_nt.  `out`: a float32 [m1 - m0, N] buffer to write."""
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    bt = np.ascontiguousarray(bt, dtype=np.float32)
+    k, n = bt.shape
+    assert a.shape[1] == k and 0 <= m0 <= m1 <= a.shape[0]
+    if out is None:
+        out = np.empty((m1 - m0, n), dtype=np.float32)
+    assert out.shape == (m1 - m0, n) and out.dtype == np.float32 and out.flags.c_contiguous
+    lib().oracle_gemm_nt_rows_bt(_ptr(a), _ptr(bt), _ptr(out), m0, m1, n, k, dtype,
+                                 threads or hardware_threads())
+    return out
 
 
 def gemm_elements(a: np.ndarray, b: np.ndarray, rows, cols, dtype: int = F16) -> np.ndarray:

@@ -186,6 +186,32 @@ def test_gemm_reference_vs_numpy_exact_and_layout(oracle):
         assert np.array_equal(rows, ref[10:20].astype(np.float32))
 
 
+def test_blocked_gemm_sums_each_element_in_k_order(oracle):
+    """The blocked GEMM (register micro-kernel for whole 4 x 16 blocks, the
+    scalar loop at the edges) and the prepared-B^T entry the CPU baseline
+    times give, on inexact normal inputs where any change of summation
+    order or a fused multiply-add shows in the bits, exactly the runner's
+    per-element float accumulation (oracle_gemm_element, runner.cpp
+    :1586-1597); every output row and column sits in a block or an edge."""
+    rng = np.random.default_rng(1)
+    m, n, k = 70, 90, 300
+    for dtype in (oracle.F16, oracle.BF16):
+        af = rng.standard_normal((m, k)).astype(np.float32)
+        bf = rng.standard_normal((n, k)).astype(np.float32)
+        a = oracle.round_output(af, dtype).reshape(m, k)
+        b = oracle.round_output(bf, dtype).reshape(n, k)
+        ref = np.array([[oracle.gemm_elements(a, b, [r], [c], dtype)[0] for c in range(n)]
+                        for r in range(m)], dtype=np.float32)
+        assert np.array_equal(oracle.gemm_nt(a, b, dtype, threads=3), ref)
+        bt = oracle.gemm_prepare_bt(b, dtype, threads=2)
+        assert np.array_equal(bt, oracle.bits_to_f32(b, dtype).reshape(n, k).T)
+        assert np.array_equal(oracle.gemm_nt_rows_bt(a, bt, 5, 66, dtype, threads=4), ref[5:66])
+        # fused multiply-add or float64 accumulation would differ somewhere
+        fused = (oracle.bits_to_f32(a, dtype).reshape(m, k).astype(np.float64)
+                 @ oracle.bits_to_f32(b, dtype).reshape(n, k).astype(np.float64).T)
+        assert not np.array_equal(fused.astype(np.float32), ref)
+
+
 def test_output_coordinate_goldens(mm):
     # rand_int_test.cpp:112-141: MFMA wave64 fragment index -> (m, n)
     c = mm["output_coordinates"]["64:0"]
