@@ -60,6 +60,28 @@ int check_gemm(const void *A, const void *B, const void *C, int M, int N, int K,
   return WAVE_OK;
 }
 
+// Every argument check of wave_gemm_streamk_launch (shared with the
+// allocation-free entry point, which must reject a call before it touches
+// its static workspace).
+int check_streamk(const void *A, const void *B, const void *C, int M, int N, int K,
+                  int in_dtype, int out_dtype, int c_layout, int workers) {
+  int st = check_gemm(A, B, C, M, N, K, in_dtype, out_dtype, c_layout);
+  if (st != WAVE_OK)
+    return st;
+  if (c_layout == WAVE_TILE_PACKED)
+    return fail(WAVE_ERR_UNSUPPORTED, "streamk: tile-packed C is not supported (the "
+                "reference's Stream-K ABI stores column-major C)");
+  const int64_t work = (int64_t)wave::gemm::tiles_for(M) *
+                       wave::gemm::tiles_for(N) * wave::gemm::k_iterations(K);
+  if (work > INT32_MAX)
+    return fail(WAVE_ERR_UNSUPPORTED, "streamk: %lld work units exceed i32",
+                (long long)work);
+  if (workers <= 0 || workers > work)
+    return fail(WAVE_ERR_INVALID, "streamk: workers=%d must be in [1, %lld]",
+                workers, (long long)work);
+  return WAVE_OK;
+}
+
 int streamk_sizes(int M, int N, int workers, size_t *scratch, size_t *counters) {
   if (M <= 0 || N <= 0)
     return fail(WAVE_ERR_INVALID, "streamk: M=%d N=%d must be positive", M, N);
@@ -132,8 +154,11 @@ std::mutex g_noalloc_mu;
 void *g_noalloc_base[kNoAllocMaxDevices];  // per device: address of its `scratch`
 
 // This device's `scratch`, looked up once per device with that device
-// current (the first call on it).
-int noalloc_workspace(void **base) {
+// current (the first call on it).  The lookup may load this library's code
+// object onto the device, which must not happen inside a stream capture: a
+// first call made while `stream` is capturing is refused (make one call on
+// the device outside capture first).
+int noalloc_workspace(void **base, hipStream_t stream) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess)
@@ -142,6 +167,14 @@ int noalloc_workspace(void **base) {
     return fail(WAVE_ERR_UNSUPPORTED, "wave_gemm_streamk_noalloc_launch: device %d", dev);
   std::lock_guard<std::mutex> lock(g_noalloc_mu);
   if (!g_noalloc_base[dev]) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cap);
+    if (e != hipSuccess)
+      return hip_status(e, "wave_gemm_streamk_noalloc_launch: hipStreamIsCapturing");
+    if (cap != hipStreamCaptureStatusNone)
+      return fail(WAVE_ERR_UNSUPPORTED, "wave_gemm_streamk_noalloc_launch: the first call on "
+                  "device %d is inside a stream capture; make one call on it outside capture "
+                  "first (it resolves the static workspace's address)", dev);
     void *p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess)
@@ -330,22 +363,11 @@ int wave_gemm_streamk_launch(const void *A, const void *B, void *C, int M,
                              int N, int K, int in_dtype, int out_dtype,
                              int c_layout, float *scratch, uint32_t *counters,
                              int workers, void *stream) {
-  int st = check_gemm(A, B, C, M, N, K, in_dtype, out_dtype, c_layout);
+  int st = check_streamk(A, B, C, M, N, K, in_dtype, out_dtype, c_layout, workers);
   if (st != WAVE_OK)
     return st;
-  if (c_layout == WAVE_TILE_PACKED)
-    return fail(WAVE_ERR_UNSUPPORTED, "streamk: tile-packed C is not supported (the "
-                "reference's Stream-K ABI stores column-major C)");
   if (!scratch || !counters)
     return fail(WAVE_ERR_INVALID, "streamk: null scratch or counters");
-  const int64_t work = (int64_t)wave::gemm::tiles_for(M) *
-                       wave::gemm::tiles_for(N) * wave::gemm::k_iterations(K);
-  if (work > INT32_MAX)
-    return fail(WAVE_ERR_UNSUPPORTED, "streamk: %lld work units exceed i32",
-                (long long)work);
-  if (workers <= 0 || workers > work)
-    return fail(WAVE_ERR_INVALID, "streamk: workers=%d must be in [1, %lld]",
-                workers, (long long)work);
   wave::gemm::GemmArgs g;
   g.A = A;
   g.B = B;
@@ -366,18 +388,22 @@ int wave_gemm_streamk_launch(const void *A, const void *B, void *C, int M,
 int wave_gemm_streamk_noalloc_launch(const void *A, const void *B, void *C, int M, int N,
                                      int K, int in_dtype, int out_dtype, int c_layout,
                                      int workers, void *stream) {
-  int st = check_gemm(A, B, C, M, N, K, in_dtype, out_dtype, c_layout);
-  if (st != WAVE_OK)
-    return st;
-  const int64_t tiles = (int64_t)wave::gemm::tiles_for(M) * wave::gemm::tiles_for(N);
   if (workers <= 0)
     return fail(WAVE_ERR_INVALID, "streamk noalloc: workers=%d must be positive", workers);
+  const int64_t tiles = M > 0 && N > 0
+                            ? (int64_t)wave::gemm::tiles_for(M) * wave::gemm::tiles_for(N)
+                            : 0;
   if (workers > kNoAllocWorkers || tiles > kNoAllocTiles)
     return fail(WAVE_ERR_UNSUPPORTED, "streamk noalloc: workers=%d and %lld output tiles "
                 "exceed the static workspace (at most %d workers and %d 256x256 tiles)",
                 workers, (long long)tiles, kNoAllocWorkers, kNoAllocTiles);
+  // Every check of wave_gemm_streamk_launch runs before the counter reset
+  // below writes the array that all calls on this GPU share.
+  int st = check_streamk(A, B, C, M, N, K, in_dtype, out_dtype, c_layout, workers);
+  if (st != WAVE_OK)
+    return st;
   void *base = nullptr;
-  st = noalloc_workspace(&base);
+  st = noalloc_workspace(&base, static_cast<hipStream_t>(stream));
   if (st != WAVE_OK)
     return st;
   float *slots = static_cast<float *>(base);

@@ -121,7 +121,13 @@ int wave_gemm_streamk_launch(const void *A, const void *B, void *C, int M,
  * larger requests return WAVE_ERR_UNSUPPORTED.  Each call first zeroes the
  * counters it uses with a fill kernel on `stream` and calls no hipMalloc,
  * hipFree or allocating library routine.  All calls on one GPU share the
- * array: calls that overlap on one GPU (on different streams) race. */
+ * array: calls that overlap on one GPU (on different streams) race.  The
+ * first call on each device resolves the array's address
+ * (hipGetSymbolAddress, which can load the library's code object): make it
+ * outside any stream capture; a first call on a capturing stream returns
+ * WAVE_ERR_UNSUPPORTED, and later calls may be captured into a HIP graph.
+ * Every argument check precedes the counter reset, so a rejected call
+ * leaves the array untouched. */
 int wave_gemm_streamk_noalloc_launch(const void *A, const void *B, void *C,
                                      int M, int N, int K, int in_dtype,
                                      int out_dtype, int c_layout, int workers,

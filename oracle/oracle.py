@@ -393,7 +393,8 @@ def fa_backward(q, k, v, do, *, scale: float | None = None, causal: bool = False
     sc = 1.0 / np.sqrt(D) if not scale else float(scale)
     kk = np.repeat(k, g, axis=1)
     vv = np.repeat(v, g, axis=1)
-    s = sc * np.einsum("bhqd,bhkd->bhqk", q, kk)
+    kt = np.swapaxes(kk, -1, -2)
+    s = sc * np.matmul(q, kt)
     if causal:
         mask = np.triu(np.ones((S, S), dtype=bool), 1)
         s = np.where(mask, -np.inf, s)
@@ -402,14 +403,14 @@ def fa_backward(q, k, v, do, *, scale: float | None = None, causal: bool = False
     tot = e.sum(axis=-1, keepdims=True)
     p = e / tot
     lse = (m + np.log(tot))[..., 0]
-    o = np.einsum("bhqk,bhkd->bhqd", p, vv)
-    dvv = np.einsum("bhqk,bhqd->bhkd", p, do)
-    dp = np.einsum("bhqd,bhkd->bhqk", do, vv)
+    o = np.matmul(p, vv)
+    dvv = np.matmul(np.swapaxes(p, -1, -2), do)
+    dp = np.matmul(do, np.swapaxes(vv, -1, -2))
     o_d = o if o_delta is None else np.asarray(o_delta, dtype=np.float64)
     delta = (do * o_d).sum(axis=-1, keepdims=True)
     ds = p * (dp - delta)
-    dq = sc * np.einsum("bhqk,bhkd->bhqd", ds, kk)
-    dkk = sc * np.einsum("bhqk,bhqd->bhkd", ds, q)
+    dq = sc * np.matmul(ds, kk)
+    dkk = sc * np.matmul(np.swapaxes(ds, -1, -2), q)
     dk = dkk.reshape(B, Hkv, g, S, D).sum(axis=2)
     dv = dvv.reshape(B, Hkv, g, S, D).sum(axis=2)
     return o, lse, dq, dk, dv

@@ -57,6 +57,41 @@ def test_fa_bwd_parity(wave, oracle, dev, dt, causal, B, Hq, Hkv, S):
     check(got, ref, dt)
 
 
+# Relative bound at the benchmarked shape, max |got - ref| / max |ref| per
+# gradient.  f16: P and dS carry 11-bit mantissas into the gradient products,
+# so the error is a few 2^-11 relative; bf16 (8-bit mantissas) about 8x that.
+TOL_FULL = {1: 5e-3, 2: 2e-2}
+
+
+@pytest.mark.parametrize("dt", [1, 2])
+def test_fa_bwd_benchmark_shape(wave, oracle, dev, dt):
+    """The backward at the shape bench.py reports (B4 H32 S4096 D128,
+    non-causal): the whole problem on the GPU, three (batch, head) pairs
+    against the float64 oracle (each head's gradients depend on that head
+    alone), at TOL_FULL relative to each gradient's largest magnitude."""
+    B, H, S, D = 4, 32, 4096, 128
+    g = torch.Generator().manual_seed(23)
+    q, k, v, do = (torch.randn((B, H, S, D), generator=g).to(TDT[dt]) for _ in range(4))
+    qd, kd, vd, dod = (t.to(dev) for t in (q, k, v, do))
+    o, lse = wave.flash_attention_lse(qd, kd, vd)
+    dq, dk, dv = wave.flash_attention_bwd(qd, kd, vd, o, dod, lse)
+    torch.cuda.synchronize()
+    f64 = lambda t: t.float().cpu().numpy().astype(np.float64)
+    worst = {}
+    for b, h in ((0, 0), (1, 13), (3, 31)):
+        one = lambda t: f64(t[b:b + 1, h:h + 1])
+        ref = oracle.fa_backward(one(q), one(k), one(v), one(do), o_delta=one(o))
+        got = (one(o), lse[b:b + 1, h:h + 1].cpu().numpy(), one(dq), one(dk), one(dv))
+        for name, x, y in zip(("o", "lse", "dq", "dk", "dv"), got, ref):
+            err = float(np.max(np.abs(x - y)))
+            rel = err if name == "lse" else err / float(np.max(np.abs(y)))
+            worst[name] = max(worst.get(name, 0.0), rel)
+    msg = ", ".join(f"{n} {r:.3g}" for n, r in worst.items())
+    assert worst["lse"] <= TOL_LSE[dt], msg
+    for name in ("o", "dq", "dk", "dv"):
+        assert worst[name] <= TOL_FULL[dt], f"{name}: {msg}"
+
+
 def test_fa_bwd_explicit_scale(wave, oracle, dev):
     got, ref = run_bwd(wave, oracle, dev, 1, 1, 2, 1, 128, True, seed=4, scale=0.05)
     check(got, ref, 1)

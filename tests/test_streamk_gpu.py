@@ -68,8 +68,11 @@ def test_workspace_reuse_many_launches(wave, oracle, dev):
 
 @pytest.mark.parametrize("in_dt", [1, 2])
 @pytest.mark.parametrize("out_dt", [torch.float32, torch.float16, torch.bfloat16])
-# (512, 512, 1056): whole tiles with K off the 64-deep stage, so Stream-K
-# runs its bounds-checked path and the tiled kernel its hybrid one.
+# All of these have K % 4 == 0 and 8-byte aligned rows, so Stream-K and the
+# tiled kernel both run the hybrid DMA path (whole 64-deep stages on the
+# ring, the K remainder through registers); (512, 512, 1056) is whole tiles
+# with K off the 64-deep stage.  test_masked_streamk_many_contributors covers
+# the bounds-checked Stream-K path.
 @pytest.mark.parametrize("shape,workers", [((128, 1024, 2048), 40), ((300, 520, 700), 9),
                                            ((257, 255, 4100), 13), ((1024, 1024, 1024), 64),
                                            ((512, 512, 1056), 7)])
@@ -80,6 +83,28 @@ def test_ragged_streamk_matches_tiled(wave, oracle, dev, in_dt, out_dt, shape, w
     tiled = wave.gemm(da, db, out_dtype=out_dt)
     torch.cuda.synchronize()
     assert torch.equal(sk, tiled)
+
+
+@pytest.mark.parametrize("in_dt", [1, 2])
+@pytest.mark.parametrize("out_dt", [torch.float32, torch.float16])
+@pytest.mark.parametrize("shape,workers", [((300, 520, 701), 30), ((257, 255, 4102), 13)])
+def test_masked_streamk_many_contributors(wave, oracle, dev, in_dt, out_dt, shape, workers):
+    """K % 4 != 0: Stream-K runs its bounds-checked kernel (element loads with
+    zero fill, the path taken for K % 4 != 0 or unaligned A/B), here with 3
+    to 6 contributors per tile, so its fold of more than two partials and
+    the two-part pass both run.  Bucket inputs: bit-exact against the tiled
+    kernel, and the counters are zero again after every launch."""
+    M, N, K = shape
+    a, b, da, db = inputs(oracle, dev, M, N, K, in_dt, seed=19)
+    ws = wave.StreamKWorkspace(M, N, workers, dev)
+    tiled = wave.gemm(da, db, out_dtype=out_dt)
+    for _ in range(3):
+        sk = wave.gemm_streamk(da, db, workers, out_dtype=out_dt, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(sk, tiled)
+        assert ws.nonzero_counters() == 0
+    if out_dt == torch.float32:
+        assert np.array_equal(sk.cpu().numpy(), oracle.gemm_nt(a, b, in_dt))
 
 
 def test_dirty_counters_are_detected_and_reset(wave, oracle, dev):
@@ -110,22 +135,55 @@ def test_config3_streamk_bf16(wave, oracle, dev):
 
 
 # ---- shape-driven dispatch (wave_gemm_auto_launch) ------------------------------
-@pytest.mark.parametrize("shape,streamk", [((2048, 512, 8192), True),   # 16 tiles, long K
-                                           ((1000, 300, 4100), True),   # ragged, 8 tiles
-                                           # ragged, K off the stage, 16 tiles:
-                                           # 128 workers, 8-9 contributors a tile
-                                           ((1000, 1000, 16400), True),
-                                           ((4096, 4096, 512), False),  # 256 tiles
-                                           ((3072, 3072, 8192), False),  # 144 tiles: uneven split
-                                           ((4096, 2048, 4096), False),  # 128 tiles, K 4096
-                                           ((128, 1024, 8192), False)])  # short-M kernel
-def test_auto_dispatch_matches_tiled(wave, oracle, dev, shape, streamk):
-    """Bucket inputs make every sum exact, so the auto path (Stream-K or not)
-    equals wave_gemm_launch bit for bit; a too-small workspace falls back to
-    the tiled kernel."""
+def auto_workers(M, N, K, cus):
+    """Stream-K workers wave_gemm_auto_launch picks for (M, N, K) on a device
+    with `cus` compute units (0: the tiled or short-M kernel); the rules of
+    auto_workers in 7_amd/csrc/wave_runtime.cpp, restated so the expected
+    choice follows the CU count the device reports."""
+    t = -(-M // 256) * -(-N // 256)
+    if M <= 128 or K < 4096 or t >= cus:
+        return 0
+    if t * 2 >= cus and K < 8192:
+        return 0
+    if t * 2 > cus:
+        return 0
+    w = min(t * 2, cus)
+    if t * 4 <= cus:
+        w = max(w, min(t * (K // 2048), cus // 2))
+    return min(w, t * -(-K // 64))
+
+
+def device_cus(dev):
+    return torch.cuda.get_device_properties(dev).multi_processor_count
+
+
+def expected_workspace(wave, M, N, K, dev):
+    w = auto_workers(M, N, K, device_cus(dev))
+    if w == 0:
+        return 0, 0
+    sb, cb = wave.streamk_workspace_bytes(M, N, w)
+    return w, sb + cb
+
+
+@pytest.mark.parametrize("shape", [(2048, 512, 8192),    # 16 tiles, long K
+                                   (1000, 300, 4100),    # ragged, 8 tiles
+                                   # K % 4 != 0: the bounds-checked Stream-K kernel
+                                   (1000, 300, 4101),
+                                   # ragged, K off the stage, 16 tiles:
+                                   # 128 workers, 8-9 contributors a tile
+                                   (1000, 1000, 16400),
+                                   (4096, 4096, 512),    # 256 tiles
+                                   (3072, 3072, 8192),   # 144 tiles: uneven split
+                                   (4096, 2048, 4096),   # 128 tiles, K 4096
+                                   (128, 1024, 8192)])   # short-M kernel
+def test_auto_dispatch_matches_tiled(wave, oracle, dev, shape):
+    """The workspace size names the worker count the dispatch picks (checked
+    against the rules for this device's CU count).  Bucket inputs make every
+    sum exact, so the auto path (Stream-K or not) equals wave_gemm_launch bit
+    for bit; a too-small workspace falls back to the tiled kernel."""
     M, N, K = shape
     need = wave.gemm_auto_workspace_bytes(M, N, K)
-    assert (need > 0) == streamk
+    assert need == expected_workspace(wave, M, N, K, dev)[1]
     a = oracle.gemm_inputs(M, K, 2, 5, 0)
     b = oracle.gemm_inputs(N, K, 2, 5, 1)
     A, B = to_dev(a, torch.bfloat16, dev), to_dev(b, torch.bfloat16, dev)
@@ -137,6 +195,50 @@ def test_auto_dispatch_matches_tiled(wave, oracle, dev, shape, streamk):
         assert torch.equal(got, ref)
     small = torch.empty((max(need // 2, 1),), dtype=torch.uint8, device=dev)
     assert torch.equal(wave.gemm_auto(A, B, out_dtype=torch.bfloat16, workspace=small), ref)
+
+
+def test_config3c_auto_dispatch(wave, oracle, dev):
+    """BASELINE config 3c (8192 x 1024 x 28672 bf16: 128 output tiles) through
+    wave_gemm_auto_launch, the path bench.py reports for it (Stream-K with
+    2 * tiles workers on 256 CUs: 448 K units a tile split in two).
+    * N(0,1)/sqrt(K) inputs: sampled rows within 2e-3 * sqrt(K) of the
+      oracle;
+    * bucket inputs: bit-identical to wave_gemm_launch, on a dirty workspace,
+      twice, with the counters back at zero."""
+    M, N, K = 8192, 1024, 28672
+    w, need = expected_workspace(wave, M, N, K, dev)
+    assert wave.gemm_auto_workspace_bytes(M, N, K) == need
+    if device_cus(dev) == 256:
+        assert w == 256
+    g = torch.Generator(device="cpu").manual_seed(31)
+    a = (torch.randn((M, K), generator=g) / np.sqrt(K)).to(torch.bfloat16)
+    b = (torch.randn((N, K), generator=g) / np.sqrt(K)).to(torch.bfloat16)
+    ws = torch.full((max(need, 1),), 0xFF, dtype=torch.uint8, device=dev)
+    c = wave.gemm_auto(a.to(dev), b.to(dev), out_dtype=torch.bfloat16, workspace=ws)
+    torch.cuda.synchronize()
+    abits = a.view(torch.int16).numpy().view(np.uint16)
+    bbits = b.view(torch.int16).numpy().view(np.uint16)
+    got = c.float().cpu().numpy()
+    bt = oracle.gemm_prepare_bt(bbits, 2)
+    rows = [0, 1, 255, 256, 4095, 4096, 8190, 8191] + list(range(97, M, 1021))
+    worst = 0.0
+    for r in rows:
+        ref = oracle.gemm_nt_rows_bt(abits, bt, r, r + 1, 2)[0]
+        worst = max(worst, float(np.abs(got[r] - ref).max()))
+    assert worst <= 2e-3 * np.sqrt(K), worst
+    del a, b, c, bt
+    a = oracle.gemm_inputs(M, K, 2, 5, 0)
+    b = oracle.gemm_inputs(N, K, 2, 5, 1)
+    A, B = to_dev(a, torch.bfloat16, dev), to_dev(b, torch.bfloat16, dev)
+    ref = wave.gemm(A, B, out_dtype=torch.bfloat16)
+    ws.fill_(0xFF)
+    for _ in range(2):
+        got = wave.gemm_auto(A, B, out_dtype=torch.bfloat16, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref)
+    if w:
+        sb, _ = wave.streamk_workspace_bytes(M, N, w)
+        assert int(ws[sb:].count_nonzero()) == 0
 
 
 @pytest.mark.parametrize("shape,workers", [((1024, 1024, 8192), 64),    # 4 contributors
