@@ -19,7 +19,7 @@ struct FwdArgs {
   int causal = 0;           // mask key > query (top-left aligned)
   float scale = 0.f;        // softmax scale; 0 selects 1/sqrt(head_dim)
   float qk_max_abs = 0.f;   // > 0: |Q|, |K| <= qk_max_abs, fixed-max kernel
-  int waves = 8;            // 8: ping-pong kernel; 4: the 4-wave kernel
+  int waves = 8;            // 12: three-group kernel; 8: ping-pong kernel; 4: 4-wave kernel
   float *lse = nullptr;     // optional [batch][q_heads][seq_q] row log-sum-exp
 };
 

@@ -1,6 +1,8 @@
 // attention_fwd.hip -- instantiation and host launch of the gfx950
-// flash-attention forward kernels: the 8-wave ping-pong kernel
-// (attention_kernels.hpp) and the 4-wave kernel (attention_fwd4.hpp).
+// flash-attention forward kernels: the 12-wave three-group kernel
+// (attention_fwd3.hpp), the 8-wave ping-pong kernel (attention_kernels.hpp)
+// and the 4-wave kernel (attention_fwd4.hpp).
+#include "attention_fwd3.hpp"
 #include "attention_fwd4.hpp"
 #include "attention_kernels.hpp"
 
@@ -20,7 +22,8 @@ hipError_t launch_fwd(const FwdArgs &a, hipStream_t stream) {
   p.kv_heads = a.kv_heads;
   p.seq_q = a.seq_q;
   p.seq_k = a.seq_k;
-  p.q_blocks = (a.seq_q + 32 * kPPWaves - 1) / (32 * kPPWaves);
+  const int rows = a.waves == kR3Waves ? kR3Rows : 32 * kPPWaves;  // 4 waves: 256 too
+  p.q_blocks = (a.seq_q + rows - 1) / rows;
   p.causal = a.causal;
   const float scale = a.scale > 0.f ? a.scale : 1.0f / std::sqrt((float)a.head_dim);
   p.scale_log2 = scale * kLog2e;
@@ -42,6 +45,22 @@ hipError_t launch_fwd(const FwdArgs &a, hipStream_t stream) {
         hipLaunchKernelGGL((fwd4_kernel<kBF16, true>), grid, block, 0, stream, p);
       else
         hipLaunchKernelGGL((fwd4_kernel<kBF16, false>), grid, block, 0, stream, p);
+    }
+    return hipGetLastError();
+  }
+  if (a.waves == kR3Waves) {
+    // 12 waves x 32 query rows per CTA, three rotating groups of 4 waves.
+    const dim3 grid(p.q_blocks * a.batch * a.q_heads), block(64 * kR3Waves);
+    if (a.dtype == kF16) {
+      if (fixed)
+        hipLaunchKernelGGL((fwd3_kernel<kF16, true>), grid, block, 0, stream, p);
+      else
+        hipLaunchKernelGGL((fwd3_kernel<kF16, false>), grid, block, 0, stream, p);
+    } else {
+      if (fixed)
+        hipLaunchKernelGGL((fwd3_kernel<kBF16, true>), grid, block, 0, stream, p);
+      else
+        hipLaunchKernelGGL((fwd3_kernel<kBF16, false>), grid, block, 0, stream, p);
     }
     return hipGetLastError();
   }

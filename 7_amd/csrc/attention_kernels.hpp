@@ -147,6 +147,13 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
   asm("" : "+v"(v));
   return v;
 }
+// The same, but never merged with another use: each call yields a value the
+// compiler cannot share, so expressions built on it are recomputed where
+// they are used instead of being kept live in registers.
+__device__ __forceinline__ uint32_t fresh(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
 
 // LDS of one CTA: K ring [4][64 keys][256 B] (XOR-swizzled chunks), V^T ring
 // [2][128 d][144 B].

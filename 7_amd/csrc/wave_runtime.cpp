@@ -523,8 +523,8 @@ int check_qk_bound(float qk_max_abs, float scale, int head_dim, int dtype) {
 int fa_fwd(const void *Q, const void *K, const void *V, void *O, int batch, int q_heads,
            int kv_heads, int seq, int head_dim, int dtype, int causal, float scale,
            float qk_max_abs, int waves, void *stream, const char *name, float *lse = nullptr) {
-  if (waves != 4 && waves != 8)
-    return fail(WAVE_ERR_INVALID, "fa: waves=%d must be 4 or 8", waves);
+  if (waves != 4 && waves != 8 && waves != 12)
+    return fail(WAVE_ERR_INVALID, "fa: waves=%d must be 4, 8 or 12", waves);
   if (!Q || !K || !V || !O)
     return fail(WAVE_ERR_INVALID, "fa: null Q, K, V or O");
   if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || seq <= 0)

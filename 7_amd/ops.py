@@ -233,8 +233,9 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
 
     qk_max_abs: the caller's bound on |Q| and |K|; selects the fixed-max
     kernel (no online max; wave_fa_fwd_bounded_launch).  waves: 8 (the
-    ping-pong kernel) or 4 (the reference's 4-wave configuration;
-    wave_fa_fwd_config_launch)."""
+    ping-pong kernel), 12 (three rotating wave groups, 384 query rows a
+    CTA) or 4 (the reference's 4-wave configuration); other than 8 through
+    wave_fa_fwd_config_launch."""
     B, Hq, Hkv, S, D = _fa_shapes(q, k, v)
     out = _out(out, q.shape, q.dtype, q.device)
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, Hq, Hkv, S, D,

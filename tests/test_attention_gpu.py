@@ -17,9 +17,10 @@
   large ones (runner :204-232), and --zero-qk (every row = mean of V).
 * wave_fa_f32_launch vs oracle.fa_f32_reference at the runner tolerance
   3e-3 (wave-fa-calibrate-runner.cpp:251-273).
-* Every forward case runs on both kernels: waves=8 (wave_fa_fwd_launch) and
-  the reference's 4-wave configuration (wave_fa_fwd_config_launch, waves=4;
-  wave_flash_attention.py:44-93).
+* Every forward case runs on all three kernels: waves=8 (the ping-pong
+  kernel), the reference's 4-wave configuration (waves=4;
+  wave_flash_attention.py:44-93) and the three-group kernel (waves=12, 384
+  query rows a CTA), through wave_fa_fwd_launch / wave_fa_fwd_config_launch.
 """
 
 import math
@@ -38,7 +39,7 @@ FIXED_TOL = {1: 1e-3, 2: 7.5e-3}
 TDT = {1: torch.float16, 2: torch.bfloat16}
 
 
-WAVES = pytest.mark.parametrize("waves", [8, 4])
+WAVES = pytest.mark.parametrize("waves", [8, 4, 12])
 
 
 def run_fa(wave, oracle, dev, q, k, v, dt, B, Hq, Hkv, S, causal, heads, rows, waves=8):
@@ -121,7 +122,7 @@ def test_config4_f16_b4_h32_s4096(wave, oracle, dev, waves):
     n = B * H * S * 128
     q, k, v = (normal_bits(n, 1, s) for s in (11, 12, 13))
     heads = oracle.fa_reference_heads(B * H)
-    rows = oracle.fa_reference_rows(S) + [1, 255, 256, 1000, 4000]
+    rows = oracle.fa_reference_rows(S) + [1, 255, 256, 383, 384, 767, 768, 1000, 4000]
     err = run_fa(wave, oracle, dev, q, k, v, 1, B, H, H, S, False, heads, sorted(set(rows)),
                  waves)
     assert err <= TOL[1], err
@@ -135,7 +136,8 @@ def test_config5_causal_gqa_bf16_s8192(wave, oracle, dev, waves):
     k = normal_bits(B * Hkv * S * 128, 2, 22)
     v = normal_bits(B * Hkv * S * 128, 2, 23)
     heads = [0, 7, 8, 31, 63]
-    rows = sorted(set(oracle.fa_reference_rows(S) + [1, 63, 64, 4097, 8191]))
+    rows = sorted(set(oracle.fa_reference_rows(S) + [1, 63, 64, 383, 384, 4097, 8063, 8064,
+                                                     8191]))
     err = run_fa(wave, oracle, dev, q, k, v, 2, B, Hq, Hkv, S, True, heads, rows, waves)
     assert err <= TOL[2], err
 
