@@ -156,6 +156,309 @@ hipError_t launch_out(const SkinnyParams &p, bool cm, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ------------------------------------------------------------ split-K
+// The same product with wider column blocks and a K split: CTA (tile, split)
+// owns C's BN-column block `tile` (BN = 128 or 64) and all M rows over one
+// of `splits` contiguous K ranges (whole 64-deep stages, split j taking
+// stages [j*q + min(j, r), +q + (j < r)) of nk = q*splits + r).  A CTA of
+// the unsplit kernel streams all of A (M x K) through LDS for 32 columns;
+// here it streams 1/splits of A for BN columns, so at 128 x 8192 x 8192
+// with BN = 128 and 4 splits each CU moves 1 MiB a launch instead of 4 MiB
+// and the L2 -> LDS traffic (which bounds the unsplit kernel) falls under
+// B's HBM stream.
+//
+// The four waves share one LDS ring of stages holding A rows 0..127, then
+// the block's BN B rows, each wave issuing a quarter of every stage; wave
+// w computes a (128 / WM) x (BN / WN) block of C, WM x WN = 2 x 2 waves at
+// BN = 128 and 4 x 1 at BN = 64.  One barrier a stage: after it every
+// wave's DMA of the stage has landed and every wave has finished reading
+// the slot the next issue overwrites.
+//
+// Reduction: each contributor takes an arrival ticket on the tile's first
+// counter when its K range is done.  All but the last store their fp32
+// partials (16-byte groups at f32x4 index group*256 + thread, fully
+// coalesced) to their slots and count themselves on the second counter
+// with an agent-scope release; the last arriver waits for that count, sums
+// the partials in split order (its own from its accumulators),
+// s = ((p_0 + p_1) + p_2) + p_3, so the result does not depend on arrival
+// order, stores C, and resets both counters to zero for the next launch.
+// Splits of a tile take consecutive CTA numbers after the XCD renumbering
+// (workgroup i runs on XCD i % 8), so they run on one XCD.
+constexpr int kXMaxSplits = 4;
+// Cache-policy operand of the buffer store builtins on gfx950: bit 4 = sc1
+// (with sc0 clear: device scope).
+constexpr int kScopeDevice = 16;
+
+template <int BN> struct SplitCfg {
+  static_assert(BN == 128 || BN == 64, "column block");
+  static constexpr int WN = BN == 128 ? 2 : 1, WM = 4 / WN;
+  static constexpr int TI = 128 / WM / 32, TJ = BN / WN / 32;  // MFMA tiles a wave
+  static constexpr int NG = TI * TJ * 4;      // 16-byte partial groups a thread
+  static constexpr int AB = 128 * kRB;        // A rows of a stage: 16 KiB
+  static constexpr int STAGE = AB + BN * kRB; // + B rows
+  static constexpr int NS = BN == 128 ? 4 : 5;
+  static constexpr int BI = BN / 32;          // B DMA issues per wave a stage
+  static constexpr int DMA = 4 + BI;          // DMA issues per wave a stage
+  static constexpr int SLOT = 128 * BN;       // floats per partial slot
+};
+
+struct SplitParams {
+  const uint16_t *A, *B;
+  void *C;
+  float *slots;         // [tiles * splits][128 * BN]
+  uint32_t *counters;   // [tiles][2] arrived, published; zero between launches
+  int M, N, K, ldc, splits;
+};
+
+template <int IN_DT, int OUT_DT, bool COL_MAJOR, int BN>
+__global__ __launch_bounds__(256, 1) void skinny_split_kernel(SplitParams p) {
+  using X = SplitCfg<BN>;
+  constexpr int TI = X::TI, TJ = X::TJ, NG = X::NG, NS = X::NS;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * X::STAGE];
+  __shared__ uint32_t arrival;
+  const uint32_t wave = uniform(threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63;
+  int id = blockIdx.x;
+  if ((gridDim.x & 7) == 0)
+    id = (id & 7) * (int)(gridDim.x >> 3) + (id >> 3);
+  const int tile = id / p.splits, split = id - tile * p.splits;
+  const int n0 = tile * BN;
+  const int nk = p.K / kBK;
+  const int q = nk / p.splits, rem = nk - q * p.splits;
+  const int k0 = split * q + min(split, rem), len = q + (split < rem ? 1 : 0);
+  const uint32_t rowbytes = (uint32_t)p.K * 2u;
+
+  // DMA issue i of a stage: local rows 32*wave + 8i .. +7 of A (i < 4),
+  // then of B (i < BI; B rows 8 * (BI * wave + i) ..), 8 lanes a row,
+  // 16-byte chunks XOR-swizzled by row.
+  uint32_t goa[4], gob[X::BI], lb[X::BI];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t R = wave * 32 + i * 8 + (lane >> 3);
+    goa[i] = (uint32_t)min((int)R, p.M - 1) * rowbytes + (((lane & 7) ^ sw8(R)) << 4);
+  }
+#pragma unroll
+  for (int i = 0; i < X::BI; ++i) {
+    const uint32_t R = (wave * X::BI + i) * 8 + (lane >> 3);
+    gob[i] = (uint32_t)min(n0 + (int)R, p.N - 1) * rowbytes + (((lane & 7) ^ sw8(R)) << 4);
+    lb[i] = X::AB + (wave * X::BI + i) * 1024;
+  }
+  const uint32_t ring = lds_addr(smem);
+  auto issue = [&](int s, int kt) {
+    const uint32_t l = ring + s * X::STAGE;
+    const char *ab = reinterpret_cast<const char *>(p.A) + (size_t)kt * kRB;
+    const char *bb = reinterpret_cast<const char *>(p.B) + (size_t)kt * kRB;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma16(l + wave * 4096 + i * 1024, ab, goa[i]);
+#pragma unroll
+    for (int i = 0; i < X::BI; ++i)
+      dma16(l + lb[i], bb, gob[i]);
+  };
+
+  const uint32_t wm = wave / X::WN, wn = wave % X::WN;
+  const uint32_t rr = lane & 31, h = lane >> 5;
+  constexpr int RM = 128 / X::WM, RN = BN / X::WN;  // rows / columns of a wave's block
+  uint32_t offa[TI], swa[TI], offb[TJ], swb[TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i) {
+    const uint32_t ra = wm * RM + i * 32 + rr;
+    offa[i] = ra * kRB;
+    swa[i] = sw8(ra) ^ h;
+  }
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const uint32_t rb = wn * RN + j * 32 + rr;
+    offb[j] = X::AB + rb * kRB;
+    swb[j] = sw8(rb) ^ h;
+  }
+  // Waves whose rows all lie past M skip their MFMAs (they still carry
+  // their share of the DMA and the barriers).
+  const bool active = (int)(wm * RM) < p.M;
+  f32x16 acc[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+      acc[i][j] = f32x16{};
+  auto compute = [&](int s) {
+    const uint8_t *st = smem + s * X::STAGE;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const uint32_t x = 2 * kk;
+      u32x4 af[TI], bf[TJ];
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+        af[i] = *reinterpret_cast<const u32x4 *>(st + offa[i] + ((x ^ swa[i]) << 4));
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+        bf[j] = *reinterpret_cast<const u32x4 *>(st + offb[j] + ((x ^ swb[j]) << 4));
+      // Row-major C: MFMA rows = n (B), columns = m (A); column-major: swapped.
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+          acc[i][j] = COL_MAJOR ? mfma32x32x16<IN_DT>(af[i], bf[j], acc[i][j])
+                                : mfma32x32x16<IN_DT>(bf[j], af[i], acc[i][j]);
+    }
+  };
+
+  // Every iteration issues exactly one stage (the last stage is re-fetched
+  // into the free slot near the end), so the vmcnt budget stays constant:
+  // NS - 1 stages in flight after each issue.
+#pragma unroll
+  for (int s = 0; s + 1 < NS; ++s)
+    issue(s, k0 + min(s, len - 1));
+  int slot = 0;
+  for (int i = 0; i < len; ++i) {
+    vm_wait_barrier<X::DMA * (NS - 2)>();
+    issue(slot == 0 ? NS - 1 : slot - 1, k0 + min(i + NS - 1, len - 1));
+    if (active)
+      compute(slot);
+    slot = slot == NS - 1 ? 0 : slot + 1;
+  }
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+
+  // 16-byte group g2 (0 .. NG-1) of the thread's partial: MFMA tile
+  // (i, j) = (g2 / (4 TJ), g2 / 4 % TJ), accumulator registers
+  // 4*(g2 % 4) .. +3.
+  auto group = [&](int g2) {
+    const f32x16 &a = acc[g2 / (4 * TJ)][(g2 / 4) % TJ];
+    const int g = g2 & 3;
+    return f32x4{a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]};
+  };
+  f32x4 out[NG];
+  if (p.splits > 1) {
+    // Arrival ticket first: the last of the tile's contributors to finish
+    // its K range reduces and never publishes its own partial; the others
+    // publish and then count themselves published with a release.
+    if (threadIdx.x == 0)
+      arrival = __hip_atomic_fetch_add(&p.counters[2 * tile], 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (arrival != (uint32_t)p.splits - 1) {
+      // Device-scope (sc1) stores: written through to the device's
+      // coherence point, so the release below has no dirty L2 lines of
+      // them to write back (35.4 against 37.4 us at 128 x 8192 x 8192).
+      const __amdgpu_buffer_rsrc_t mine = __builtin_amdgcn_make_buffer_rsrc(
+          p.slots + (size_t)id * X::SLOT, 0, X::SLOT * 4, 0x00020000);
+#pragma unroll
+      for (int g2 = 0; g2 < NG; ++g2)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, group(g2)), mine,
+                                               (g2 * 256 + threadIdx.x) * 16, 0, kScopeDevice);
+      // Every wave's partial stores are acknowledged before the barrier;
+      // thread 0's agent-scope release then publishes all of them.
+      vm_wait_barrier();
+      if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(&p.counters[2 * tile + 1], 1u, __ATOMIC_RELEASE,
+                               __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    // Last arriver: every other contributor has taken its ticket, so it is
+    // resident and finishes its publish without waiting on anything; the
+    // wait below ends once the last of them has.  Both counters then go
+    // back to zero for the next launch (ordered after this one by the
+    // kernel boundary; no contributor touches them again in this one).
+    if (threadIdx.x == 0) {
+      while (__hip_atomic_load(&p.counters[2 * tile + 1], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT) != (uint32_t)p.splits - 1)
+        __builtin_amdgcn_s_sleep(1);
+      __hip_atomic_store(&p.counters[2 * tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&p.counters[2 * tile + 1], 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    // Synchronises with the release of every published count (one release
+    // sequence on the counter).
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // The other contributors' partials, all loads in flight at once: other
+    // o (0 .. splits-2) is split o + (o >= split).
+    const f32x4 *base =
+        reinterpret_cast<const f32x4 *>(p.slots + (size_t)tile * p.splits * X::SLOT) + threadIdx.x;
+    f32x4 x[kXMaxSplits - 1][NG];
+#pragma unroll
+    for (int o = 0; o < kXMaxSplits - 1; ++o) {
+      if (o + 1 < p.splits) {
+        const int c = o + (o >= split ? 1 : 0);
+#pragma unroll
+        for (int g2 = 0; g2 < NG; ++g2)
+          x[o][g2] = __builtin_nontemporal_load(base + (size_t)c * (X::SLOT / 4) + g2 * 256);
+      }
+    }
+    // Sum in split order; contributor c is this CTA's own (c == split) or
+    // other c - (c > split).
+#pragma unroll
+    for (int g2 = 0; g2 < NG; ++g2) {
+      const f32x4 own = group(g2);
+      f32x4 s = split == 0 ? own : x[0][g2];
+#pragma unroll
+      for (int c = 1; c < kXMaxSplits; ++c) {
+        if (c < p.splits) {
+          const int lo = c < kXMaxSplits - 1 ? c : kXMaxSplits - 2;  // constant once unrolled
+          const f32x4 v = c == split ? own : (c < split ? x[lo][g2] : x[c - 1][g2]);
+          s += v;
+        }
+      }
+      out[g2] = s;
+    }
+  } else {
+#pragma unroll
+    for (int g2 = 0; g2 < NG; ++g2)
+      out[g2] = group(g2);
+  }
+
+  // Store: each 16-byte group holds 4 consecutive values along C's
+  // contiguous dimension.
+#pragma unroll
+  for (int g2 = 0; g2 < NG; ++g2) {
+    const int i = g2 / (4 * TJ), j = (g2 / 4) % TJ, g = g2 & 3;
+    const int e0 = 8 * g + 4 * (int)h;
+    // Row-major: n = n0 + RN wn + 32j + e0 .. +3 at row m = RM wm + 32i + rr;
+    // column-major: m = RM wm + 32i + e0 .. +3 at column n = n0 + RN wn + 32j + rr.
+    const int mb = (int)(wm * RM) + 32 * i, nb = n0 + (int)(wn * RN) + 32 * j;
+    const int q = COL_MAJOR ? nb + (int)rr : mb + (int)rr;
+    const int pp = COL_MAJOR ? mb + e0 : nb + e0;
+    const int qext = COL_MAJOR ? p.N : p.M, pext = COL_MAJOR ? p.M : p.N;
+    if (q >= qext)
+      continue;
+    const f32x4 v = out[g2];
+    const size_t idx = (size_t)q * p.ldc + pp;
+    if (pp + 3 < pext) {
+      if constexpr (OUT_DT == kF32) {
+        *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(p.C) + idx) = v;
+      } else {
+        u32x2 w = {pack2<OUT_DT>(v[0], v[1]), pack2<OUT_DT>(v[2], v[3])};
+        *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(p.C) + idx) = w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (pp + e < pext) {
+          if constexpr (OUT_DT == kF32)
+            reinterpret_cast<float *>(p.C)[idx + e] = v[e];
+          else
+            reinterpret_cast<uint16_t *>(p.C)[idx + e] = to_bits<OUT_DT>(v[e]);
+        }
+    }
+  }
+}
+
+template <int IN, int OUT, int BN>
+hipError_t launch_split_bn(const SplitParams &p, bool cm, hipStream_t s) {
+  const int tiles = (p.N + BN - 1) / BN;
+  const dim3 grid((unsigned)(tiles * p.splits)), block(256);
+  if (cm)
+    hipLaunchKernelGGL((skinny_split_kernel<IN, OUT, true, BN>), grid, block, 0, s, p);
+  else
+    hipLaunchKernelGGL((skinny_split_kernel<IN, OUT, false, BN>), grid, block, 0, s, p);
+  return hipGetLastError();
+}
+
+template <int IN, int OUT>
+hipError_t launch_split_out(const SplitParams &p, int bn, bool cm, hipStream_t s) {
+  return bn == 128 ? launch_split_bn<IN, OUT, 128>(p, cm, s) : launch_split_bn<IN, OUT, 64>(p, cm, s);
+}
+
 } // namespace
 
 bool skinny_supported(const GemmArgs &g) {
@@ -179,6 +482,74 @@ hipError_t launch_skinny(const GemmArgs &g, hipStream_t s) {
   if (g.out_dtype == kF32) return launch_out<kBF16, kF32>(p, g.col_major, s);
   if (g.out_dtype == kF16) return launch_out<kBF16, kF16>(p, g.col_major, s);
   return launch_out<kBF16, kBF16>(p, g.col_major, s);
+}
+
+SplitPlan skinny_split_plan(int M, int N, int K, int cus) {
+  SplitPlan plan;
+  if (M > 128 || N < 1024 || K % kBK != 0 || (uint64_t)K * 2u * 128u >= (1ull << 32) ||
+      (uint64_t)N * K * 2u >= (1ull << 32))
+    return plan;
+  // 64-column blocks when they leave room for at least two splits, else
+  // 128-column ones; at most 4 splits (at least 2 when the unsplit kernel
+  // would take more than one round of CTAs), at least 8 stages a split.
+  // The split pays its partial exchange (about 12 us at 256 CUs: publish,
+  // release, acquire, reduce), so it runs only where each split keeps at
+  // least 2048 of K, and where the unsplit kernel fills one round of CUs
+  // only for M > 96 and at least 4096 of K a split.  Measured (bf16, us,
+  // unsplit / split, fill kernel included): 128 x N x 8192 with N = 1024
+  // 31.1 / 22.4, 2048 33.0 / 23.4, 4096 33.7 / 26.6, 8192 39.6 / 37.3,
+  // 16384 91.5 / 58.4; 128 x 8192 x K with K = 4096 23.1 / 25.8, 16384
+  // 88.8 / 63.4; 64 x 8192 x 8192 35.4 / 35.1; 96 x 8192 x 8192 36.2 /
+  // 36.8; 128 x 4096 x 4096 18.4 / 20.1; 128 x 24576 x 4096 64.9 / 59.6.
+  const int nk = K / kBK;
+  const int unsplit = (N + 31) / 32;  // CTAs of the unsplit kernel
+  const bool one_round = unsplit > cus / 2 && unsplit <= cus;
+  for (int bn : {64, 128}) {
+    const int tiles = (N + bn - 1) / bn;
+    int s = cus / tiles;
+    if (s > kXMaxSplits)
+      s = kXMaxSplits;
+    if (s < 2 && bn == 128 && unsplit > cus)
+      s = 2;
+    while (s > 1 && nk < 8 * s)
+      --s;
+    if (s < 2)
+      continue;
+    const int ks = K / s;
+    if (ks < 2048 || (one_round && (ks < 4096 || M <= 96)))
+      return plan;
+    plan.splits = s;
+    plan.bn = bn;
+    return plan;
+  }
+  return plan;
+}
+
+size_t skinny_split_slot_bytes(int N, const SplitPlan &plan) {
+  return (size_t)((N + plan.bn - 1) / plan.bn) * plan.splits * 128 * plan.bn * sizeof(float);
+}
+
+size_t skinny_split_counter_count(int N, const SplitPlan &plan) {
+  return 2 * (size_t)((N + plan.bn - 1) / plan.bn);  // arrived, published
+}
+
+hipError_t launch_skinny_split(const GemmArgs &g, const SplitPlan &plan, float *slots,
+                               uint32_t *counters, hipStream_t s) {
+  if (plan.splits < 1 || plan.splits > kXMaxSplits || g.K / kBK < plan.splits ||
+      (plan.bn != 128 && plan.bn != 64))
+    return hipErrorInvalidValue;
+  SplitParams p{static_cast<const uint16_t *>(g.A), static_cast<const uint16_t *>(g.B),
+                g.C, slots, counters, g.M, g.N, g.K, g.col_major ? g.M : g.N, plan.splits};
+  const bool cm = g.col_major;
+  const int bn = plan.bn;
+  if (g.in_dtype == kF16) {
+    if (g.out_dtype == kF32) return launch_split_out<kF16, kF32>(p, bn, cm, s);
+    if (g.out_dtype == kF16) return launch_split_out<kF16, kF16>(p, bn, cm, s);
+    return launch_split_out<kF16, kBF16>(p, bn, cm, s);
+  }
+  if (g.out_dtype == kF32) return launch_split_out<kBF16, kF32>(p, bn, cm, s);
+  if (g.out_dtype == kF16) return launch_split_out<kBF16, kF16>(p, bn, cm, s);
+  return launch_split_out<kBF16, kBF16>(p, bn, cm, s);
 }
 
 } // namespace gemm

@@ -10,7 +10,7 @@
 //                   [--c-type f32|f16|bf16] [--output-layout row-major|column-major]
 //                   [--streamk-workers W] [--iters N] [--warmup N] [--repeats R]
 //                   [--seed S] [--input-mode uniform|normal|bucket|rand-int|hpl|all-ones]
-//                   [--rand-int] [--hpl] [--all-ones] [--check]
+//                   [--rand-int] [--hpl] [--all-ones] [--auto] [--check]
 //   wave-bench fa   [--batch B] [--heads H] [--kv-heads H] [--sequence S]
 //                   [--dtype f16|bf16] [--causal] [--iters N] [--warmup N]
 //                   [--repeats R] [--seed S] [--check]
@@ -399,6 +399,17 @@ int run_gemm(Opts &o) {
   check_hip(hipMalloc(&C, (size_t)M * N * (out == WAVE_F32 ? 4 : 2)), "hipMalloc C");
   float *scratch = nullptr;
   uint32_t *counters = nullptr;
+  // --auto: wave_gemm_auto_launch with the workspace it asks for.
+  const bool use_auto = o.flag("--auto");
+  void *ws = nullptr;
+  size_t ws_bytes = 0;
+  if (use_auto) {
+    if (workers > 0)
+      die("--auto picks its own kernel; drop --streamk-workers");
+    check_wave(wave_gemm_auto_workspace_bytes(M, N, K, &ws_bytes), "auto workspace");
+    if (ws_bytes)
+      check_hip(hipMalloc(&ws, ws_bytes), "hipMalloc workspace");
+  }
   if (workers > 0) {
     size_t sb = 0, cb = 0;
     check_wave(wave_gemm_streamk_workspace_bytes(M, N, workers, &sb, &cb), "workspace");
@@ -407,7 +418,10 @@ int run_gemm(Opts &o) {
     check_wave(wave_gemm_streamk_workspace_reset(counters, M, N, nullptr), "reset");
   }
   auto launch = [&]() {
-    if (workers > 0)
+    if (use_auto)
+      check_wave(wave_gemm_auto_launch(A, B, C, M, N, K, in, out, layout, ws, ws_bytes, nullptr),
+                 "wave_gemm_auto_launch");
+    else if (workers > 0)
       check_wave(wave_gemm_streamk_launch(A, B, C, M, N, K, in, out, layout, scratch, counters,
                                           workers, nullptr),
                  "wave_gemm_streamk_launch");
@@ -417,7 +431,10 @@ int run_gemm(Opts &o) {
   };
   const double us = median_us(launch, iters, warmup, repeats);
   print_device();
-  std::printf("kernel: %s\n", workers > 0 ? "gfx950_f16_streamk_gemm" : "wmma_f16_matmul_tiled");
+  std::printf("kernel: %s\n", use_auto ? "wave_gemm_auto_launch"
+                              : workers > 0 ? "gfx950_f16_streamk_gemm" : "wmma_f16_matmul_tiled");
+  if (use_auto)
+    std::printf("auto_workspace_bytes: %zu\n", ws_bytes);
   std::printf("shape: m=%d n=%d k=%d input_type=%s c_type=%s output_layout=%s\n", M, N, K,
               o.str("--input-type", "f16").c_str(), o.str("--c-type", "f16").c_str(), lay.c_str());
   if (workers > 0)
@@ -484,6 +501,8 @@ int run_gemm(Opts &o) {
     (void)hipFree(scratch);
     (void)hipFree(counters);
   }
+  if (ws)
+    (void)hipFree(ws);
   (void)hipFree(A);
   (void)hipFree(B);
   (void)hipFree(C);

@@ -430,7 +430,11 @@ int wave_gemm_auto_workspace_bytes(int M, int N, int K, size_t *bytes) {
   if (st != WAVE_OK)
     return st;
   const int workers = auto_workers(M, N, K, cus);
+  const wave::gemm::SplitPlan plan = wave::gemm::skinny_split_plan(M, N, K, cus);
   *bytes = 0;
+  if (plan.splits > 0)
+    *bytes = wave::gemm::skinny_split_slot_bytes(N, plan) +
+             wave::gemm::skinny_split_counter_count(N, plan) * sizeof(uint32_t);
   if (workers > 0) {
     size_t scratch = 0, counters = 0;
     st = streamk_sizes(M, N, workers, &scratch, &counters);
@@ -453,6 +457,38 @@ int wave_gemm_auto_launch(const void *A, const void *B, void *C, int M, int N, i
   st = device_cus(&cus);
   if (st != WAVE_OK)
     return st;
+  if (workspace && (uintptr_t)workspace % 16 != 0)
+    return fail(WAVE_ERR_INVALID, "gemm auto: workspace must be 16-byte aligned");
+  const wave::gemm::SplitPlan plan = wave::gemm::skinny_split_plan(M, N, K, cus);
+  if (plan.splits > 0) {
+    // Short M: the split-K short-M kernel when the workspace holds its
+    // partial slots and counters and the operands suit the short-M kernel;
+    // otherwise wave_gemm_launch (the unsplit short-M kernel or the tiled one).
+    const size_t slot_bytes = wave::gemm::skinny_split_slot_bytes(N, plan);
+    const size_t count = wave::gemm::skinny_split_counter_count(N, plan);
+    wave::gemm::GemmArgs g;
+    g.A = A;
+    g.B = B;
+    g.C = C;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.in_dtype = in_dtype;
+    g.out_dtype = out_dtype;
+    g.col_major = c_layout == WAVE_COL_MAJOR;
+    if (!workspace || workspace_bytes < slot_bytes + count * sizeof(uint32_t) ||
+        !wave::gemm::skinny_supported(g))
+      return wave_gemm_launch(A, B, C, M, N, K, in_dtype, out_dtype, c_layout, stream);
+    float *slots = static_cast<float *>(workspace);
+    uint32_t *counters = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + slot_bytes);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    st = hip_status(wave::gemm::zero_counters(counters, count, s),
+                    "wave_gemm_auto_launch: counter reset");
+    if (st != WAVE_OK)
+      return st;
+    return hip_status(wave::gemm::launch_skinny_split(g, plan, slots, counters, s),
+                      "wave_gemm_auto_launch (split-K short-M)");
+  }
   const int workers = auto_workers(M, N, K, cus);
   size_t scratch = 0, counter_bytes = 0;
   if (workers > 0) {

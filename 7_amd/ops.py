@@ -87,8 +87,9 @@ def gemm_auto(a: torch.Tensor, b: torch.Tensor, *, out_dtype="f16", layout: str 
               workspace: torch.Tensor | None = None,
               out: torch.Tensor | None = None) -> torch.Tensor:
     """C = A . B^T through the shape-driven dispatch (wave_gemm_auto_launch):
-    Stream-K when the 256x256 tiles would leave half the CUs idle, else the tiled
-    kernel.  workspace: a device byte tensor of at least
+    for M <= 128 the short-M kernel, split over K when its 128-column blocks
+    would leave CUs idle; otherwise Stream-K when the 256x256 tiles would leave
+    half the CUs idle, else the tiled kernel.  workspace: a device byte tensor of at least
     gemm_auto_workspace_bytes(M, N, K) bytes (allocated here when None)."""
     M, N, K = _gemm_operands(a, b)
     if layout not in ("row", "col"):

@@ -298,6 +298,20 @@ def config_lines(wave, torch, dev, steps, warmup):
             gbs = nbytes / (ms * 1e-3) / 1e9
             line.update({"gbps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                          "algorithmic_bytes": int(nbytes)})
+        if name == "3a":  # short M: the auto dispatch's split-K short-M kernel
+            ws = torch.empty(max(wave.gemm_auto_workspace_bytes(M, N, K), 1), dtype=torch.uint8,
+                             device=dev)
+            ams = time_launches(lambda: wave.gemm_auto(a, b, out_dtype=torch.bfloat16,
+                                                       workspace=ws, out=c), steps, warmup,
+                                torch)
+            atf = fl / (ams * 1e-3) / 1e12
+            gbs = nbytes / (ams * 1e-3) / 1e9
+            line.update({"value": round(atf, 2), "ms_per_step": round(ams, 4),
+                         "frac_of_mfma_peak": round(atf / MFMA_PEAK_TFLOPS, 4),
+                         "gbps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                         "kernel": "wave_gemm_auto_launch (split-K short-M, 4 K splits of "
+                                   "128-column blocks, + counter fill)",
+                         "unsplit_kernel_value": round(tf, 2)})
         if name == "3c":  # fewer 256x256 tiles (128) than CUs: the auto dispatch's Stream-K
             ws = torch.empty(max(wave.gemm_auto_workspace_bytes(M, N, K), 1), dtype=torch.uint8,
                              device=dev)

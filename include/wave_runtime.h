@@ -145,15 +145,18 @@ int wave_gemm_streamk_counters_check(const uint32_t *counters, int M, int N,
  * No kernel symbol of the reference: the reference's harness picks its
  * tiled or Stream-K kernel per run (tools/wave-matmul-calibrate/
  * wave-matmul-perf-sweep.py:151-326 kernel matrix).  This entry point picks
- * for the caller: the tiled kernel (or the short-M kernel for M <= 128), or
- * Stream-K with 2 * tiles workers when the 256x256 output tiles would leave
+ * for the caller: the tiled kernel (or, for M <= 128, the short-M kernel,
+ * split over K into 2 to 4 ranges of 128-column blocks when N / 128 leaves
+ * CUs idle: fp32 partials reduced in the launch by each block's last
+ * arriver), or Stream-K with 2 * tiles workers when the 256x256 output tiles would leave
  * at least half the CUs idle (tiles <= CUs / 2) and K >= 4096 (K >= 8192
  * at exactly CUs / 2 tiles); with at most CUs / 4 tiles,
  * max(2 * tiles, min(tiles * (K / 2048), CUs / 2)) workers.  Stream-K
- * takes its workspace from `workspace` (caller-owned device memory of
- * wave_gemm_auto_workspace_bytes(M, N, K) bytes, 0 when the shape takes
- * the tiled path; no initialisation needed, each launch zeroes the counters
- * it uses with a fill kernel); with a smaller workspace the tiled kernel
+ * and the split short-M kernel take their workspace from `workspace`
+ * (caller-owned, 16-byte aligned device memory of
+ * wave_gemm_auto_workspace_bytes(M, N, K) bytes, 0 when the shape takes an
+ * unsplit path; no initialisation needed, each launch zeroes the counters
+ * it uses with a fill kernel); with a smaller workspace the unsplit kernel
  * runs.  One launch in flight per workspace.  Same C as wave_gemm_launch
  * (c_layout row- or column-major). */
 int wave_gemm_auto_workspace_bytes(int M, int N, int K, size_t *bytes);

@@ -153,11 +153,43 @@ def auto_workers(M, N, K, cus):
     return min(w, t * -(-K // 64))
 
 
+def short_m_plan(M, N, K, cus):
+    """(column block, K splits) of the split short-M kernel
+    wave_gemm_auto_launch picks for (M, N, K), (0, 0) for none; the rules of
+    skinny_split_plan in 7_amd/csrc/gemm_skinny.hip: 64-column blocks when
+    CUs / blocks >= 2, else 128-column ones (2 splits at least when the
+    unsplit kernel's N / 32 CTAs exceed the CUs); at most 4 splits, at least
+    8 stages of 64 a split; none when a split keeps less than 2048 of K, or
+    when the unsplit kernel fills one round of CUs and M <= 96 or a split
+    keeps less than 4096 of K."""
+    if M > 128 or N < 1024 or K % 64 or K * 2 * 128 >= 2**32 or N * K * 2 >= 2**32:
+        return 0, 0
+    unsplit = -(-N // 32)
+    one_round = cus // 2 < unsplit <= cus
+    for bn in (64, 128):
+        s = min(cus // -(-N // bn), 4)
+        if s < 2 and bn == 128 and unsplit > cus:
+            s = 2
+        while s > 1 and K // 64 < 8 * s:
+            s -= 1
+        if s < 2:
+            continue
+        ks = K // s
+        if ks < 2048 or (one_round and (ks < 4096 or M <= 96)):
+            return 0, 0
+        return bn, s
+    return 0, 0
+
+
 def device_cus(dev):
     return torch.cuda.get_device_properties(dev).multi_processor_count
 
 
 def expected_workspace(wave, M, N, K, dev):
+    bn, s = short_m_plan(M, N, K, device_cus(dev))
+    if s:
+        tiles = -(-N // bn)
+        return 0, tiles * s * 128 * bn * 4 + tiles * 8
     w = auto_workers(M, N, K, device_cus(dev))
     if w == 0:
         return 0, 0
@@ -175,7 +207,8 @@ def expected_workspace(wave, M, N, K, dev):
                                    (4096, 4096, 512),    # 256 tiles
                                    (3072, 3072, 8192),   # 144 tiles: uneven split
                                    (4096, 2048, 4096),   # 128 tiles, K 4096
-                                   (128, 1024, 8192)])   # short-M kernel
+                                   (128, 1024, 8192),    # split short-M kernel
+                                   (128, 1024, 192)])    # unsplit short-M kernel
 def test_auto_dispatch_matches_tiled(wave, oracle, dev, shape):
     """The workspace size names the worker count the dispatch picks (checked
     against the rules for this device's CU count).  Bucket inputs make every
@@ -239,6 +272,99 @@ def test_config3c_auto_dispatch(wave, oracle, dev):
     if w:
         sb, _ = wave.streamk_workspace_bytes(M, N, w)
         assert int(ws[sb:].count_nonzero()) == 0
+
+
+# ---- split short-M kernel (wave_gemm_auto_launch, M <= 128) ---------------------
+def test_config3a_auto_dispatch(wave, oracle, dev):
+    """BASELINE config 3a (128 x 8192 x 8192 bf16) through
+    wave_gemm_auto_launch, the path bench.py reports for it: 128 column
+    blocks of 64, K split in 2 on 256 CUs, partials reduced by each block's
+    last arriver.
+    * N(0,1)/sqrt(K) inputs: every row within 2e-3 * sqrt(K) of the oracle;
+    * bucket inputs: bit-identical to wave_gemm_launch (the unsplit short-M
+      kernel), on a dirty workspace, twice, with the counters back at zero."""
+    M, N, K = 128, 8192, 8192
+    cus = device_cus(dev)
+    bn, s = short_m_plan(M, N, K, cus)
+    need = wave.gemm_auto_workspace_bytes(M, N, K)
+    assert need == expected_workspace(wave, M, N, K, dev)[1]
+    if cus == 256:
+        assert (bn, s) == (64, 2)
+    g = torch.Generator(device="cpu").manual_seed(37)
+    a = (torch.randn((M, K), generator=g) / np.sqrt(K)).to(torch.bfloat16)
+    b = (torch.randn((N, K), generator=g) / np.sqrt(K)).to(torch.bfloat16)
+    ws = torch.full((max(need, 1),), 0xFF, dtype=torch.uint8, device=dev)
+    c = wave.gemm_auto(a.to(dev), b.to(dev), out_dtype=torch.bfloat16, workspace=ws)
+    torch.cuda.synchronize()
+    abits = a.view(torch.int16).numpy().view(np.uint16)
+    bbits = b.view(torch.int16).numpy().view(np.uint16)
+    ref = oracle.gemm_nt_rows_bt(abits, oracle.gemm_prepare_bt(bbits, 2), 0, M, 2)
+    worst = float(np.abs(c.float().cpu().numpy() - ref).max())
+    assert worst <= 2e-3 * np.sqrt(K), worst
+    a = oracle.gemm_inputs(M, K, 2, 5, 0)
+    b = oracle.gemm_inputs(N, K, 2, 5, 1)
+    A, B = to_dev(a, torch.bfloat16, dev), to_dev(b, torch.bfloat16, dev)
+    ref = wave.gemm(A, B, out_dtype=torch.bfloat16)
+    ws.fill_(0xFF)
+    for _ in range(2):
+        got = wave.gemm_auto(A, B, out_dtype=torch.bfloat16, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref)
+    if s:
+        tiles = -(-N // bn)
+        assert int(ws[tiles * s * 128 * bn * 4:].count_nonzero()) == 0
+
+
+@pytest.mark.parametrize("in_dt", [1, 2])
+@pytest.mark.parametrize("out_dt,layout", [(torch.float32, "row"), (torch.float16, "col"),
+                                           (torch.bfloat16, "row")])
+# On 256 CUs: M from 1 to 128 (waves with no rows skip their MFMAs), N
+# ragged against the column block, K splits of unequal length (131 stages
+# in 4 splits), 64-column blocks in 4, 3 and 2 splits (N 1500, 5000, 8192)
+# and 128-column blocks in 2 (N 11000, 16384, and 24576: 384 CTAs, two
+# rounds); 128 x 4096 x 4096 takes the unsplit kernel (1024 of K a split).
+@pytest.mark.parametrize("shape", [(1, 1024, 8192), (33, 1500, 8384), (100, 8192, 8192),
+                                   (100, 11000, 4096), (128, 16384, 4096), (128, 4096, 8192),
+                                   (100, 5000, 12288), (128, 24576, 4096), (128, 4096, 4096)])
+def test_split_short_m_matches_unsplit(wave, oracle, dev, in_dt, out_dt, layout, shape):
+    """Bucket inputs make every fp32 sum exact, so the split short-M kernel
+    equals the unsplit one (wave_gemm_launch) bit for bit, on a dirty
+    workspace, twice in a row."""
+    M, N, K = shape
+    need = wave.gemm_auto_workspace_bytes(M, N, K)
+    assert need == expected_workspace(wave, M, N, K, dev)[1]
+    a = oracle.gemm_inputs(M, K, in_dt, 7, 0)
+    b = oracle.gemm_inputs(N, K, in_dt, 7, 1)
+    A, B = to_dev(a, TDT[in_dt], dev), to_dev(b, TDT[in_dt], dev)
+    ref = wave.gemm(A, B, out_dtype=out_dt, layout=layout)
+    ws = torch.full((max(need, 1),), 0xFF, dtype=torch.uint8, device=dev)
+    for _ in range(2):
+        got = wave.gemm_auto(A, B, out_dtype=out_dt, layout=layout, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref)
+
+
+def test_split_short_m_float_inputs_same_bits(wave, oracle, dev):
+    """Inexact inputs, fp32 C: the last arriver sums the partials in split
+    order whichever arrives last, so every launch gives the same bits, within
+    2e-3 * sqrt(K) of the oracle."""
+    M, N, K = 96, 4096, 8192
+    g = torch.Generator(device="cpu").manual_seed(41)
+    a = (torch.randn((M, K), generator=g) / np.sqrt(K)).to(torch.float16)
+    b = (torch.randn((N, K), generator=g) / np.sqrt(K)).to(torch.float16)
+    A, B = a.to(dev), b.to(dev)
+    ws = torch.empty((max(wave.gemm_auto_workspace_bytes(M, N, K), 1),), dtype=torch.uint8,
+                     device=dev)
+    first = wave.gemm_auto(A, B, out_dtype=torch.float32, workspace=ws)
+    out = torch.empty_like(first)
+    for _ in range(20):
+        wave.gemm_auto(A, B, out_dtype=torch.float32, workspace=ws, out=out)
+        torch.cuda.synchronize()
+        assert torch.equal(out, first)
+    abits = a.view(torch.int16).numpy().view(np.uint16)
+    bbits = b.view(torch.int16).numpy().view(np.uint16)
+    ref = oracle.gemm_nt_rows_bt(abits, oracle.gemm_prepare_bt(bbits, 1), 0, M, 1)
+    assert float(np.abs(first.cpu().numpy() - ref).max()) <= 2e-3 * np.sqrt(K)
 
 
 @pytest.mark.parametrize("shape,workers", [((1024, 1024, 8192), 64),    # 4 contributors
