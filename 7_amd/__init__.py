@@ -11,9 +11,9 @@ the reference's kernel symbols, one shape each) with hipModuleLoad.
 
 from . import code_object, runtime
 from .ops import (StreamKWorkspace, flash_attention, flash_attention_bwd,
-                  flash_attention_f32, flash_attention_lse, gemm, gemm_auto,
-                  gemm_auto_workspace_bytes, gemm_mxfp4, gemm_streamk, gemm_tile_packed,
-                  streamk_workspace_bytes)
+                  flash_attention_f32, flash_attention_lse, flash_attention_mxfp8, gemm,
+                  gemm_auto, gemm_auto_workspace_bytes, gemm_mxfp4, gemm_streamk,
+                  gemm_tile_packed, mxfp8_quantize, streamk_workspace_bytes)
 from .runtime import WaveError
 
 __all__ = [
@@ -21,5 +21,6 @@ __all__ = [
     "gemm_tile_packed", "gemm_mxfp4", "gemm_streamk",
     "StreamKWorkspace", "streamk_workspace_bytes",
     "flash_attention", "flash_attention_lse", "flash_attention_bwd", "flash_attention_f32",
+    "flash_attention_mxfp8", "mxfp8_quantize",
     "WaveError",
 ]

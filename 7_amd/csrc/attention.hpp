@@ -40,6 +40,22 @@ struct BwdArgs {
 };
 hipError_t launch_bwd(const BwdArgs &args, hipStream_t stream);
 
+// Block-scaled FP8 forward (attention_fwd8.hip): Q, K, V e4m3 bytes in the
+// FwdArgs layouts (head_dim 128), e8m0 scales Q_scale [batch][q_heads][seq_q]
+// [4] and K_scale [batch][kv_heads][seq_k][4] (blocks of 32 d), V_scale
+// [batch][kv_heads][ceil(seq_k / 32)][128] (blocks of 32 keys); O f16 / bf16.
+struct Fp8FwdArgs {
+  const void *Q = nullptr, *K = nullptr, *V = nullptr;
+  const void *Q_scale = nullptr, *K_scale = nullptr, *V_scale = nullptr;
+  void *O = nullptr;
+  int batch = 1, q_heads = 1, kv_heads = 1, seq_q = 0, seq_k = 0;
+  int out_dtype = 1;        // wave::kF16 or wave::kBF16
+  int causal = 0;
+  float scale = 0.f;        // 0 selects 1/sqrt(128)
+  float *lse = nullptr;
+};
+hipError_t launch_fwd_fp8(const Fp8FwdArgs &args, hipStream_t stream);
+
 // flash_attention_f32 ABI: Q [block_m][head_dim] f16 already multiplied by
 // log2(e)/sqrt(head_dim), K/V [seq_n][head_dim] f16, O [block_m][head_dim]
 // f32 = sum_n 2^(s_n - max) V_n / sum_n 2^(s_n - max), s_n = Q.K_n.

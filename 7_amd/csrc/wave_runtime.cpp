@@ -700,6 +700,58 @@ int wave_fa_fwd_config_launch(const void *Q, const void *K, const void *V, void 
                 qk_max_abs, waves, stream, "wave_fa_fwd_config_launch");
 }
 
+int wave_fa_fwd_mxfp8_launch(const void *Q, const void *Q_scale, const void *K,
+                             const void *K_scale, const void *V, const void *V_scale, void *O,
+                             float *lse, int batch, int q_heads, int kv_heads, int seq,
+                             int head_dim, int out_dtype, int causal, float scale,
+                             void *stream) {
+  if (!Q || !K || !V || !O || !Q_scale || !K_scale || !V_scale)
+    return fail(WAVE_ERR_INVALID, "fa mxfp8: null Q, K, V, O or scale pointer");
+  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || seq <= 0)
+    return fail(WAVE_ERR_INVALID,
+                "fa mxfp8: batch=%d q_heads=%d kv_heads=%d seq=%d must be positive", batch,
+                q_heads, kv_heads, seq);
+  if (q_heads % kv_heads != 0)
+    return fail(WAVE_ERR_INVALID, "fa mxfp8: q_heads=%d not a multiple of kv_heads=%d",
+                q_heads, kv_heads);
+  if (out_dtype != WAVE_F16 && out_dtype != WAVE_BF16)
+    return fail(WAVE_ERR_INVALID, "fa mxfp8: out_dtype %d is not f16/bf16", out_dtype);
+  if (causal != 0 && causal != 1)
+    return fail(WAVE_ERR_INVALID, "fa mxfp8: causal=%d must be 0 or 1", causal);
+  if (!(scale >= 0.f) || scale != scale)
+    return fail(WAVE_ERR_INVALID, "fa mxfp8: scale must be >= 0");
+  if (head_dim != 128)
+    return fail(WAVE_ERR_UNSUPPORTED, "fa mxfp8: head_dim=%d (only 128 is built)", head_dim);
+  // Per-head buffer resources hold seq * 128 bytes in 32 bits.
+  if ((int64_t)batch * q_heads * ((seq + 255) / 256) > INT32_MAX || seq >= (1 << 24))
+    return fail(WAVE_ERR_UNSUPPORTED, "fa mxfp8: problem too large");
+  if ((reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(K) |
+       reinterpret_cast<uintptr_t>(V) | reinterpret_cast<uintptr_t>(O)) & 15)
+    return fail(WAVE_ERR_INVALID, "fa mxfp8: Q, K, V and O must be 16-byte aligned");
+  if ((reinterpret_cast<uintptr_t>(Q_scale) | reinterpret_cast<uintptr_t>(K_scale) |
+       reinterpret_cast<uintptr_t>(lse)) & 3)
+    return fail(WAVE_ERR_INVALID, "fa mxfp8: Q_scale, K_scale and lse must be 4-byte aligned");
+  wave::attention::Fp8FwdArgs a;
+  a.Q = Q;
+  a.K = K;
+  a.V = V;
+  a.Q_scale = Q_scale;
+  a.K_scale = K_scale;
+  a.V_scale = V_scale;
+  a.O = O;
+  a.batch = batch;
+  a.q_heads = q_heads;
+  a.kv_heads = kv_heads;
+  a.seq_q = seq;
+  a.seq_k = seq;
+  a.out_dtype = out_dtype;
+  a.causal = causal;
+  a.scale = scale;
+  a.lse = lse;
+  return hip_status(wave::attention::launch_fwd_fp8(a, static_cast<hipStream_t>(stream)),
+                    "wave_fa_fwd_mxfp8_launch");
+}
+
 int wave_fa_f32_launch(const void *Q, const void *K, const void *V, float *O,
                        int block_m, int seq_n, int head_dim, void *stream) {
   if (!Q || !K || !V || !O)

@@ -265,6 +265,72 @@ def _fa_shapes(q, k, v):
     return B, Hq, k.shape[1], S, D
 
 
+def mxfp8_quantize(x: torch.Tensor, dim: int = -1) -> tuple[torch.Tensor, torch.Tensor]:
+    """OCP MX-FP8 encoding of x along `dim` (its size a multiple of 32, or
+    padded with zeros to one): blocks of 32 elements share the e8m0 scale
+    2^(floor(log2(amax)) - 8) (the OCP MX rule for e4m3, whose largest
+    exponent is 8), and each element is x / scale rounded to e4m3, saturated at
+    +-448.  Returns (e4m3 bytes as uint8, x's shape; e8m0 bytes as uint8, x's
+    shape with `dim` divided by 32, rounded up)."""
+    dim = dim % x.dim()
+    xs = x.float().movedim(dim, -1)
+    n = xs.shape[-1]
+    nb = -(-n // 32)
+    if nb * 32 != n:
+        xs = torch.nn.functional.pad(xs, (0, nb * 32 - n))
+    blocks = xs.reshape(*xs.shape[:-1], nb, 32)
+    amax = blocks.abs().amax(dim=-1)
+    e = torch.where(amax > 0, torch.floor(torch.log2(amax)) - 8, torch.full_like(amax, -127))
+    e = e.clamp(-127, 127)
+    q = (blocks / torch.exp2(e).unsqueeze(-1)).clamp(-448.0, 448.0)
+    elems = q.to(torch.float8_e4m3fn).view(torch.uint8).reshape(*xs.shape)[..., :n]
+    scales = (e + 127).to(torch.uint8)
+    return elems.movedim(-1, dim).contiguous(), scales.movedim(-1, dim).contiguous()
+
+
+def flash_attention_mxfp8(q: torch.Tensor, q_scale: torch.Tensor, k: torch.Tensor,
+                          k_scale: torch.Tensor, v: torch.Tensor, v_scale: torch.Tensor, *,
+                          causal: bool = False, scale: float | None = None, out_dtype="f16",
+                          out: torch.Tensor | None = None, lse: torch.Tensor | None = None
+                          ) -> torch.Tensor:
+    """softmax(Q K^T * scale) V of block-scaled FP8 inputs
+    (wave_fa_fwd_mxfp8_launch): q [B, Hq, S, 128], k / v [B, Hkv, S, 128]
+    e4m3 bytes (uint8 or float8_e4m3fn); q_scale [B, Hq, S, 4], k_scale
+    [B, Hkv, S, 4] and v_scale [B, Hkv, ceil(S/32), 128] e8m0 bytes, as
+    mxfp8_quantize(q), mxfp8_quantize(k) and mxfp8_quantize(v, dim=2) return
+    them.  lse: an optional float32 [B, Hq, S] output."""
+    def raw(t, name):
+        _need(t, name, q.device)
+        if t.dtype == torch.float8_e4m3fn:
+            t = t.view(torch.uint8)
+        if t.dtype != torch.uint8:
+            raise ValueError(f"{name} must be uint8 (e4m3 / e8m0 bytes)")
+        return t
+    q, k, v = raw(q, "q"), raw(k, "k"), raw(v, "v")
+    qs, ks, vs = raw(q_scale, "q_scale"), raw(k_scale, "k_scale"), raw(v_scale, "v_scale")
+    if q.dim() != 4 or k.dim() != 4 or k.shape != v.shape:
+        raise ValueError("q must be [B, Hq, S, 128] and k, v [B, Hkv, S, 128]")
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    if k.shape[0] != B or k.shape[2] != S or k.shape[3] != D:
+        raise ValueError("k and v must be [batch, kv_heads, seq, head_dim]")
+    if (qs.shape != (B, Hq, S, D // 32) or ks.shape != (B, Hkv, S, D // 32)
+            or vs.shape != (B, Hkv, -(-S // 32), D)):
+        raise ValueError("scales must be [B, Hq, S, D/32], [B, Hkv, S, D/32] and "
+                         "[B, Hkv, ceil(S/32), D]")
+    odt = _dtype(out_dtype)
+    out = _out(out, (B, Hq, S, D), odt, q.device)
+    if lse is not None:
+        _need(lse, "lse", q.device)
+        if lse.dtype != torch.float32 or lse.shape != (B, Hq, S):
+            raise ValueError("lse must be float32 [B, Hq, S]")
+    rt.check(rt.lib().wave_fa_fwd_mxfp8_launch(
+        q.data_ptr(), qs.data_ptr(), k.data_ptr(), ks.data_ptr(), v.data_ptr(), vs.data_ptr(),
+        out.data_ptr(), lse.data_ptr() if lse is not None else None, B, Hq, Hkv, S, D,
+        _DT[odt], int(causal), float(scale or 0.0), _stream(q)))
+    return out
+
+
 def flash_attention_lse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
                         causal: bool = False, scale: float | None = None
                         ) -> tuple[torch.Tensor, torch.Tensor]:

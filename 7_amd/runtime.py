@@ -45,6 +45,8 @@ _SIGNATURES = {
                                        _P]),
     "wave_fa_f32_launch": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     "wave_fa_fwd_lse_launch": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P]),
+    "wave_fa_fwd_mxfp8_launch": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
+                                      _I, _F, _P]),
     "wave_fa_bwd_launch": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,
                                 _I, _I, _F, _P]),
     "wave_status_string": (ctypes.c_char_p, [_I]),

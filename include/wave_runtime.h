@@ -249,6 +249,29 @@ int wave_fa_fwd_lse_launch(const void *Q, const void *K, const void *V, void *O,
                            int batch, int q_heads, int kv_heads, int seq, int head_dim,
                            int dtype, int causal, float scale, void *stream);
 
+/* ---- block-scaled FP8 flash-attention forward ----------------------------
+ * O = softmax(scale * Qd Kd^T) Vd, where Qd, Kd, Vd are OCP MX-FP8 inputs
+ * decoded: e4m3 bytes times 2^(e - 127) of their e8m0 block scale, one scale
+ * per 32 elements along the dimension each product contracts.
+ *   Q [batch][q_heads][seq][128], Q_scale [batch][q_heads][seq][4]   (d blocks)
+ *   K [batch][kv_heads][seq][128], K_scale [batch][kv_heads][seq][4] (d blocks)
+ *   V [batch][kv_heads][seq][128], V_scale [batch][kv_heads][ceil(seq/32)][128]
+ *                                                              (key blocks)
+ * O [batch][q_heads][seq][128] in out_dtype (f16 or bf16).  The
+ * probabilities are rounded to e4m3 for the PV product (as 2^4 times the
+ * probability, at most 2^8, after the running max); fp32 accumulation, fp32
+ * row sums.  causal, GQA, scale (<= 0: 1/sqrt(128)) and the optional lse
+ * output (nullptr for none) as wave_fa_fwd_lse_launch.  Q, K, V, O 16-byte
+ * aligned, Q_scale and K_scale 4-byte aligned; head_dim must be 128.  No
+ * kernel of the reference: its FA notes name a block-scaled FP8 attention
+ * contract as the next step (docs/PerfReferences/
+ * WaveGfx950FlashAttention.md:94-99). */
+int wave_fa_fwd_mxfp8_launch(const void *Q, const void *Q_scale, const void *K,
+                             const void *K_scale, const void *V, const void *V_scale,
+                             void *O, float *lse, int batch, int q_heads, int kv_heads,
+                             int seq, int head_dim, int out_dtype, int causal, float scale,
+                             void *stream);
+
 /* ---- flash-attention backward --------------------------------------------
  * dQ, dK, dV of O = softmax(scale * Q K^T) V (causal and GQA as the forward;
  * dK, dV sum over the q heads of each KV head) from dO, O and the lse of

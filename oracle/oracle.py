@@ -414,3 +414,71 @@ def fa_backward(q, k, v, do, *, scale: float | None = None, causal: bool = False
     dk = dkk.reshape(B, Hkv, g, S, D).sum(axis=2)
     dv = dvv.reshape(B, Hkv, g, S, D).sum(axis=2)
     return o, lse, dq, dk, dv
+
+
+# ---- block-scaled FP8 (OCP MX-FP8) ---------------------------------------------
+# No reference counterpart: the reference only names a block-scaled FP8 attention
+# contract as future work (docs/PerfReferences/WaveGfx950FlashAttention.md:94-99).
+# The formats are the OCP ones (OCP 8-bit Floating Point Specification, E4M3;
+# OCP Microscaling Formats (MX) v1.0, E8M0 scales over blocks of 32).  Pinned
+# in tests/test_mxfp8_oracle.py: every e4m3 code against torch's float8_e4m3fn
+# conversion, e8m0 against its closed form, and the attention against
+# attention computed by torch in float64 on the same decoded values.
+
+def _e4m3_table() -> np.ndarray:
+    t = np.empty(256, dtype=np.float64)
+    for b in range(256):
+        sign = -1.0 if b & 0x80 else 1.0
+        e = (b >> 3) & 0xF
+        m = b & 7
+        if e == 0xF and m == 7:
+            t[b] = np.nan
+        elif e == 0:
+            t[b] = sign * m * 2.0 ** -9
+        else:
+            t[b] = sign * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+    return t
+
+
+_E4M3 = _e4m3_table()
+
+
+def e4m3_to_float(b: np.ndarray) -> np.ndarray:
+    """OCP E4M3 bytes -> float64: sign, 4-bit exponent (bias 7), 3-bit
+    mantissa; exponent 0 is subnormal (m * 2^-9); 0x7F / 0xFF are NaN."""
+    return _E4M3[np.asarray(b, dtype=np.uint8)]
+
+
+def e8m0_to_float(b: np.ndarray) -> np.ndarray:
+    """E8M0 scale bytes -> 2^(b - 127) (255 is NaN)."""
+    b = np.asarray(b, dtype=np.uint8).astype(np.float64)
+    return np.where(b == 255, np.nan, np.exp2(b - 127.0))
+
+
+def mxfp8_decode(elems: np.ndarray, scales: np.ndarray, axis: int) -> np.ndarray:
+    """Decode MX-FP8: each e4m3 element times the e8m0 scale of its block of
+    32 along `axis` (scales has that axis divided by 32, rounded up)."""
+    x = e4m3_to_float(elems)
+    sc = np.repeat(e8m0_to_float(scales), 32, axis=axis)
+    sc = np.take(sc, np.arange(x.shape[axis]), axis=axis)
+    return x * sc
+
+
+def attention_forward(q, k, v, *, scale: float | None = None, causal: bool = False):
+    """Float64 softmax(scale Q K^T) V for q [B, Hq, S, D], k / v [B, Hkv, S, D]
+    (kv head = q head / (Hq / Hkv)), key > query masked when causal.  Returns
+    (o, lse) with lse = ln sum_k exp(scale q.k)."""
+    q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
+    B, Hq, S, D = q.shape
+    g = Hq // k.shape[1]
+    sc = 1.0 / np.sqrt(D) if not scale else float(scale)
+    kk = np.repeat(k, g, axis=1)
+    vv = np.repeat(v, g, axis=1)
+    s = sc * np.matmul(q, np.swapaxes(kk, -1, -2))
+    if causal:
+        s = np.where(np.triu(np.ones((S, S), dtype=bool), 1), -np.inf, s)
+    m = s.max(axis=-1, keepdims=True)
+    e = np.exp(s - m)
+    tot = e.sum(axis=-1, keepdims=True)
+    return np.matmul(e / tot, vv), (m + np.log(tot))[..., 0]
+
