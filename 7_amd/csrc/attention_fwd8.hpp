@@ -34,7 +34,8 @@
 //  * P = exp2(c s - m + 4) is at most 2^8 (the running max is raised when a
 //    tile's max exceeds it by more than 4), so it fits e4m3 (max 448) and
 //    values down to 2^-13 of the running max stay representable; the PV
-//    MFMA's B scale is the constant 2^-4.  Row sums add the fp32 P.
+//    MFMA's B scale is the constant 2^-4.  Row sums are one more MFMA a
+//    tile (a ones operand against the same e4m3 P).
 //  * V: each thread of a group loads a 4-key x 4-d block (four dwords) of its
 //    group's 64 d columns, transposes it with 8 v_perm and writes four dwords
 //    of V^T.  K: LDS DMA, 64 rows x 128 B a tile, 16-byte chunk c of row r at
@@ -244,7 +245,15 @@ __device__ __forceinline__ void fwd8_cta(const Fp8Params &p, int raw, uint8_t *s
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     o[i] = f32x16{};
-  float lsum = 0.f;
+  // Row sums of the e4m3 P on the MFMA: lacc = ones . P^T, so every
+  // accumulator register of lane l holds the sum for query l%32 (only
+  // register 0 is kept up to date through the rescales).  That takes 32
+  // VALU adds a tile out of the softmax segment and puts one MFMA into the
+  // matrix segment, which has room; the sums are then exactly those of the
+  // values that multiply V.
+  f32x16 lacc = f32x16{};
+  const i32x8 ones8 = {0x38383838, 0x38383838, 0x38383838, 0x38383838,
+                       0x38383838, 0x38383838, 0x38383838, 0x38383838};  // e4m3 1.0
   float m = -__builtin_inff();  // running max (log2 units), minus the P shift
   const float c = p.scale_log2;
   auto pin = [](auto x) { asm volatile("" ::"v"(x)); };
@@ -286,6 +295,7 @@ __device__ __forceinline__ void fwd8_cta(const Fp8Params &p, int raw, uint8_t *s
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    lacc = mfma_fp8(ones8, pf, lacc, 127u, (uint32_t)k8PScale);
   };
 
   auto mask = [&](f32x16(&sc)[2], int t) {
@@ -310,7 +320,7 @@ __device__ __forceinline__ void fwd8_cta(const Fp8Params &p, int raw, uint8_t *s
       const float mn = fmaxf(m, mx);
       const float alpha = (m == -__builtin_inff()) ? 0.f : __builtin_amdgcn_exp2f(m - mn);
       m = mn;
-      lsum *= alpha;
+      lacc[0] *= alpha;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         o[i] *= alpha;
@@ -330,7 +340,6 @@ __device__ __forceinline__ void fwd8_cta(const Fp8Params &p, int raw, uint8_t *s
     half_pair(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])), lo, hi);
     update_max(fmaxf(lo, hi) * c);
     const float mb = m - k8PShift;
-    float l0 = 0.f, l1 = 0.f;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -339,12 +348,8 @@ __device__ __forceinline__ void fwd8_cta(const Fp8Params &p, int raw, uint8_t *s
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           v[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][4 * i + e], c, -mb));
-        l0 += v[0] + v[1];
-        l1 += v[2] + v[3];
         pf[4 * j + i] = (int)pack_fp8x4(v[0], v[1], v[2], v[3]);
       }
-    lsum += l0 + l1;
-    pin(lsum);
     pin(pf);
   };
 
@@ -426,11 +431,9 @@ __device__ __forceinline__ void fwd8_cta(const Fp8Params &p, int raw, uint8_t *s
   if (grp == 0)
     lds_barrier();
 
-  // Normalise (the P shift cancels: both O and the sums carry 2^4 ... the
-  // MFMA took 2^-4 off O) and store O[my_q][d], d = 32dt + 8(r/4) + 4h + r%4.
-  float s_lo, s_hi;
-  half_pair(lsum, s_lo, s_hi);
-  const float total = (s_lo + s_hi) * (1.0f / 16.0f);
+  // Normalise (both O and the row sums took the 2^-4 off P in their MFMAs)
+  // and store O[my_q][d], d = 32dt + 8(r/4) + 4h + r%4.
+  const float total = lacc[0];
   const float inv = total > 0.f ? 1.0f / total : 0.f;
   if (p.lse != nullptr && half == 0 && my_q < p.seq_q)
     p.lse[(size_t)bh * p.seq_q + my_q] = (m + __builtin_log2f(total)) * kLn2;

@@ -38,6 +38,7 @@ sys.path.insert(0, ROOT)
 
 MFMA_PEAK_TFLOPS = 2516.6   # MI355X dense f16/bf16: 256 CU x 2.4 GHz x 4096
 FP4_PEAK_TFLOPS = 10066.3  # MI355X dense fp4 MFMA: 256 CU x 2.4 GHz x 16384
+FP8_PEAK_TFLOPS = 5033.2    # MI355X dense fp8: twice the f16 rate
 HBM_PEAK_GBS = 8000.0
 PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "gemm_f16_8192_traffic.txt")
 
@@ -268,6 +269,33 @@ def mxfp4_line(wave, torch, dev, steps, warmup):
                 "value": 4460.0, "unit": "TFLOP/s", "hardware": "gfx950",
                 "kernel": "gfx950-mxfp4-256x256-8wave, random inputs",
                 "source": "docs/Gfx950MatmulProfiles.md:57-68"}}
+
+
+def mxfp8_fa_lines(wave, torch, dev, steps, warmup):
+    """Block-scaled FP8 flash-attention forward (wave_fa_fwd_mxfp8_launch) on
+    the f16 benchmark shape B4 H32 S4096 and on the reference's FA profile
+    shape B2 H64 S8192: N(0,1) inputs quantized to MX-FP8 on the device
+    (mxfp8_quantize, outside the timing), f16 O, FLOPs 4*B*H*S^2*D."""
+    lines = []
+    g = torch.Generator(device=dev).manual_seed(19)
+    for B, H, S in ((4, 32, 4096), (2, 64, 8192)):
+        D = 128
+        q, k, v = (torch.randn((B, H, S, D), generator=g, device=dev) for _ in range(3))
+        (qe, qs), (ke, ks), (ve, vs) = (wave.mxfp8_quantize(q), wave.mxfp8_quantize(k),
+                                        wave.mxfp8_quantize(v, dim=2))
+        del q, k, v
+        o = torch.empty((B, H, S, D), dtype=torch.float16, device=dev)
+        ms = time_launches(lambda: wave.flash_attention_mxfp8(qe, qs, ke, ks, ve, vs, out=o),
+                           steps, warmup, torch)
+        tf = 4.0 * B * H * S * S * D / (ms * 1e-3) / 1e12
+        log(f"fa fwd mxfp8 B{B} H{H} S{S} D128 (f16 O): {ms * 1e3:.1f} us/launch, {tf:.1f} "
+            f"TFLOP/s ({100 * tf / FP8_PEAK_TFLOPS:.1f}% of fp8 {FP8_PEAK_TFLOPS})")
+        lines.append({"workload": f"fa_fwd_mxfp8_b{B}_h{H}_s{S}_d128_noncausal_f16out",
+                      "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+                      "frac_of_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4),
+                      "dtype": "MX-FP8 (e4m3 + e8m0 per 32) in, fp32 accumulate, f16 out"})
+        del qe, qs, ke, ks, ve, vs, o
+    return lines
 
 
 def config_lines(wave, torch, dev, steps, warmup):
@@ -520,6 +548,7 @@ def main():
                               "source": "docs/PerfReferences/WaveGfx950FlashAttention.md:67"}})
         del q, k, v, o
         secondary.append(mxfp4_line(wave, torch, dev, 20, 3))
+        secondary.extend(mxfp8_fa_lines(wave, torch, dev, 10, 2))
         secondary.extend(vendor_lines(torch, dev, a, b, max(10, args.steps // 2)))
 
     cpu = None

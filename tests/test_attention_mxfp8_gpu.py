@@ -5,16 +5,19 @@ decoded MX-FP8 inputs (oracle.mxfp8_decode + oracle.attention_forward).
 No reference counterpart: the reference names a block-scaled FP8 attention
 contract as its next FA step (docs/PerfReferences/WaveGfx950FlashAttention.md:
 94-99), so the oracle is the math of the decoded values.  The kernel rounds
-the probabilities to e4m3 before the PV product (relative error at most 2^-4,
-as 2^4 times the probability after the running max), so:
+the probabilities to e4m3 before the PV product and the row sums (relative
+error at most 2^-4 each, as 2^4 times the probability after the running max;
+O = sum P~ V / sum P~ then lies within 2 * 2^-4 relative of the exact
+weights to first order), so:
   * zero Q: every probability is exactly 2^4 in e4m3, and O is the mean of
     the decoded V rows (the unmasked ones): pinned to fp32-accumulation level
     beyond the output rounding.  This pins the V path (transpose, key order,
     V scales, lane-half swap, normalisation);
   * V rows one-hot (V[k] = e_k): O[q][k] is the probability of key k, within
-    2^-4 of it relative.  This pins the QK path (Q, K and their scales);
-  * general inputs: |O - O_ref| <= 2^-4 max|V| + output rounding, a bound the
-    P rounding cannot exceed, and the mean error below 2e-3 max|V|.
+    2 * 2^-4 of it relative.  This pins the QK path (Q, K and their scales);
+  * general inputs: |O - O_ref| <= 2 * 2^-4 max|V| + output rounding, a bound
+    the P rounding cannot exceed, and the mean error below 2e-3 max|V|; lse
+    within ln(1 + 2^-4) (the row sums are of the rounded P), mean 5e-3.
 """
 
 import numpy as np
@@ -82,9 +85,10 @@ def test_one_hot_v_shows_the_probabilities(wave, oracle, dev, causal):
     vd = decode(oracle, ve, vs, 2)
     assert np.array_equal(vd, v.numpy())
     ref, _ = oracle.attention_forward(qd, kd, vd, causal=causal)
-    # O[q][k] = P[q][k]: e4m3 rounding of 2^4 P (relative 2^-4, plus the
-    # smallest subnormal step 2^-13 of the row max) and f16 output rounding.
-    tol = 2.0 ** -4 * ref + 2.0 ** -13 + REL[1] * ref
+    # O[q][k] = P[q][k]: e4m3 rounding of 2^4 P in the numerator and in the
+    # row sum (relative 2^-4 each, plus the smallest subnormal step 2^-13 of
+    # the row max) and f16 output rounding.
+    tol = 2 * 2.0 ** -4 * ref + 2.0 ** -13 + REL[1] * ref
     assert np.all(np.abs(o - ref) <= tol), np.abs(o - ref).max()
 
 
@@ -103,10 +107,12 @@ def test_random_inputs_against_decoded_float64(wave, oracle, dev, out_dt, causal
     ref, ref_lse = oracle.attention_forward(qd, kd, vd, causal=causal)
     vmax = np.abs(vd).max()
     err = np.abs(o - ref)
-    assert err.max() <= 2.0 ** -4 * vmax + REL[out_dt] * np.abs(ref).max(), err.max()
+    assert err.max() <= 2 * 2.0 ** -4 * vmax + REL[out_dt] * np.abs(ref).max(), err.max()
     assert err.mean() <= 2e-3 * vmax, err.mean()
-    # lse sums the fp32 probabilities: float32-level agreement.
-    assert np.abs(lse - ref_lse).max() <= 1e-4 * max(1.0, np.abs(ref_lse).max())
+    dl = np.abs(lse - ref_lse)
+    # Unbiased rounding of each term (std 2^-4 / sqrt 3 relative) over a row
+    # of >= 50 effective terms: a mean of at most about 5e-3.
+    assert dl.max() <= np.log1p(2.0 ** -4) and dl.mean() <= 5e-3, (dl.max(), dl.mean())
 
 
 def test_benchmark_shape_sampled_rows(wave, oracle, dev):
@@ -131,7 +137,7 @@ def test_benchmark_shape_sampled_rows(wave, oracle, dev):
         p = np.exp(s - s.max(-1, keepdims=True))
         ref = (p / p.sum(-1, keepdims=True)) @ vd
         err = np.abs(o[b, h, rows].float().cpu().numpy() - ref)
-        assert err.max() <= 2.0 ** -4 * np.abs(vd).max(), err.max()
+        assert err.max() <= 2 * 2.0 ** -4 * np.abs(vd).max(), err.max()
         assert err.mean() <= 2e-3 * np.abs(vd).max(), err.mean()
 
 
