@@ -385,10 +385,12 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=24.0)
     ap.add_argument("--no-ref-compare", action="store_true",
                     help="skip the runs on the reference's published input modes / shapes")
-    ap.add_argument("--workload", choices=["all", "gemm", "fa", "mxfp4", "copy", "configs"],
+    ap.add_argument("--workload",
+                    choices=["all", "gemm", "fa", "mxfp4", "mxfp8fa", "copy", "configs"],
                     default="all",
-                    help="gemm / fa / mxfp4: run only that kernel (for profiler passes); copy: "
-                         "a 1 GiB device copy used to calibrate rocprofv3 byte counters")
+                    help="gemm / fa / mxfp4 / mxfp8fa: run only that kernel (for profiler "
+                         "passes); copy: a 1 GiB device copy used to calibrate rocprofv3 byte "
+                         "counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -410,11 +412,15 @@ def main():
         ms = time_launches(lambda: dst.copy_(src), args.steps, args.warmup, torch)
         log(f"copy 1 GiB: {ms:.3f} ms, {2 * 4 * src.numel() / (ms * 1e-3) / 1e9:.0f} GB/s")
         return
-    if args.workload in ("fa", "mxfp4", "configs"):
+    if args.workload in ("fa", "mxfp4", "mxfp8fa", "configs"):
         args.no_cpu = True
     if args.workload == "mxfp4":
         m = mxfp4_line(wave, torch, dev, args.steps, args.warmup)
         print(json.dumps(m), flush=True)
+        return
+    if args.workload == "mxfp8fa":
+        for m in mxfp8_fa_lines(wave, torch, dev, args.steps, args.warmup):
+            print(json.dumps(m), flush=True)
         return
 
     M = N = K = 8192
