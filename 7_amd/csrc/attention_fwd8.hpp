@@ -190,12 +190,19 @@ __device__ __forceinline__ void fwd8_cta(const Fp8Params &p, int raw, uint8_t *s
       dst[dt] = __builtin_amdgcn_raw_buffer_load_b8(vsrs, off + 32 * dt, 0, 0);
   };
 
-  // V: thread tg of group g loads keys 4kg .. 4kg+3 (kg = tg / 16) x d
-  // 64g + 4dg .. +3 (dg = tg % 16) and writes them to V^T rows d at the
-  // byte of key 4kg in the operand order: key 32j + 8i + 4h + e at byte
-  // 32h + 16j + 4i + e (kg = 8j + 2i + h).
+  // V: thread tg of group g loads keys 4kg .. 4kg+3 x d 64g + 4dg .. +3 and
+  // writes them to V^T rows d at the byte of key 4kg in the operand order:
+  // key 32j + 8i + 4h + e at byte 32h + 16j + 4i + e (kg = 8j + 2i + h).
+  // A wave covers 8 key groups x 8 dg: each load instruction reads 8 rows
+  // x 32 contiguous bytes, and each V^T store (bank = 16 (dg % 4) + a
+  // bijection of kg, at the 80-byte pitch) hits 32 distinct banks, 2-way.
+  // Measured in one process against 16 x 4 (conflict-free stores, 16-byte
+  // load segments) and 4 x 16 (64-byte segments, 4-way conflicts), TFLOP/s:
+  // B4 H32 S4096 1717 / 1486-1561 / 1530-1537, B2 H64 S8192 1616 / 1494 /
+  // 1585, causal B1 Hq64 Hkv8 S8192 1540-1546 / 1404-1464 / 1358-1371.
   const int tg = threadIdx.x & 255;
-  const int kg = tg >> 4, dg = tg & 15;
+  const int kg = (tg & 7) | (((tg >> 6) & 1) << 3);
+  const int dg = ((tg >> 3) & 7) | ((tg >> 7) << 3);
   const int vd = 64 * (int)grp + 4 * dg;
   const int vpos = 32 * (kg & 1) + 16 * (kg >> 3) + 4 * ((kg >> 1) & 3);
   uint32_t vr[4], vr1[4];
