@@ -28,19 +28,22 @@
 //  * O^T(dt) += V^T(dt) . P^T: the S^T accumulators give lane half h keys
 //    32j + 8i + 4h + 0..3 (i = 0..3) of query l%32, i.e. 16 keys of each
 //    32-key block j; packed to e4m3 (4 a dword, block j in bytes 16j ..) they
-//    are the B operand as they stand, and A = V^T row 32dt + l%32 stored with
-//    the same keys at the same bytes (key 32j + 8i + 4h + e at byte
-//    32h + 16j + 4i + e), scaled by V_scale of (key block h, d).
+//    are the B operand as they stand, and A = the same keys of V column
+//    32dt + l%32 at the same bytes (key 32j + 8i + 4h + e at byte
+//    16j + 4i + e), scaled by V_scale of (key block h, d).
 //  * P = exp2(c s - m + 4) is at most 2^8 (the running max is raised when a
 //    tile's max exceeds it by more than 4), so it fits e4m3 (max 448) and
 //    values down to 2^-13 of the running max stay representable; the PV
 //    MFMA's B scale is the constant 2^-4.  Row sums are one more MFMA a
 //    tile (a ones operand against the same e4m3 P).
-//  * V: each thread of a group loads a 4-key x 4-d block (four dwords) of its
-//    group's 64 d columns, transposes it with 8 v_perm and writes four dwords
-//    of V^T.  K: LDS DMA, 64 rows x 128 B a tile, 16-byte chunk c of row r at
-//    c ^ ((r >> 1) & 7) (rows r and r + 1 share a 256-byte bank line, so the
-//    16 rows one ds_read_b128 phase reads hit 16 distinct chunk slots).
+//  * K and V both arrive by LDS DMA in 4-tile rings, 64 rows x 128 B a tile.
+//    K: 16-byte chunk c of row r at c ^ ((r >> 1) & 7) (rows r and r + 1
+//    share a 256-byte bank line, so the 16 rows one ds_read_b128 phase reads
+//    hit 16 distinct chunk slots).  V stays row-major and the PV operand is
+//    read with ds_read_b64_tr_b8 (gfx950's transposing LDS read: in each
+//    16-lane group, source lane 2e + p addresses 8 bytes of a row and lane
+//    i receives byte i % 8 of source lanes 2e + i / 8, e = 0..7 -- measured
+//    by a probe on the box), so no transpose runs in the softmax segment.
 #pragma once
 
 #include "attention_kernels.hpp"
@@ -53,12 +56,10 @@ constexpr int k8Rows = 32 * k8Waves;             // query rows a CTA
 constexpr int k8KRowBytes = kD;                  // 128 B per K / V row
 constexpr int k8KBytes = kBN * k8KRowBytes;      // 8 KiB per K tile
 constexpr int k8KRing = 4;
-constexpr int k8VtPitch = kBN + 16;              // 80 B per d row of V^T
-constexpr int k8VtBytes = kD * k8VtPitch;        // 10 KiB
-constexpr int k8VtOff = k8KRing * k8KBytes;      // 32 KiB
-constexpr int k8StageOff = k8VtOff + 2 * k8VtBytes;  // 52 KiB
+constexpr int k8VtOff = k8KRing * k8KBytes;      // V ring: 4 tiles from 32 KiB
+constexpr int k8StageOff = 2 * k8KRing * k8KBytes;  // 64 KiB
 constexpr int k8StageBytes = 32 * kD * 2;        // one wave's 32 output rows
-constexpr int k8Smem = k8StageOff + k8Waves * k8StageBytes;  // 116 KiB
+constexpr int k8Smem = k8StageOff + k8Waves * k8StageBytes;  // 128 KiB
 constexpr float k8Threshold = 4.0f;              // lazy rescale (log2 units)
 constexpr float k8PShift = 4.0f;                 // P = 2^4 * probability
 constexpr int k8PScale = 127 - 4;                // e8m0 of 2^-4
@@ -75,6 +76,7 @@ struct Fp8Params {
 };
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x2v __attribute__((ext_vector_type(2)));
 
 // D[32x32] += (A * 2^(sa-127))[32x64] (B * 2^(sb-127))[64x32], e4m3 A and B;
 // lane l supplies 32 bytes of row / column l%32 at K offset 32*(l/32) and in
@@ -116,14 +118,12 @@ __device__ __forceinline__ void fwd8_cta(const Fp8Params &p, int raw, uint8_t *s
   const int hkv = hq / (p.q_heads / p.kv_heads);
   const size_t kvh = (size_t)(b * p.kv_heads + hkv);
   const uint8_t *Kh = p.K + kvh * p.seq_k * kD;
+  const uint8_t *Vh = p.V + kvh * p.seq_k * kD;
   const int vsrows = (p.seq_k + 31) / 32;
-  // Buffer resources over this head's V, K scales and V scales: 32-bit
+  // Buffer resources over this head's K scales and V scales: 32-bit
   // offsets from an SGPR base, and reads past the end return 0 (keys past
-  // seq_k are masked out of the softmax, so their V rows and scales only
-  // need to be finite).
-  const __amdgpu_buffer_rsrc_t vrs =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(p.V + kvh * p.seq_k * kD), 0,
-                                        p.seq_k * kD, 0x00020000);
+  // seq_k are masked out of the softmax, so their scales only need to be
+  // finite).
   const __amdgpu_buffer_rsrc_t ksrs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(p.Ks + kvh * p.seq_k * 4), 0,
                                         p.seq_k * 4, 0x00020000);
@@ -190,44 +190,36 @@ __device__ __forceinline__ void fwd8_cta(const Fp8Params &p, int raw, uint8_t *s
       dst[dt] = __builtin_amdgcn_raw_buffer_load_b8(vsrs, off + 32 * dt, 0, 0);
   };
 
-  // V: thread tg of group g loads keys 4kg .. 4kg+3 x d 64g + 4dg .. +3 and
-  // writes them to V^T rows d at the byte of key 4kg in the operand order:
-  // key 32j + 8i + 4h + e at byte 32h + 16j + 4i + e (kg = 8j + 2i + h).
-  // A wave covers 8 key groups x 8 dg: each load instruction reads 8 rows
-  // x 32 contiguous bytes, and each V^T store (bank = 16 (dg % 4) + a
-  // bijection of kg, at the 80-byte pitch) hits 32 distinct banks, 2-way.
-  // Measured in one process against 16 x 4 (conflict-free stores, 16-byte
-  // load segments) and 4 x 16 (64-byte segments, 4-way conflicts), TFLOP/s:
-  // B4 H32 S4096 1717 / 1486-1561 / 1530-1537, B2 H64 S8192 1616 / 1494 /
-  // 1585, causal B1 Hq64 Hkv8 S8192 1540-1546 / 1404-1464 / 1358-1371.
-  const int tg = threadIdx.x & 255;
-  const int kg = (tg & 7) | (((tg >> 6) & 1) << 3);
-  const int dg = ((tg >> 3) & 7) | ((tg >> 7) << 3);
-  const int vd = 64 * (int)grp + 4 * dg;
-  const int vpos = 32 * (kg & 1) + 16 * (kg >> 3) + 4 * ((kg >> 1) & 3);
-  uint32_t vr[4], vr1[4];
-  const uint32_t vgoff = (uint32_t)(4 * kg) * k8KRowBytes + vd;
-  auto load_v_to = [&](int kt, uint32_t(&dst)[4]) {
+  // V by LDS DMA into a 4-tile ring (64 rows x 128 B; wave w fills rows
+  // 8w .. 8w+7, rows past seq_k re-read the last key), 16-byte chunk c of row
+  // r at c ^ fv(r), fv(r) = 2 (((r >> 1) & 1) | ((r >> 3) & 1) << 1): the
+  // eight rows one transposing read touches in each lane half (4h + 0..3,
+  // 8 + 4h + 0..3) sit in distinct bank slots, and the two column halves
+  // keep opposite chunk parity, so 32 lanes read 256 bytes without conflict.
+  // V(t+3) is issued in iteration t into the slot of V(t-1), whose last
+  // reader (group B's G(t-1)) finished two segments earlier.
+  const int vrow = wave * 8 + (lane >> 3);
+  auto fv = [](uint32_t r) { return 2u * (((r >> 1) & 1u) | (((r >> 3) & 1u) << 1)); };
+  const uint32_t vgoff = ((lane & 7) ^ fv((uint32_t)vrow)) << 4;
+  auto issue_v = [&](int kt) {
+    const uint32_t l = lds0 + k8VtOff + (kt & 3) * k8KBytes + wave * 1024;
+    const int key = min(kt * kBN + vrow, p.seq_k - 1);
+    dma16(l, Vh, (uint32_t)key * k8KRowBytes + vgoff);
+  };
+  // ds_read_b64_tr_b8: in each 16-lane group source lane 2e + p addresses
+  // V[row R(e)][d0 + 8p .. +7] and lane i then holds V[R(0..7)][d0 + i].
+  // Read q: R(e) = 16q + 4h + (e & 3) + 8 (e >> 2), d0 = 32dt + 16 ((l >> 4) & 1),
+  // i.e. operand bytes 8q .. 8q+7 are keys 16q + 4h + 0..3 and 16q + 8 + 4h +
+  // 0..3 of column 32dt + l%32: the key order of the P operand.
+  uint32_t vread[4];
+  {
+    const uint32_t rl = 4 * half + ((lane >> 1) & 3) + 8 * ((lane >> 3) & 1);
+    const uint32_t cl = (lane >> 4) & 1;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      dst[e] = __builtin_amdgcn_raw_buffer_load_b32(
-          vrs, (uint32_t)(kt * kBN) * k8KRowBytes + vgoff + e * k8KRowBytes, 0, 0);
-  };
-  const uint32_t vt_store = opaque(lds0 + k8VtOff + (uint32_t)vd * k8VtPitch + vpos);
-  auto store_vt_from = [&](uint32_t vst, const uint32_t(&w)[4]) {
-    const uint32_t x01l = __builtin_amdgcn_perm(w[1], w[0], 0x05010400u);
-    const uint32_t x01h = __builtin_amdgcn_perm(w[1], w[0], 0x07030602u);
-    const uint32_t x23l = __builtin_amdgcn_perm(w[3], w[2], 0x05010400u);
-    const uint32_t x23h = __builtin_amdgcn_perm(w[3], w[2], 0x07030602u);
-    lds_store4(vst + 0 * k8VtPitch, __builtin_amdgcn_perm(x23l, x01l, 0x05040100u));
-    lds_store4(vst + 1 * k8VtPitch, __builtin_amdgcn_perm(x23l, x01l, 0x07060302u));
-    lds_store4(vst + 2 * k8VtPitch, __builtin_amdgcn_perm(x23h, x01h, 0x05040100u));
-    lds_store4(vst + 3 * k8VtPitch, __builtin_amdgcn_perm(x23h, x01h, 0x07060302u));
-  };
-  // V^T(t+1+grp) is stored in SM(t+1): buffer ((t+1) & 1) ^ grp.
-  const uint32_t vst_par[2] = {opaque(vt_store + grp * k8VtBytes),
-                               opaque(vt_store + (grp ^ 1) * k8VtBytes)};
-
+    for (int dt = 0; dt < 4; ++dt)
+      vread[dt] = opaque(lds0 + k8VtOff + rl * k8KRowBytes + (((2 * dt + cl) ^ fv(rl)) << 4) +
+                         8 * (lane & 1));
+  }
   // Fragment bases: K row kr of block j at +j*4096, d chunks 4s + h (bytes
   // 0-15 of the operand) and 4s + 2 + h (bytes 16-31); V^T row 32dt + kr,
   // bytes 32h .. +31.
@@ -238,14 +230,18 @@ __device__ __forceinline__ void fwd8_cta(const Fp8Params &p, int raw, uint8_t *s
     for (int i = 0; i < 2; ++i)
       kread[s][i] = opaque(lds0 + kr * k8KRowBytes +
                            (((4 * s + 2 * i + half) ^ ((kr >> 1) & 7)) << 4));
-  const uint32_t vt_read = opaque(lds0 + k8VtOff + kr * k8VtPitch + 32 * half);
   auto kfrag = [&](uint32_t kb, int j, int s) {
     return join8(lds_load16(kread[s][0] + kb * k8KBytes + j * 32 * k8KRowBytes),
                  lds_load16(kread[s][1] + kb * k8KBytes + j * 32 * k8KRowBytes));
   };
+  typedef __attribute__((address_space(3))) i32x2v lds_i2v;
   auto vfrag = [&](uint32_t vb, int dt) {
-    const uint32_t a = vt_read + vb * k8VtBytes + dt * 32 * k8VtPitch;
-    return join8(lds_load16(a), lds_load16(a + 16));
+    const uint32_t a = vread[dt] + vb * k8KBytes;
+    i32x2v r[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      r[q] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i2v *)(uintptr_t)(a + 16 * q * k8KRowBytes));
+    return i32x8{r[0][0], r[0][1], r[1][0], r[1][1], r[2][0], r[2][1], r[3][0], r[3][1]};
   };
 
   f32x16 o[4];
@@ -295,10 +291,10 @@ __device__ __forceinline__ void fwd8_cta(const Fp8Params &p, int raw, uint8_t *s
       const int x = idx(i);
       if (is_s(i)) {
         const int j = x >> 1, s = x & 1;
-        sn[j] = mfma_fp8(f[i], qf[s], s == 0 ? f32x16{} : sn[j], ks[VB ^ 1][j] >> (16 * s),
+        sn[j] = mfma_fp8(f[i], qf[s], s == 0 ? f32x16{} : sn[j], ks[(VB & 1) ^ 1][j] >> (16 * s),
                          qs[s]);
       } else {
-        o[x] = mfma_fp8(f[i], pf, o[x], vs[VB][x], (uint32_t)k8PScale);
+        o[x] = mfma_fp8(f[i], pf, o[x], vs[VB & 1][x], (uint32_t)k8PScale);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -363,35 +359,31 @@ __device__ __forceinline__ void fwd8_cta(const Fp8Params &p, int raw, uint8_t *s
   // One iteration t < ntiles - 1: G(t), barrier, SM(t+1), barrier.
   auto iter = [&](auto ph_tag, int t, f32x16(&sn)[2]) {
     constexpr int PH = decltype(ph_tag)::value;
-    load_v_to(t + 1 + (int)grp, vr);
     load_ks(t + 2, ks[PH & 1]);
     load_vs(t + 1, vs[(PH + 1) & 1]);
     seg_g(std::true_type{}, std::integral_constant<uint32_t, (PH + 1) % k8KRing>{},
-          std::integral_constant<uint32_t, PH & 1>{}, sn);
+          std::integral_constant<uint32_t, PH>{}, sn);
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
     softmax(sn, t + 1);
-    store_vt_from(vst_par[(PH + 1) & 1], vr);  // first use of vr: waits for the loads
     issue_k(t + 4);
-    lds_barrier();
+    issue_v(t + 3);
+    vm_wait_barrier<2>();
   };
 
-  // ---- prologue: K(0..3), V^T(0), B's half of V^T(1), S(0), softmax(0)
+  // ---- prologue: K(0..3), V(0..2), S(0), softmax(0)
   f32x16 sa[2];
   issue_k(0);
   issue_k(1);
   issue_k(2);
-  load_v_to(0, vr);
-  if (grp == 1)
-    load_v_to(1, vr1);
+  issue_v(0);
+  issue_v(1);
+  issue_v(2);
   load_ks(0, ks[0]);
   load_ks(1, ks[1]);
   load_vs(0, vs[0]);
   vm_wait_barrier();
-  store_vt_from(vt_store, vr);
-  if (grp == 1)
-    store_vt_from(vt_store + k8VtBytes, vr1);
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
     const int j = x >> 1, s = x & 1;
@@ -425,13 +417,13 @@ __device__ __forceinline__ void fwd8_cta(const Fp8Params &p, int raw, uint8_t *s
     }
     iter(I_<3>{}, t + 3, sa);
   }
-  // Last tile: G = PV(t) only (V^T buffer t & 1).
-  if (t & 1)
-    seg_g(std::false_type{}, std::integral_constant<uint32_t, 0>{},
-          std::integral_constant<uint32_t, 1>{}, sa);
-  else
-    seg_g(std::false_type{}, std::integral_constant<uint32_t, 0>{},
-          std::integral_constant<uint32_t, 0>{}, sa);
+  // Last tile: G = PV(t) only (V buffer t & 3, scales of parity t & 1).
+  switch (t & 3) {
+  case 0: seg_g(std::false_type{}, std::integral_constant<uint32_t, 0>{}, std::integral_constant<uint32_t, 0>{}, sa); break;
+  case 1: seg_g(std::false_type{}, std::integral_constant<uint32_t, 0>{}, std::integral_constant<uint32_t, 1>{}, sa); break;
+  case 2: seg_g(std::false_type{}, std::integral_constant<uint32_t, 0>{}, std::integral_constant<uint32_t, 2>{}, sa); break;
+  default: seg_g(std::false_type{}, std::integral_constant<uint32_t, 0>{}, std::integral_constant<uint32_t, 3>{}, sa); break;
+  }
   // K DMA issued for tiles past the end may still be in flight: let it land
   // before the workgroup's LDS can be handed to another workgroup.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
