@@ -24,13 +24,14 @@
 // tiles on v_mfma_f32_32x32x16.  The operands fixed for a CTA (K, V in the
 // dK/dV kernel; Q, dO in the dQ kernel) are held as MFMA fragments in
 // registers; the rest are read as 16-byte row chunks from LDS.  Operands
-// needed K-contiguous the other way (Q^T, dO^T, K^T) are written to LDS
-// transposed when a block is loaded, and P^T / dS^T (dS for dQ) go through
-// LDS between the score products and the gradient products.  LDS tiles are
+// needed K-contiguous the other way (Q^T, dO^T, K^T as the B operand of
+// dK, dV, dQ) are read from the row-major Q, dO, K tiles by transposing LDS
+// reads (ds_read_b64_tr_b16), and P^T / dS^T (dS for dQ) go through LDS
+// between the score products and the gradient products.  LDS tiles are
 // unpadded with XOR-swizzled 16-byte chunks (256-byte rows: chunk c of row
 // r at c ^ (r % 16); 128-byte rows: at c ^ ((r / 2) % 8)), so that 16
-// consecutive rows read at one chunk cover all 16 bank groups: 80 KiB
-// (dK/dV) and 56 KiB (dQ) of LDS, two CTAs per CU.
+// consecutive rows read at one chunk cover all 16 bank groups: 48 KiB
+// (dK/dV) and 40 KiB (dQ) of LDS, two CTAs per CU (register-bound).
 #include "attention.hpp"
 #include "wave_common.hpp"
 
@@ -42,7 +43,6 @@ namespace {
 constexpr int kBD = 128;               // head dim
 constexpr int kBlk = 64;               // query or key rows per block
 constexpr int kWide = kBlk * 256;      // [64][128] 16-bit tile: 16 KiB
-constexpr int kNarrowT = kBD * 128;    // [128][64] tile: 16 KiB
 constexpr int kNarrowS = kBlk * 128;   // [64][64] tile: 8 KiB
 constexpr float kLog2eB = 1.4426950408889634f;
 
@@ -68,8 +68,7 @@ struct BwdParams {
 
 // acc += A[32 rows][K] * B^T with A rows a0 .. a0+31 of a ROWB-byte-row LDS
 // tile, K = 16 * NK, and B as per-slice register fragments bf[kk] (lane l:
-// row l % 32 of B, elements 16 kk + 8 (l / 32) .. +8) (mma_nt_reg) or as
-// rows b0 .. b0+31 of an LDS tile of the same row size (mma_nt_lds).
+// row l % 32 of B, elements 16 kk + 8 (l / 32) .. +8).
 template <int DT, int NK, int ROWB>
 __device__ __forceinline__ void mma_nt_reg(f32x16 &acc, const uint8_t *A, uint32_t a0,
                                            const u32x4 (&bf)[NK]) {
@@ -81,16 +80,35 @@ __device__ __forceinline__ void mma_nt_reg(f32x16 &acc, const uint8_t *A, uint32
     acc = mfma32x32x16<DT>(a, bf[kk], acc);
   }
 }
-template <int DT, int NK, int ROWB>
-__device__ __forceinline__ void mma_nt_lds(f32x16 &acc, const uint8_t *A, uint32_t a0,
-                                           const uint8_t *B, uint32_t b0) {
-  const uint32_t lane = threadIdx.x & 63, ra = a0 + (lane & 31), rb = b0 + (lane & 31);
-  const uint32_t sa = (lane >> 5) ^ swz<ROWB>(ra), sb = (lane >> 5) ^ swz<ROWB>(rb);
+
+// acc += A[32 rows][K] * R[K][32 columns], K = 16 * NK, with A rows
+// a0 .. a0+31 of a 128-byte-row LDS tile and R a row-major [K][128] tile of
+// 256-byte rows (columns c0 .. c0+31): the B operand comes from R by
+// transposing reads (ds_read_b64_tr_b16: in each 16-lane group source lane
+// 4a + p addresses R[k + a][c + 4p .. +3] and lane i then holds
+// R[k .. k+3][c + i]), so no transposed copy of R is needed.  Lane l reads
+// rows 16 kk + 8 (l / 32) + 4 r + (l >> 2) % 4, columns c0 + 16 ((l >> 4) % 2)
+// + 4 (l % 4), r = 0, 1: the 8 K values of the B fragment, in order.
+template <int DT, int NK>
+__device__ __forceinline__ void mma_nt_tr(f32x16 &acc, const uint8_t *A, uint32_t a0,
+                                          const uint8_t *R, uint32_t c0) {
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s4 lds_s4;
+  const uint32_t lane = threadIdx.x & 63, ra = a0 + (lane & 31);
+  const uint32_t sa = (lane >> 5) ^ swz<128>(ra);
+  const uint32_t rb = 8 * (lane >> 5) + ((lane >> 2) & 3);
+  const uint32_t cb = 2 * c0 + 32 * ((lane >> 4) & 1) + 8 * (lane & 3);
+  const uint32_t rbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)R;
 #pragma unroll
   for (int kk = 0; kk < NK; ++kk) {
-    const u32x4 a = *reinterpret_cast<const u32x4 *>(A + ra * ROWB + (((2u * kk) ^ sa) << 4));
-    const u32x4 b = *reinterpret_cast<const u32x4 *>(B + rb * ROWB + (((2u * kk) ^ sb) << 4));
-    acc = mfma32x32x16<DT>(a, b, acc);
+    const u32x4 a = *reinterpret_cast<const u32x4 *>(A + ra * 128 + (((2u * kk) ^ sa) << 4));
+    const u32x2 lo = __builtin_bit_cast(
+        u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                   (lds_s4 *)(uintptr_t)(rbase + toff<256>(16 * kk + rb, cb))));
+    const u32x2 hi = __builtin_bit_cast(
+        u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                   (lds_s4 *)(uintptr_t)(rbase + toff<256>(16 * kk + rb + 4, cb))));
+    acc = mfma32x32x16<DT>(a, u32x4{lo[0], lo[1], hi[0], hi[1]}, acc);
   }
 }
 
@@ -105,7 +123,7 @@ __device__ __forceinline__ void load_frags(const uint16_t *row, u32x4 (&f)[8]) {
 
 // A [64][128] block of rows (row stride 128 elements) in flight through
 // registers: fetch() issues the global loads, put() writes the rows to LDS
-// (wide tile R) and, when T != nullptr, transposed ([128][64] narrow tile T).
+// (wide tile R).
 // Thread t handles row pairs x 16-byte chunks: unit u = t + 256*i, row pair
 // u / 16, chunk u % 16.
 struct BlockRegs {
@@ -119,23 +137,13 @@ struct BlockRegs {
       b[i] = *reinterpret_cast<const u32x4 *>(src + (size_t)(2 * rp + 1) * kBD + 8 * c);
     }
   }
-  __device__ __forceinline__ void put(uint8_t *R, uint8_t *T) const {
+  __device__ __forceinline__ void put(uint8_t *R) const {
     const uint32_t t = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const uint32_t u = t + 256u * i, rp = u >> 4, c = u & 15u;
       *reinterpret_cast<u32x4 *>(R + toff<256>(2 * rp, 16 * c)) = a[i];
       *reinterpret_cast<u32x4 *>(R + toff<256>(2 * rp + 1, 16 * c)) = b[i];
-      if (T != nullptr) {
-        // Element d = 8c + e of rows 2rp, 2rp+1 -> T[8c + e][2rp .. 2rp+1].
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          *reinterpret_cast<uint32_t *>(T + toff<128>(8 * c + 2 * e, 4 * rp)) =
-              __builtin_amdgcn_perm(b[i][e], a[i][e], 0x05040100u);
-          *reinterpret_cast<uint32_t *>(T + toff<128>(8 * c + 2 * e + 1, 4 * rp)) =
-              __builtin_amdgcn_perm(b[i][e], a[i][e], 0x07060302u);
-        }
-      }
     }
   }
 };
@@ -189,9 +197,8 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(BwdParams p, int rows) {
 // dK, dV of one 64-key block of one KV head.
 template <int DT, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kWide + 2 * kNarrowT + 2 * kNarrowS];
-  uint8_t *sQ = smem, *sdO = sQ + kWide, *sQt = sdO + kWide, *sdOt = sQt + kNarrowT;
-  uint8_t *sPt = sdOt + kNarrowT, *sdSt = sPt + kNarrowS;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kWide + 2 * kNarrowS];
+  uint8_t *sQ = smem, *sdO = sQ + kWide, *sPt = sdO + kWide, *sdSt = sPt + kNarrowS;
   const int nb = p.seq / kBlk;
   const int pid = xcd_pid((int)blockIdx.x, (int)gridDim.x);
   const int kb = pid % nb, bhk = pid / nb;
@@ -225,8 +232,8 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdParams p) {
     const int qb = qb0 + it % nq;
     const size_t row_base = q_offset(it) / kBD;  // bh * seq + qb * 64
     __syncthreads();  // the previous item's readers are done
-    rq.put(sQ, sQt);
-    rdo.put(sdO, sdOt);
+    rq.put(sQ);
+    rdo.put(sdO);
     if (it + 1 < items) {
       rq.fetch(p.Q + q_offset(it + 1));
       rdo.fetch(p.dO + q_offset(it + 1));
@@ -272,8 +279,8 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdParams p) {
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      mma_nt_lds<DT, 4, 128>(dv[t], sPt, kh * 32, sdOt, (2 * dq + t) * 32);
-      mma_nt_lds<DT, 4, 128>(dk[t], sdSt, kh * 32, sQt, (2 * dq + t) * 32);
+      mma_nt_tr<DT, 4>(dv[t], sPt, kh * 32, sdO, (2 * dq + t) * 32);
+      mma_nt_tr<DT, 4>(dk[t], sdSt, kh * 32, sQ, (2 * dq + t) * 32);
     }
   }
   uint16_t *dK = p.dK + kv_off, *dV = p.dV + kv_off;
@@ -287,8 +294,8 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdParams p) {
 // dQ of one 64-query block of one q head.
 template <int DT, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kWide + kNarrowT + kNarrowS];
-  uint8_t *sK = smem, *sV = sK + kWide, *sKt = sV + kWide, *sdS = sKt + kNarrowT;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kWide + kNarrowS];
+  uint8_t *sK = smem, *sV = sK + kWide, *sdS = sV + kWide;
   const int nb = p.seq / kBlk;
   const int pid = xcd_pid((int)blockIdx.x, (int)gridDim.x);
   const int qb = pid % nb, bh = pid / nb;
@@ -316,8 +323,8 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdParams p) {
   rv.fetch(p.V + kv_base);
   for (int kb = 0; kb < kb_end; ++kb) {
     __syncthreads();
-    rk.put(sK, sKt);
-    rv.put(sV, nullptr);
+    rk.put(sK);
+    rv.put(sV);
     if (kb + 1 < kb_end) {
       rk.fetch(p.K + kv_base + (size_t)(kb + 1) * kBlk * kBD);
       rv.fetch(p.V + kv_base + (size_t)(kb + 1) * kBlk * kBD);
@@ -347,7 +354,7 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdParams p) {
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < 2; ++t)
-      mma_nt_lds<DT, 4, 128>(dqa[t], sdS, qh * 32, sKt, (2 * dq + t) * 32);
+      mma_nt_tr<DT, 4>(dqa[t], sdS, qh * 32, sK, (2 * dq + t) * 32);
   }
   uint16_t *dQ = p.dQ + q_off;
 #pragma unroll
