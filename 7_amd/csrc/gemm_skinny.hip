@@ -177,16 +177,18 @@ hipError_t launch_out(const SkinnyParams &p, bool cm, hipStream_t s) {
 // Reduction: each contributor takes an arrival ticket on the tile's first
 // counter when its K range is done.  All but the last store their fp32
 // partials (16-byte groups at f32x4 index group*256 + thread, fully
-// coalesced) to their slots and count themselves on the second counter
-// with an agent-scope release; the last arriver waits for that count, sums
-// the partials in split order (its own from its accumulators),
+// coalesced) to their slots with device-scope stores and, once those are
+// acknowledged, count themselves on the second counter; the last arriver
+// waits for that count, reads the partials with device-scope loads (no
+// release or acquire: the data never sits in a non-coherent cache), sums
+// them in split order (its own from its accumulators),
 // s = ((p_0 + p_1) + p_2) + p_3, so the result does not depend on arrival
 // order, stores C, and resets both counters to zero for the next launch.
 // Splits of a tile take consecutive CTA numbers after the XCD renumbering
 // (workgroup i runs on XCD i % 8), so they run on one XCD.
 constexpr int kXMaxSplits = 4;
-// Cache-policy operand of the buffer store builtins on gfx950: bit 4 = sc1
-// (with sc0 clear: device scope).
+// Cache-policy operand of the buffer load/store builtins on gfx950: bit 4 =
+// sc1 (with sc0 clear: device scope).
 constexpr int kScopeDevice = 16;
 
 template <int BN> struct SplitCfg {
@@ -346,11 +348,13 @@ __global__ __launch_bounds__(256, 1) void skinny_split_kernel(SplitParams p) {
       for (int g2 = 0; g2 < NG; ++g2)
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, group(g2)), mine,
                                                (g2 * 256 + threadIdx.x) * 16, 0, kScopeDevice);
-      // Every wave's partial stores are acknowledged before the barrier;
-      // thread 0's agent-scope release then publishes all of them.
+      // Every wave's partial stores are acknowledged at the coherence
+      // point before the barrier, so thread 0's count, issued after it,
+      // needs no release (whose L2 write-back measured 1-4 us a launch):
+      // the reader's device-coherent loads below find them there.
       vm_wait_barrier();
       if (threadIdx.x == 0)
-        __hip_atomic_fetch_add(&p.counters[2 * tile + 1], 1u, __ATOMIC_RELEASE,
+        __hip_atomic_fetch_add(&p.counters[2 * tile + 1], 1u, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
       return;
     }
@@ -368,13 +372,15 @@ __global__ __launch_bounds__(256, 1) void skinny_split_kernel(SplitParams p) {
                          __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    // Synchronises with the release of every published count (one release
-    // sequence on the counter).
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     // The other contributors' partials, all loads in flight at once: other
-    // o (0 .. splits-2) is split o + (o >= split).
-    const f32x4 *base =
-        reinterpret_cast<const f32x4 *>(p.slots + (size_t)tile * p.splits * X::SLOT) + threadIdx.x;
+    // o (0 .. splits-2) is split o + (o >= split).  They are device-scope
+    // (sc1) loads, the cache policy of agent-scope atomic loads, so they
+    // read the coherence point the publishers' sc1 stores were
+    // acknowledged at before their counts, and no acquire (an L2
+    // invalidate, 1-3 us a launch) is needed; the barrier above issues
+    // them after thread 0 has seen every count.
+    const __amdgpu_buffer_rsrc_t peers = __builtin_amdgcn_make_buffer_rsrc(
+        p.slots + (size_t)tile * p.splits * X::SLOT, 0, p.splits * X::SLOT * 4, 0x00020000);
     f32x4 x[kXMaxSplits - 1][NG];
 #pragma unroll
     for (int o = 0; o < kXMaxSplits - 1; ++o) {
@@ -382,7 +388,10 @@ __global__ __launch_bounds__(256, 1) void skinny_split_kernel(SplitParams p) {
         const int c = o + (o >= split ? 1 : 0);
 #pragma unroll
         for (int g2 = 0; g2 < NG; ++g2)
-          x[o][g2] = __builtin_nontemporal_load(base + (size_t)c * (X::SLOT / 4) + g2 * 256);
+          x[o][g2] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         peers, ((uint32_t)c * (X::SLOT / 4) + g2 * 256 + threadIdx.x) * 16, 0,
+                         kScopeDevice));
       }
     }
     // Sum in split order; contributor c is this CTA's own (c == split) or
@@ -492,18 +501,21 @@ SplitPlan skinny_split_plan(int M, int N, int K, int cus) {
   // 64-column blocks when they leave room for at least two splits, else
   // 128-column ones; at most 4 splits (at least 2 when the unsplit kernel
   // would take more than one round of CTAs), at least 8 stages a split.
-  // The split pays its partial exchange (about 12 us at 256 CUs: publish,
-  // release, acquire, reduce), so it runs only where each split keeps at
-  // least 2048 of K, and where the unsplit kernel fills one round of CUs
-  // only for M > 96 and at least 4096 of K a split.  Measured (bf16, us,
-  // unsplit / split, fill kernel included): 128 x N x 8192 with N = 1024
-  // 31.1 / 22.4, 2048 33.0 / 23.4, 4096 33.7 / 26.6, 8192 39.6 / 37.3,
-  // 16384 91.5 / 58.4; 128 x 8192 x K with K = 4096 23.1 / 25.8, 16384
-  // 88.8 / 63.4; 64 x 8192 x 8192 35.4 / 35.1; 96 x 8192 x 8192 36.2 /
-  // 36.8; 128 x 4096 x 4096 18.4 / 20.1; 128 x 24576 x 4096 64.9 / 59.6.
+  // The split pays its partial exchange (a few us at 256 CUs: the wait for
+  // the last publisher, the partial loads, the sums), so it runs only where
+  // each split keeps at least 4096 of K, or 2048 where M > 96 and the
+  // unsplit kernel's N / 32 CTAs fill the CUs.  Measured (bf16, us,
+  // unsplit / this plan, fill kernel included): 128 x N x 8192 with
+  // N = 1024 31.2 / 21.5, 2048 33.7 / 21.2, 4096 34.8 / 23.7, 6144
+  // 39.9 / 31.6, 8192 38.5 / 32.2, 12288 70.9 / 44.1, 16384 94.5 / 53.6,
+  // 24576 153.2 / 105.7; 128 x N x 4096 with N = 8192 23.2 / 21.4, 16384
+  // 44.3 / 31.3; M x 8192 x 8192 with M = 1 33.0 / 29.6, 32 34.7 / 30.7,
+  // 64 35.5 / 31.5, 96 36.1 / 32.6; 100 x 5000 x 12288 49.5 / 32.3.  Not
+  // split: 128 x 6144 x 4096 18.9 (20.8 in two splits), 32 x 8192 x 4096
+  // 20.1 (19.8), 128 x 8192 x 2048 11.3 (16.2), 128 x 2048 x 2048 9.6
+  // (13.2 in four).
   const int nk = K / kBK;
   const int unsplit = (N + 31) / 32;  // CTAs of the unsplit kernel
-  const bool one_round = unsplit > cus / 2 && unsplit <= cus;
   for (int bn : {64, 128}) {
     const int tiles = (N + bn - 1) / bn;
     int s = cus / tiles;
@@ -516,7 +528,7 @@ SplitPlan skinny_split_plan(int M, int N, int K, int cus) {
     if (s < 2)
       continue;
     const int ks = K / s;
-    if (ks < 2048 || (one_round && (ks < 4096 || M <= 96)))
+    if (ks < 2048 || (ks < 4096 && (M <= 96 || unsplit < cus)))
       return plan;
     plan.splits = s;
     plan.bn = bn;

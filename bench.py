@@ -329,16 +329,30 @@ def config_lines(wave, torch, dev, steps, warmup):
         if name == "3a":  # short M: the auto dispatch's split-K short-M kernel
             ws = torch.empty(max(wave.gemm_auto_workspace_bytes(M, N, K), 1), dtype=torch.uint8,
                              device=dev)
-            ams = time_launches(lambda: wave.gemm_auto(a, b, out_dtype=torch.bfloat16,
-                                                       workspace=ws, out=c), steps, warmup,
-                                torch)
+            wrapped = time_launches(lambda: wave.gemm_auto(a, b, out_dtype=torch.bfloat16,
+                                                           workspace=ws, out=c), steps, warmup,
+                                    torch)
+            # The same C-ABI call with its arguments bound once: the Python
+            # wrapper's checks take about as long as this ~32 us launch, so
+            # through it the stream can run dry between launches.
+            launch = wave.runtime.lib().wave_gemm_auto_launch
+            cargs = (a.data_ptr(), b.data_ptr(), c.data_ptr(), M, N, K, wave.runtime.BF16,
+                     wave.runtime.BF16,
+                     wave.runtime.ROW_MAJOR, ws.data_ptr(), ws.numel(),
+                     torch.cuda.current_stream(dev).cuda_stream)
+
+            def direct():
+                if launch(*cargs) != 0:
+                    raise RuntimeError("wave_gemm_auto_launch failed")
+            ams = time_launches(direct, max(steps, 200), warmup, torch)  # ~32 us each
             atf = fl / (ams * 1e-3) / 1e12
             gbs = nbytes / (ams * 1e-3) / 1e9
             line.update({"value": round(atf, 2), "ms_per_step": round(ams, 4),
                          "frac_of_mfma_peak": round(atf / MFMA_PEAK_TFLOPS, 4),
                          "gbps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-                         "kernel": "wave_gemm_auto_launch (split-K short-M, 4 K splits of "
-                                   "128-column blocks, + counter fill)",
+                         "kernel": "wave_gemm_auto_launch (split-K short-M kernel, + counter "
+                                   "fill), called through ctypes with pre-bound arguments",
+                         "ms_per_step_through_python_wrapper": round(wrapped, 4),
                          "unsplit_kernel_value": round(tf, 2)})
         if name == "3c":  # fewer 256x256 tiles (128) than CUs: the auto dispatch's Stream-K
             ws = torch.empty(max(wave.gemm_auto_workspace_bytes(M, N, K), 1), dtype=torch.uint8,

@@ -160,12 +160,11 @@ def short_m_plan(M, N, K, cus):
     CUs / blocks >= 2, else 128-column ones (2 splits at least when the
     unsplit kernel's N / 32 CTAs exceed the CUs); at most 4 splits, at least
     8 stages of 64 a split; none when a split keeps less than 2048 of K, or
-    when the unsplit kernel fills one round of CUs and M <= 96 or a split
-    keeps less than 4096 of K."""
+    less than 4096 where M <= 96 or the unsplit kernel's N / 32 CTAs do not
+    fill the CUs."""
     if M > 128 or N < 1024 or K % 64 or K * 2 * 128 >= 2**32 or N * K * 2 >= 2**32:
         return 0, 0
     unsplit = -(-N // 32)
-    one_round = cus // 2 < unsplit <= cus
     for bn in (64, 128):
         s = min(cus // -(-N // bn), 4)
         if s < 2 and bn == 128 and unsplit > cus:
@@ -175,7 +174,7 @@ def short_m_plan(M, N, K, cus):
         if s < 2:
             continue
         ks = K // s
-        if ks < 2048 or (one_round and (ks < 4096 or M <= 96)):
+        if ks < 2048 or (ks < 4096 and (M <= 96 or unsplit < cus)):
             return 0, 0
         return bn, s
     return 0, 0
@@ -342,6 +341,30 @@ def test_split_short_m_matches_unsplit(wave, oracle, dev, in_dt, out_dt, layout,
         got = wave.gemm_auto(A, B, out_dtype=out_dt, layout=layout, workspace=ws)
         torch.cuda.synchronize()
         assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("shape", [(128, 8192, 8192), (128, 4096, 8192), (100, 5000, 12288)])
+def test_split_short_m_alternating_inputs(wave, oracle, dev, shape):
+    """Two different B on one workspace, alternated launch after launch: each
+    output equals wave_gemm_launch's for its own B, so the last arriver never
+    reads a partial of the other input (the exchange's device-scope stores
+    and loads leave no stale copy in a cache on the way)."""
+    M, N, K = shape
+    need = wave.gemm_auto_workspace_bytes(M, N, K)
+    assert need == expected_workspace(wave, M, N, K, dev)[1]
+    a = oracle.gemm_inputs(M, K, 2, 7, 0)
+    b0 = oracle.gemm_inputs(N, K, 2, 7, 1)
+    b1 = oracle.gemm_inputs(N, K, 2, 7, 2)
+    A = to_dev(a, torch.bfloat16, dev)
+    Bs = [to_dev(b0, torch.bfloat16, dev), to_dev(b1, torch.bfloat16, dev)]
+    refs = [wave.gemm(A, B, out_dtype=torch.bfloat16) for B in Bs]
+    assert not torch.equal(refs[0], refs[1])
+    ws = torch.zeros((max(need, 1),), dtype=torch.uint8, device=dev)
+    out = torch.empty_like(refs[0])
+    for i in range(24):
+        wave.gemm_auto(A, Bs[i & 1], out_dtype=torch.bfloat16, workspace=ws, out=out)
+        torch.cuda.synchronize()
+        assert torch.equal(out, refs[i & 1]), i
 
 
 def test_split_short_m_float_inputs_same_bits(wave, oracle, dev):
