@@ -1280,7 +1280,9 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
     }
     // Publish this worker's fp32 partial: 16-byte group g of MFMA tile
     // (tp, tq) of thread t at f32x4 index ((tp*TQ + tq)*NG + g)*NT + t, so
-    // every store and load instruction covers 4 KiB contiguously.
+    // every store and load instruction covers 4 KiB contiguously.  Plain
+    // stores: the accumulators go out of AGPRs directly (device-coherent
+    // buffer stores need them in VGPRs and spilled 146 VGPRs here).
     f32x4 *mine = reinterpret_cast<f32x4 *>(p.scratch + ((size_t)worker * 2 + slot) * kTileElems);
 #pragma unroll
     for (int tp = 0; tp < TP; ++tp)
@@ -1296,15 +1298,14 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
     const int last_owner = sk_owner(total, p.workers, (tile + 1) * iters - 1);
     const int parts = last_owner - first_owner + 1;
     // Every wave waits for its partial stores (vmcnt(0): acknowledged by
-    // L2) before the barrier; thread 0's agent-scope acq_rel ticket then
-    // writes the XCD's L2 back, which releases all of them at once.  The
-    // last arriver's waves each invalidate with an agent-scope acquire
-    // before reading the others' partials.  So one wave per worker does the
-    // L2-wide write-back (a __threadfence in every wave did it four times,
-    // plus an invalidate each, before and after the ticket).
+    // L2) before the barrier; thread 0's agent-scope release ticket then
+    // writes the XCD's L2 back, which publishes all of them at once.  The
+    // last arriver reads the partials with device-coherent (sc1) loads,
+    // issued after the barrier that follows its ticket: they read the
+    // coherence point, so it needs no acquire (an L2 invalidate).
     vm_wait_barrier();
     if (threadIdx.x == 0)
-      *arrival = __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_ACQ_REL,
+      *arrival = __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_RELEASE,
                                         __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (*arrival != parts - 1)
@@ -1312,13 +1313,17 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
     // Last arriver: reduce all contributors' partials (its own included,
     // reloaded) in worker order, a fixed order, so the result does not
     // depend on arrival order: s = ((0 + p_first) + p_second) + ....
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     auto part_of = [&](int c) {
-      return reinterpret_cast<const f32x4 *>(
-          p.scratch + ((size_t)c * 2 + sk_slot(total, p.workers, c, tile, iters)) * kTileElems);
+      return coherent_rsrc(
+          p.scratch + ((size_t)c * 2 + sk_slot(total, p.workers, c, tile, iters)) * kTileElems,
+          kTileElems * 4);
     };
+    // Partial group (tp, tq, g) of this thread: byte offset tid16 + at()
+    // (the asm keeps tid16 from being hoisted, live, across the mainloop).
+    uint32_t tid16 = threadIdx.x * 16;
+    asm volatile("" : "+v"(tid16));
     auto at = [&](int tp, int tq, int g) {
-      return (size_t)((tp * TQ + tq) * C::NG + g) * NT + threadIdx.x;
+      return (uint32_t)((tp * TQ + tq) * C::NG + g) * NT * 16u;
     };
     if (parts >= 2) {
       if (parts > 2) {
@@ -1333,9 +1338,8 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
         // inside the store callback instead spilled 96-141 VGPRs.
         constexpr int kGroups = TP * TQ * C::NG, kFold = 8;
         static_assert(kGroups % kFold == 0, "whole fold batches");
-        f32x4 *dst = reinterpret_cast<f32x4 *>(
-            p.scratch + ((size_t)first_owner * 2 +
-                         sk_slot(total, p.workers, first_owner, tile, iters)) * kTileElems);
+        const __amdgpu_buffer_rsrc_t dst = part_of(first_owner);
+        auto off = [&](int q) { return (uint32_t)q * NT * 16u; };
         for (int q0 = 0; q0 < kGroups; q0 += kFold) {
           f32x4 r[kFold];
 #pragma unroll
@@ -1343,12 +1347,12 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
             r[j] = f32x4{0.f, 0.f, 0.f, 0.f};
           int c = first_owner;
           for (; c + 1 < last_owner; c += 2) {
-            const f32x4 *x = part_of(c), *y = part_of(c + 1);
+            const __amdgpu_buffer_rsrc_t x = part_of(c), y = part_of(c + 1);
             f32x4 a[kFold], b[kFold];
 #pragma unroll
             for (int j = 0; j < kFold; ++j) {
-              a[j] = __builtin_nontemporal_load(x + (size_t)(q0 + j) * NT + threadIdx.x);
-              b[j] = __builtin_nontemporal_load(y + (size_t)(q0 + j) * NT + threadIdx.x);
+              a[j] = coherent_load16(x, tid16, off(q0 + j));
+              b[j] = coherent_load16(y, tid16, off(q0 + j));
             }
 #pragma unroll
             for (int j = 0; j < kFold; ++j) {
@@ -1357,15 +1361,18 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
             }
           }
           if (c < last_owner) {
-            const f32x4 *x = part_of(c);
+            const __amdgpu_buffer_rsrc_t x = part_of(c);
 #pragma unroll
             for (int j = 0; j < kFold; ++j)
-              r[j] += __builtin_nontemporal_load(x + (size_t)(q0 + j) * NT + threadIdx.x);
+              r[j] += coherent_load16(x, tid16, off(q0 + j));
           }
 #pragma unroll
           for (int j = 0; j < kFold; ++j)
-            dst[(size_t)(q0 + j) * NT + threadIdx.x] = r[j];
+            coherent_store16(dst, tid16, r[j], off(q0 + j));
         }
+        // The pass below reads these groups back (same thread, same
+        // offsets): let the stores complete first.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
       // s = (0 + X) + Y with X the first slot (p_first, or the fold) and Y
       // the last contributor's partial.  The last arriver still holds its
@@ -1383,7 +1390,7 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
       // epilogue costs VGPR spills here.
       constexpr int kBatch = 8 / C::NG < TP ? 8 / C::NG : TP;
       static_assert(TP % kBatch == 0, "whole batches per row");
-      const f32x4 *pa = part_of(first_owner), *pb = part_of(last_owner);
+      const __amdgpu_buffer_rsrc_t pa = part_of(first_owner), pb = part_of(last_owner);
       auto reduce = [&](auto role) {
         // R: 0 both slots, 1 X from registers, 2 Y from registers.
         constexpr int R = decltype(role)::value;
@@ -1401,10 +1408,14 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
 #pragma unroll
                     for (int h = 0; h < C::NG; ++h) {
                       if constexpr (R != 1)
-                        rx[u][j][h] = __builtin_nontemporal_load(pa + at(tp + j, tq + u, h));
+                        rx[u][j][h] = coherent_load16(pa, tid16, at(tp + j, tq + u, h));
                       if constexpr (R != 2)
-                        ry[u][j][h] = __builtin_nontemporal_load(pb + at(tp + j, tq + u, h));
+                        ry[u][j][h] = coherent_load16(pb, tid16, at(tp + j, tq + u, h));
                     }
+                // Buffer loads do not alias C's global stores for the
+                // compiler, which would otherwise hoist every batch's loads
+                // to the top (spilling); keep each batch at its place.
+                asm volatile("" ::: "memory");
               }
               f32x4 s = {0.f, 0.f, 0.f, 0.f};
               if constexpr (R == 1)
@@ -1431,7 +1442,7 @@ __device__ __forceinline__ void streamk_cta(const Params &p, int worker, uint8_t
           p, tm * kTile, tn * kTile, [&](int tp, int tq, int g) {
             f32x4 s = {0.f, 0.f, 0.f, 0.f};
             for (int c = first_owner; c <= last_owner; ++c)
-              s += __builtin_nontemporal_load(part_of(c) + at(tp, tq, g));
+              s += coherent_load16(part_of(c), tid16, at(tp, tq, g));
             return s;
           });
     }

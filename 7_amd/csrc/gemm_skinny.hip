@@ -187,9 +187,6 @@ hipError_t launch_out(const SkinnyParams &p, bool cm, hipStream_t s) {
 // Splits of a tile take consecutive CTA numbers after the XCD renumbering
 // (workgroup i runs on XCD i % 8), so they run on one XCD.
 constexpr int kXMaxSplits = 4;
-// Cache-policy operand of the buffer load/store builtins on gfx950: bit 4 =
-// sc1 (with sc0 clear: device scope).
-constexpr int kScopeDevice = 16;
 
 template <int BN> struct SplitCfg {
   static_assert(BN == 128 || BN == 64, "column block");
@@ -342,12 +339,10 @@ __global__ __launch_bounds__(256, 1) void skinny_split_kernel(SplitParams p) {
       // Device-scope (sc1) stores: written through to the device's
       // coherence point, so the release below has no dirty L2 lines of
       // them to write back (35.4 against 37.4 us at 128 x 8192 x 8192).
-      const __amdgpu_buffer_rsrc_t mine = __builtin_amdgcn_make_buffer_rsrc(
-          p.slots + (size_t)id * X::SLOT, 0, X::SLOT * 4, 0x00020000);
+      const __amdgpu_buffer_rsrc_t mine = coherent_rsrc(p.slots + (size_t)id * X::SLOT, X::SLOT * 4);
 #pragma unroll
       for (int g2 = 0; g2 < NG; ++g2)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, group(g2)), mine,
-                                               (g2 * 256 + threadIdx.x) * 16, 0, kScopeDevice);
+        coherent_store16(mine, (g2 * 256 + threadIdx.x) * 16, group(g2));
       // Every wave's partial stores are acknowledged at the coherence
       // point before the barrier, so thread 0's count, issued after it,
       // needs no release (whose L2 write-back measured 1-4 us a launch):
@@ -379,8 +374,8 @@ __global__ __launch_bounds__(256, 1) void skinny_split_kernel(SplitParams p) {
     // acknowledged at before their counts, and no acquire (an L2
     // invalidate, 1-3 us a launch) is needed; the barrier above issues
     // them after thread 0 has seen every count.
-    const __amdgpu_buffer_rsrc_t peers = __builtin_amdgcn_make_buffer_rsrc(
-        p.slots + (size_t)tile * p.splits * X::SLOT, 0, p.splits * X::SLOT * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t peers =
+        coherent_rsrc(p.slots + (size_t)tile * p.splits * X::SLOT, p.splits * X::SLOT * 4);
     f32x4 x[kXMaxSplits - 1][NG];
 #pragma unroll
     for (int o = 0; o < kXMaxSplits - 1; ++o) {
@@ -388,10 +383,8 @@ __global__ __launch_bounds__(256, 1) void skinny_split_kernel(SplitParams p) {
         const int c = o + (o >= split ? 1 : 0);
 #pragma unroll
         for (int g2 = 0; g2 < NG; ++g2)
-          x[o][g2] = __builtin_bit_cast(
-              f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                         peers, ((uint32_t)c * (X::SLOT / 4) + g2 * 256 + threadIdx.x) * 16, 0,
-                         kScopeDevice));
+          x[o][g2] = coherent_load16(
+              peers, ((uint32_t)c * (X::SLOT / 4) + g2 * 256 + threadIdx.x) * 16);
       }
     }
     // Sum in split order; contributor c is this CTA's own (c == split) or

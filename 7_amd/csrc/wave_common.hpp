@@ -151,6 +151,35 @@ template <int VMCNT = 0> __device__ __forceinline__ void vm_wait_barrier() {
                : "memory");
 }
 
+// Device-coherent 16-byte loads and stores through a buffer resource over
+// [base, base + bytes).  Cache policy sc1 (sc0 clear) is what gfx950 gives
+// agent-scope atomic accesses: they read and write the device's coherence
+// point, never a stale or dirty line of one XCD's L2, so data that CTAs on
+// different XCDs exchange within a launch this way needs no L2 write-back
+// (release) or invalidate (acquire) around it -- only the waits that order
+// the accesses: the writer's vmcnt(0) before it signals, the reader's loads
+// issued after it has seen the signal.
+constexpr int kCoherentDevice = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void *base,
+                                                                uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, 0x00020000);
+}
+// The byte offset is voff (per lane, range-checked against `bytes`) plus
+// soff (wave-uniform, an SGPR or constant; not range-checked, so callers
+// keep voff + soff inside the buffer by construction).  Splitting a
+// per-thread base from a per-access constant keeps one offset VGPR for a
+// whole run of accesses.
+__device__ __forceinline__ f32x4 coherent_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                                 uint32_t soff = 0) {
+  return __builtin_bit_cast(
+      f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kCoherentDevice));
+}
+__device__ __forceinline__ void coherent_store16(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                                 f32x4 v, uint32_t soff = 0) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, voff, soff,
+                                         kCoherentDevice);
+}
+
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
