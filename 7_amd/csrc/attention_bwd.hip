@@ -14,7 +14,8 @@
 // torch autograd.
 //
 // Three kernels, deterministic (no atomics):
-//  * bwd_delta_kernel: delta[row] = sum_d dO[row][d] * O[row][d] in fp32.
+//  * bwd_delta_kernel: -delta[row] = -sum_d dO[row][d] * O[row][d] in fp32
+//    (into the caller's scratch).
 //  * bwd_kv_kernel: one CTA (4 waves) per 64-key block of one KV head; it
 //    loops over the query blocks of every q head of the group (causal: the
 //    blocks at or after the key block) and accumulates dK, dV in registers.
@@ -66,49 +67,91 @@ struct BwdParams {
   float inv_scale;    // 1 / scale
 };
 
-// acc += A[32 rows][K] * B^T with A rows a0 .. a0+31 of a ROWB-byte-row LDS
-// tile, K = 16 * NK, and B as per-slice register fragments bf[kk] (lane l:
-// row l % 32 of B, elements 16 kk + 8 (l / 32) .. +8).
-template <int DT, int NK, int ROWB>
-__device__ __forceinline__ void mma_nt_reg(f32x16 &acc, const uint8_t *A, uint32_t a0,
-                                           const u32x4 (&bf)[NK]) {
+// Two NT products over K = 128 that share their A rows: c0 += A0 . b0^T and
+// c1 += A1 . b1^T, with A rows a0 .. a0+31 of two [rows][128] 16-bit LDS
+// tiles (256-byte rows) and B as per-slice register fragments (lane l: row
+// l % 32 of B, elements 16 kk + 8 (l / 32) .. +8).  The two accumulation
+// chains alternate (each MFMA's predecessor on its chain is two MFMAs
+// back), and each A fragment is read kPF slices ahead of its MFMA.
+constexpr int kPF = 2;
+template <int DT>
+__device__ __forceinline__ void mma2_nt_reg(f32x16 &c0, const uint8_t *A0, const u32x4 (&b0)[8],
+                                            f32x16 &c1, const uint8_t *A1, const u32x4 (&b1)[8],
+                                            uint32_t a0) {
   const uint32_t lane = threadIdx.x & 63, ra = a0 + (lane & 31);
-  const uint32_t s = (lane >> 5) ^ swz<ROWB>(ra);
+  const uint32_t sw = (lane >> 5) ^ swz<256>(ra);
+  auto frag = [&](const uint8_t *A, int kk) {
+    return *reinterpret_cast<const u32x4 *>(A + ra * 256 + (((2u * kk) ^ sw) << 4));
+  };
+  u32x4 f0[8], f1[8];
 #pragma unroll
-  for (int kk = 0; kk < NK; ++kk) {
-    const u32x4 a = *reinterpret_cast<const u32x4 *>(A + ra * ROWB + (((2u * kk) ^ s) << 4));
-    acc = mfma32x32x16<DT>(a, bf[kk], acc);
+  for (int kk = 0; kk < kPF; ++kk) {
+    f0[kk] = frag(A0, kk);
+    f1[kk] = frag(A1, kk);
+  }
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    if (kk + kPF < 8) {
+      f0[kk + kPF] = frag(A0, kk + kPF);
+      f1[kk + kPF] = frag(A1, kk + kPF);
+    }
+    c0 = mfma32x32x16<DT>(f0[kk], b0[kk], c0);
+    c1 = mfma32x32x16<DT>(f1[kk], b1[kk], c1);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
-// acc += A[32 rows][K] * R[K][32 columns], K = 16 * NK, with A rows
-// a0 .. a0+31 of a 128-byte-row LDS tile and R a row-major [K][128] tile of
-// 256-byte rows (columns c0 .. c0+31): the B operand comes from R by
-// transposing reads (ds_read_b64_tr_b16: in each 16-lane group source lane
-// 4a + p addresses R[k + a][c + 4p .. +3] and lane i then holds
-// R[k .. k+3][c + i]), so no transposed copy of R is needed.  Lane l reads
-// rows 16 kk + 8 (l / 32) + 4 r + (l >> 2) % 4, columns c0 + 16 ((l >> 4) % 2)
-// + 4 (l % 4), r = 0, 1: the 8 K values of the B fragment, in order.
-template <int DT, int NK>
-__device__ __forceinline__ void mma_nt_tr(f32x16 &acc, const uint8_t *A, uint32_t a0,
-                                          const uint8_t *R, uint32_t c0) {
+// The B operand of a gradient product from a row-major [K][128] 16-bit LDS
+// tile R of 256-byte rows, columns c0 .. c0+31, slice kk (K rows 16 kk ..
+// 16 kk + 15), by transposing reads (ds_read_b64_tr_b16: in each 16-lane
+// group source lane 4a + p addresses R[k + a][c + 4p .. +3] and lane i then
+// holds R[k .. k+3][c + i]).  Lane l reads rows 16 kk + 8 (l / 32) + 4 r +
+// (l >> 2) % 4, columns c0 + 16 ((l >> 4) % 2) + 4 (l % 4), r = 0, 1: the 8
+// K values of its B fragment, in order.  So no transposed copy of R is
+// needed.
+__device__ __forceinline__ u32x4 tr_frag(uint32_t rbase, int kk, uint32_t c0) {
   typedef short s4 __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) s4 lds_s4;
-  const uint32_t lane = threadIdx.x & 63, ra = a0 + (lane & 31);
-  const uint32_t sa = (lane >> 5) ^ swz<128>(ra);
-  const uint32_t rb = 8 * (lane >> 5) + ((lane >> 2) & 3);
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t rb = 16 * kk + 8 * (lane >> 5) + ((lane >> 2) & 3);
   const uint32_t cb = 2 * c0 + 32 * ((lane >> 4) & 1) + 8 * (lane & 3);
-  const uint32_t rbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)R;
+  const u32x2 lo = __builtin_bit_cast(
+      u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)(uintptr_t)(rbase + toff<256>(rb, cb))));
+  const u32x2 hi = __builtin_bit_cast(
+      u32x2,
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4 *)(uintptr_t)(rbase + toff<256>(rb + 4, cb))));
+  return u32x4{lo[0], lo[1], hi[0], hi[1]};
+}
+
+// 2 NT gradient chains over K = 64 (4 slices): for tile pair i < NT and
+// t = 0, 1, acc[2i + t] += A_i . R_i[:, c_t .. c_t + 31], with A_i rows
+// a0 .. a0+31 of a 128-byte-row LDS tile and R_i a row-major [64][128] LDS
+// tile read transposed (tr_frag).  Steps (slice kk, pair i) run in order,
+// two MFMAs each, and the fragments of step n + 1 are read before the MFMAs
+// of step n.
+template <int DT, int NT>
+__device__ __forceinline__ void mma_grad(f32x16 (&acc)[2 * NT], const uint8_t *const (&A)[NT],
+                                         uint32_t a0, const uint8_t *const (&R)[NT],
+                                         uint32_t c0, uint32_t c1) {
+  const uint32_t lane = threadIdx.x & 63, ra = a0 + (lane & 31);
+  const uint32_t sw = (lane >> 5) ^ swz<128>(ra);
+  constexpr int NS = 4 * NT;
+  u32x4 fa[2], fb[2][2];
+  auto load = [&](int n, int slot) {
+    const int kk = n / NT, i = n % NT;
+    fa[slot] = *reinterpret_cast<const u32x4 *>(A[i] + ra * 128 + (((2u * kk) ^ sw) << 4));
+    fb[slot][0] = tr_frag(lds_addr(R[i]), kk, c0);
+    fb[slot][1] = tr_frag(lds_addr(R[i]), kk, c1);
+  };
+  load(0, 0);
 #pragma unroll
-  for (int kk = 0; kk < NK; ++kk) {
-    const u32x4 a = *reinterpret_cast<const u32x4 *>(A + ra * 128 + (((2u * kk) ^ sa) << 4));
-    const u32x2 lo = __builtin_bit_cast(
-        u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                   (lds_s4 *)(uintptr_t)(rbase + toff<256>(16 * kk + rb, cb))));
-    const u32x2 hi = __builtin_bit_cast(
-        u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                   (lds_s4 *)(uintptr_t)(rbase + toff<256>(16 * kk + rb + 4, cb))));
-    acc = mfma32x32x16<DT>(a, u32x4{lo[0], lo[1], hi[0], hi[1]}, acc);
+  for (int n = 0; n < NS; ++n) {
+    if (n + 1 < NS)
+      load(n + 1, (n + 1) & 1);
+    const int i = n % NT;
+    acc[2 * i] = mfma32x32x16<DT>(fa[n & 1], fb[n & 1][0], acc[2 * i]);
+    acc[2 * i + 1] = mfma32x32x16<DT>(fa[n & 1], fb[n & 1][1], acc[2 * i + 1]);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -171,8 +214,8 @@ __device__ __forceinline__ void store_tile32(uint16_t *dst, int row0, int col0, 
 
 } // namespace
 
-// delta[row] = sum_d dO[row][d] * O[row][d]; 16 lanes per row, 8 elements
-// a lane.
+// delta[row] = -sum_d dO[row][d] * O[row][d] (stored negated: it is the
+// start value of the dP accumulators); 16 lanes per row, 8 elements a lane.
 template <int DT>
 __global__ __launch_bounds__(256) void bwd_delta_kernel(BwdParams p, int rows) {
   const int row = (int)(blockIdx.x * 16 + (threadIdx.x >> 4));
@@ -191,7 +234,7 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(BwdParams p, int rows) {
   for (int m = 8; m >= 1; m >>= 1)
     s += __shfl_xor(s, m, 16);
   if (row < rows && c == 0)
-    p.delta[row] = s;
+    p.delta[row] = -s;
 }
 
 // dK, dV of one 64-key block of one KV head.
@@ -216,54 +259,67 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdParams p) {
   u32x4 kf[8], vf[8];
   load_frags(p.K + kv_off + (size_t)(kh2 * 32 + (lane & 31)) * kBD, kf);
   load_frags(p.V + kv_off + (size_t)(kh2 * 32 + (lane & 31)) * kBD, vf);
-  f32x16 dv[2] = {f32x16{}, f32x16{}}, dk[2] = {f32x16{}, f32x16{}};
+  // Gradient accumulators: dV columns (2 dq) * 32 and (2 dq + 1) * 32, then
+  // dK's.
+  f32x16 g[4] = {f32x16{}, f32x16{}, f32x16{}, f32x16{}};
   const int key = kb * kBlk + kh2 * 32 + (int)(lane & 31);
-  // Work items: (q head of the group, query block), flattened; the next
-  // item's Q and dO rows are fetched while this one's products run.
-  const int qb0 = CAUSAL ? kb : 0, nq = nb - qb0, items = group * nq;
-  auto q_offset = [&](int it) {
-    const size_t bh = (size_t)b * p.q_heads + hkv * group + it / nq;
-    return (bh * p.seq + (size_t)(qb0 + it % nq) * kBlk) * kBD;
+  // Work items: (q head h of the group, query block qb), h major (causal:
+  // the blocks at or after the key block); the next item's Q and dO rows
+  // and its lse / delta are fetched while this one's products run.
+  const int qb0 = CAUSAL ? kb : 0, items = group * (nb - qb0);
+  auto rows_of = [&](int h, int q) {  // first row of item (h, q) in [B*Hq*S]
+    return ((size_t)b * p.q_heads + (size_t)hkv * group + h) * p.seq + (size_t)q * kBlk;
   };
+  // This wave's score rows of an item: lse and -delta of rows
+  // qh2*32 + 8 g + 4 (l / 32) + e as the accumulators' start values.
+  f32x16 s, dp;
+  auto load_stats = [&](size_t rb) {
+    const size_t r0 = rb + qh2 * 32 + 4 * (lane >> 5);
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const f32x4 a = *reinterpret_cast<const f32x4 *>(p.lse + r0 + 8 * g4);
+      const f32x4 d = *reinterpret_cast<const f32x4 *>(p.delta + r0 + 8 * g4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s[4 * g4 + e] = a[e];
+        dp[4 * g4 + e] = d[e];
+      }
+    }
+  };
+  int h = 0, qb = qb0;
   BlockRegs rq, rdo;
-  rq.fetch(p.Q + q_offset(0));
-  rdo.fetch(p.dO + q_offset(0));
+  rq.fetch(p.Q + rows_of(0, qb0) * kBD);
+  rdo.fetch(p.dO + rows_of(0, qb0) * kBD);
+  load_stats(rows_of(0, qb0));
   for (int it = 0; it < items; ++it) {
-    const int qb = qb0 + it % nq;
-    const size_t row_base = q_offset(it) / kBD;  // bh * seq + qb * 64
+    int hn = h, qbn = qb + 1;
+    if (qbn == nb) {
+      qbn = qb0;
+      ++hn;
+    }
+    const bool more = it + 1 < items;
     __syncthreads();  // the previous item's readers are done
     rq.put(sQ);
     rdo.put(sdO);
-    if (it + 1 < items) {
-      rq.fetch(p.Q + q_offset(it + 1));
-      rdo.fetch(p.dO + q_offset(it + 1));
+    if (more) {
+      rq.fetch(p.Q + rows_of(hn, qbn) * kBD);
+      rdo.fetch(p.dO + rows_of(hn, qbn) * kBD);
     }
-    // The score accumulator starts at -lse / scale and dP's at -delta
-    // (per query row), so exp2(c * s) = P and dp = dP - delta after the
-    // products.
-    f32x16 s, dp;
-    const size_t row0 = row_base + qh2 * 32 + 4 * (lane >> 5);
+    // The score accumulator starts at -lse / scale and dP's at -delta, so
+    // exp2(c * s) = P and dp = dP - delta after the products.
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const f32x4 a = *reinterpret_cast<const f32x4 *>(p.lse + row0 + 8 * g);
-      const f32x4 d = *reinterpret_cast<const f32x4 *>(p.delta + row0 + 8 * g);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        s[4 * g + e] = -a[e] * p.inv_scale;
-        dp[4 * g + e] = -d[e];
-      }
-    }
+    for (int r = 0; r < 16; ++r)
+      s[r] *= -p.inv_scale;
     __syncthreads();
-    mma_nt_reg<DT, 8, 256>(s, sQ, qh2 * 32, kf);
-    mma_nt_reg<DT, 8, 256>(dp, sdO, qh2 * 32, vf);
+    mma2_nt_reg<DT>(s, sQ, kf, dp, sdO, vf, qh2 * 32);
     // P and dS; P^T / dS^T rows = keys, 4 consecutive queries per store.
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
+    for (int g4 = 0; g4 < 4; ++g4) {
       float pv[4], dsv[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int r = 4 * g + e;
-        const int q = qb * kBlk + qh2 * 32 + 8 * g + 4 * (int)(lane >> 5) + e;
+        const int r = 4 * g4 + e;
+        const int q = qb * kBlk + qh2 * 32 + 8 * g4 + 4 * (int)(lane >> 5) + e;
         float pr = __builtin_amdgcn_exp2f(s[r] * p.scale_log2);
         if (CAUSAL && key > q)
           pr = 0.f;
@@ -271,23 +327,25 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdParams p) {
         dsv[e] = pr * dp[r];
       }
       const uint32_t off =
-          toff<128>(kh2 * 32 + (lane & 31), 2 * (qh2 * 32 + 8 * g + 4 * (lane >> 5)));
+          toff<128>(kh2 * 32 + (lane & 31), 2 * (qh2 * 32 + 8 * g4 + 4 * (lane >> 5)));
       *reinterpret_cast<u32x2 *>(sPt + off) = u32x2{pack2<DT>(pv[0], pv[1]), pack2<DT>(pv[2], pv[3])};
       *reinterpret_cast<u32x2 *>(sdSt + off) =
           u32x2{pack2<DT>(dsv[0], dsv[1]), pack2<DT>(dsv[2], dsv[3])};
     }
     __syncthreads();
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      mma_nt_tr<DT, 4>(dv[t], sPt, kh * 32, sdO, (2 * dq + t) * 32);
-      mma_nt_tr<DT, 4>(dk[t], sdSt, kh * 32, sQ, (2 * dq + t) * 32);
-    }
+    const uint8_t *const ga[2] = {sPt, sdSt};
+    const uint8_t *const gr[2] = {sdO, sQ};
+    mma_grad<DT, 2>(g, ga, kh * 32, gr, (2 * dq) * 32, (2 * dq + 1) * 32);
+    if (more)
+      load_stats(rows_of(hn, qbn));
+    h = hn;
+    qb = qbn;
   }
   uint16_t *dK = p.dK + kv_off, *dV = p.dV + kv_off;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    store_tile32<DT>(dV, kh * 32, (2 * dq + t) * 32, dv[t], 1.f);
-    store_tile32<DT>(dK, kh * 32, (2 * dq + t) * 32, dk[t], p.scale);
+    store_tile32<DT>(dV, kh * 32, (2 * dq + t) * 32, g[t], 1.f);
+    store_tile32<DT>(dK, kh * 32, (2 * dq + t) * 32, g[2 + t], p.scale);
   }
 }
 
@@ -314,7 +372,7 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdParams p) {
   load_frags(p.dO + q_off + (size_t)(qh2 * 32 + (lane & 31)) * kBD, dof);
   const int q = qb * kBlk + qh2 * 32 + (int)(lane & 31);
   const size_t row = (size_t)bh * p.seq + q;
-  const float l2 = p.lse[row] * kLog2eB, dl = p.delta[row];
+  const float l2 = p.lse[row] * kLog2eB, ndl = p.delta[row];  // -delta
   f32x16 dqa[2] = {f32x16{}, f32x16{}};
   const size_t kv_base = (size_t)(b * p.kv_heads + hkv) * p.seq * kBD;
   const int kb_end = CAUSAL ? qb + 1 : nb;
@@ -331,8 +389,7 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdParams p) {
     }
     __syncthreads();
     f32x16 st = {}, dpt = {};
-    mma_nt_reg<DT, 8, 256>(st, sK, kh2 * 32, qf);
-    mma_nt_reg<DT, 8, 256>(dpt, sV, kh2 * 32, dof);
+    mma2_nt_reg<DT>(st, sK, qf, dpt, sV, dof, kh2 * 32);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       float dsv[4];
@@ -343,7 +400,7 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdParams p) {
         float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(st[r], p.scale_log2, -l2));
         if (CAUSAL && key > q)
           pr = 0.f;
-        dsv[e] = pr * (dpt[r] - dl);
+        dsv[e] = pr * (dpt[r] + ndl);
       }
       // dS row q, 4 consecutive keys.
       const uint32_t off =
@@ -352,9 +409,9 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdParams p) {
           u32x2{pack2<DT>(dsv[0], dsv[1]), pack2<DT>(dsv[2], dsv[3])};
     }
     __syncthreads();
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-      mma_nt_tr<DT, 4>(dqa[t], sdS, qh * 32, sK, (2 * dq + t) * 32);
+    const uint8_t *const ga[1] = {sdS};
+    const uint8_t *const gr[1] = {sK};
+    mma_grad<DT, 1>(dqa, ga, qh * 32, gr, (2 * dq) * 32, (2 * dq + 1) * 32);
   }
   uint16_t *dQ = p.dQ + q_off;
 #pragma unroll

@@ -298,6 +298,27 @@ def mxfp8_fa_lines(wave, torch, dev, steps, warmup):
     return lines
 
 
+def fa_bwd_line(wave, torch, dev, steps):
+    """Flash-attention backward (no reference counterpart) on the FA forward's
+    benchmark shape B4 H32 S4096 D128 f16, non-causal: delta, dK/dV and dQ
+    kernels; FLOPs counted as flash-attention does, 2.5 x the forward's (five
+    S x S x D products)."""
+    B, H, S, D = 4, 32, 4096, 128
+    g = torch.Generator(device="cpu").manual_seed(11)
+    q, k, v, do = (torch.randn((B, H, S, D), generator=g).to(torch.float16).to(dev)
+                   for _ in range(4))
+    o, lse = wave.flash_attention_lse(q, k, v)
+    bw_ms = time_launches(lambda: wave.flash_attention_bwd(q, k, v, o, do, lse), steps, 1,
+                          torch)
+    bw_tf = 10.0 * B * H * S * S * D / (bw_ms * 1e-3) / 1e12
+    log(f"fa bwd f16 B4 H32 S4096 D128: {bw_ms * 1e3:.1f} us/launch, {bw_tf:.1f} TFLOP/s "
+        f"({100 * bw_tf / MFMA_PEAK_TFLOPS:.1f}%)")
+    return {"workload": "fa_bwd_f16_b4_h32_s4096_d128_noncausal",
+            "value": round(bw_tf, 2), "unit": "TFLOP/s", "ms_per_step": round(bw_ms, 4),
+            "frac_of_mfma_peak": round(bw_tf / MFMA_PEAK_TFLOPS, 4),
+            "flops": "10*B*H*S^2*D"}
+
+
 def config_lines(wave, torch, dev, steps, warmup):
     """BASELINE.json configs 3 (ragged / skinny bf16 GEMMs, entries N(0,1)
     scaled by 1/sqrt(K), bf16 in and out, fp32 accumulate) and 5 (causal GQA
@@ -400,11 +421,12 @@ def main():
     ap.add_argument("--no-ref-compare", action="store_true",
                     help="skip the runs on the reference's published input modes / shapes")
     ap.add_argument("--workload",
-                    choices=["all", "gemm", "fa", "mxfp4", "mxfp8fa", "copy", "configs"],
+                    choices=["all", "gemm", "fa", "fabwd", "mxfp4", "mxfp8fa", "copy",
+                             "configs"],
                     default="all",
-                    help="gemm / fa / mxfp4 / mxfp8fa: run only that kernel (for profiler "
-                         "passes); copy: a 1 GiB device copy used to calibrate rocprofv3 byte "
-                         "counters")
+                    help="gemm / fa / fabwd / mxfp4 / mxfp8fa: run only that kernel (for "
+                         "profiler passes); copy: a 1 GiB device copy used to calibrate "
+                         "rocprofv3 byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -426,8 +448,11 @@ def main():
         ms = time_launches(lambda: dst.copy_(src), args.steps, args.warmup, torch)
         log(f"copy 1 GiB: {ms:.3f} ms, {2 * 4 * src.numel() / (ms * 1e-3) / 1e9:.0f} GB/s")
         return
-    if args.workload in ("fa", "mxfp4", "mxfp8fa", "configs"):
+    if args.workload in ("fa", "fabwd", "mxfp4", "mxfp8fa", "configs"):
         args.no_cpu = True
+    if args.workload == "fabwd":
+        print(json.dumps(fa_bwd_line(wave, torch, dev, args.steps)), flush=True)
+        return
     if args.workload == "mxfp4":
         m = mxfp4_line(wave, torch, dev, args.steps, args.warmup)
         print(json.dumps(m), flush=True)
@@ -473,24 +498,9 @@ def main():
                           "value": round(fa_tf, 2), "unit": "TFLOP/s",
                           "ms_per_step": round(fa_ms, 4),
                           "frac_of_mfma_peak": round(fa_tf / MFMA_PEAK_TFLOPS, 4)})
-        if args.workload == "all":
-            # Backward (no reference counterpart) on the same shape: delta,
-            # dK/dV and dQ kernels; FLOPs counted as flash-attention does,
-            # 2.5 x the forward's (five S x S x D products).
-            o, lse = wave.flash_attention_lse(q, k, v)
-            do = torch.randn((B, H, S, D), generator=gq).to(torch.float16).to(dev)
-            bw_ms = time_launches(lambda: wave.flash_attention_bwd(q, k, v, o, do, lse), 5, 1,
-                                  torch)
-            bw_tf = 10.0 * B * H * S * S * D / (bw_ms * 1e-3) / 1e12
-            log(f"fa bwd f16 B4 H32 S4096 D128: {bw_ms * 1e3:.1f} us/launch, {bw_tf:.1f} TFLOP/s "
-                f"({100 * bw_tf / MFMA_PEAK_TFLOPS:.1f}%)")
-            secondary.append({"workload": "fa_bwd_f16_b4_h32_s4096_d128_noncausal",
-                              "value": round(bw_tf, 2), "unit": "TFLOP/s",
-                              "ms_per_step": round(bw_ms, 4),
-                              "frac_of_mfma_peak": round(bw_tf / MFMA_PEAK_TFLOPS, 4),
-                              "flops": "10*B*H*S^2*D"})
-            del do, lse
         del q, k, v, o
+        if args.workload == "all":
+            secondary.append(fa_bwd_line(wave, torch, dev, 5))
 
     if args.workload in ("all", "configs"):
         secondary.extend(config_lines(wave, torch, dev, max(10, args.steps // 2), 3))
