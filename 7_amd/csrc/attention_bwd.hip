@@ -47,9 +47,16 @@ constexpr int kWide = kBlk * 256;      // [64][128] 16-bit tile: 16 KiB
 constexpr int kNarrowS = kBlk * 128;   // [64][64] tile: 8 KiB
 constexpr float kLog2eB = 1.4426950408889634f;
 
-// Byte offset of (row r, byte b) in a tile of ROWB-byte rows.
+// Byte offset of (row r, byte b) in a tile of ROWB-byte rows: 16-byte chunk
+// c of row r at c ^ swz(r).  256-byte rows: swz(r) = 4 (r % 4) + (r / 4) % 4,
+// under which both access patterns of these tiles are free of LDS bank
+// conflicts on gfx950 (measured: a 16-byte row-fragment read of 32
+// consecutive rows, and the transposing 8-byte reads of tr_frag, which
+// touch rows k .. k+3 and k+8 .. k+11 in one instruction; c ^ (r % 16)
+// served the first but made the second 2.6x slower).  128-byte rows:
+// swz(r) = (r / 2) % 8.
 template <int ROWB> __device__ __forceinline__ uint32_t swz(uint32_t r) {
-  return ROWB == 256 ? (r & 15u) : ((r >> 1) & 7u);
+  return ROWB == 256 ? (((r & 3u) << 2) | ((r >> 2) & 3u)) : ((r >> 1) & 7u);
 }
 template <int ROWB> __device__ __forceinline__ uint32_t toff(uint32_t r, uint32_t b) {
   return r * ROWB + ((((b >> 4) ^ swz<ROWB>(r))) << 4) + (b & 15u);
