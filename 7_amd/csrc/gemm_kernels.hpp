@@ -172,20 +172,20 @@ using Fp4ACfg = Fp4ACfgW<>;
 // "super-rows" of eight 16-byte slots: with BK = 64 super-row R is tile row
 // R; with BK = 32 it holds row R in slots 0-3 and row R + 128 in slots 4-7.
 // Logical slot lc of super-row R lives at physical slot lc ^ Geo<C>::swz(R).
-// rocprofv3 (SQ_LDS_BANK_CONFLICT, SQ_LDS_IDX_ACTIVE) on the fragment
-// reads, in the kernel and in a probe of single ds_read_b128 lane patterns:
-//  * 32x32 fragments (32 consecutive rows at one chunk) with
-//    swz_rr(R) = (R ^ R>>3) & 7: 4 LDS cycles per read, no conflict;
-//  * 16x16 fragments (16 consecutive rows x 4 chunks): 8 cycles per read,
-//    half of them conflict cycles, with every slot permutation tried
-//    (swz_rr, two others chosen to separate the chunks of each row class,
-//    no swizzle: 16).
-// swz_16(R) = 2*((R>>2)&3) + ((R>>4)&1) gives the 16x16 path no fewer LDS
-// cycles but measured 1-3 % faster than swz_rr there (8192^3 f16
-// 1282-1287 -> 1314 TFLOP/s, bf16 1353-1360 -> 1365-1382, same box), while
-// it costs 32x32 fragments a 2-way conflict; so each MFMA shape has its own.
+// Fragment reads, timed by a probe that repeats one ds_read_b128 lane
+// pattern from precomputed addresses (ns per wave access per CU; a linear
+// 1 KiB read: 2.0):
+//  * 32x32 fragments (32 consecutive rows at one chunk): swz_rr(R) =
+//    (R ^ R>>3) & 7 1.92, (R >> 1) & 7 1.82 (rocprofv3: 4 LDS cycles per
+//    read, no conflict);
+//  * 16x16 fragments (16 consecutive rows x 4 chunks): (R >> 1) & 7 1.77
+//    (conflict-free), swz_rr 3.39, 2*((R>>2)&3) + ((R>>4)&1) (the previous
+//    16x16 swizzle) 3.49, none 6.70.  With 64 banks of 4 bytes, rows R and
+//    R + 2 of 128 bytes fall on the same banks, so a swizzle has to differ
+//    between them: (R >> 1) & 7 gives the 16 rows 16 distinct 16-byte bank
+//    groups.  8192^3 f16 with it: +0.5 % (wave-bench, same box, 3 passes).
 __device__ __forceinline__ uint32_t swz_rr(uint32_t R) { return (R ^ (R >> 3)) & 7u; }
-__device__ __forceinline__ uint32_t swz_16(uint32_t R) { return ((R >> 1) & 6u) | ((R >> 4) & 1u); }
+__device__ __forceinline__ uint32_t swz_16(uint32_t R) { return (R >> 1) & 7u; }
 
 template <class C> struct Geo {
   static __device__ __forceinline__ uint32_t swz(uint32_t R) {
