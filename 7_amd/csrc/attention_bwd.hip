@@ -16,23 +16,27 @@
 // Three kernels, deterministic (no atomics):
 //  * bwd_delta_kernel: -delta[row] = -sum_d dO[row][d] * O[row][d] in fp32
 //    (into the caller's scratch).
-//  * bwd_kv_kernel: one CTA (4 waves) per 64-key block of one KV head; it
-//    loops over the query blocks of every q head of the group (causal: the
-//    blocks at or after the key block) and accumulates dK, dV in registers.
+//  * bwd_kv_pp_kernel (seq a multiple of 128): one CTA (8 waves, two groups
+//    of 4 one segment apart) per 128-key block of one KV head; it loops over
+//    the query blocks of every q head of the group (causal: the blocks at or
+//    after the key block), with each block's Q, dO, lse and -delta arriving
+//    by LDS DMA, and accumulates dK, dV in registers.  bwd_kv_kernel (one
+//    CTA of 4 waves per 64-key block, Q and dO staged through registers)
+//    covers seq = 64 (mod 128).
 //  * bwd_q_kernel: one CTA per 64-query block of one q head; it loops over
 //    the key blocks (causal: up to the diagonal) and accumulates dQ.
 // Every product is an "NT" product C[m][n] = sum_k A[m][k] B[n][k] of 32x32
 // tiles on v_mfma_f32_32x32x16.  The operands fixed for a CTA (K, V in the
-// dK/dV kernel; Q, dO in the dQ kernel) are held as MFMA fragments in
+// dK/dV kernels; Q, dO in the dQ kernel) are held as MFMA fragments in
 // registers; the rest are read as 16-byte row chunks from LDS.  Operands
 // needed K-contiguous the other way (Q^T, dO^T, K^T as the B operand of
 // dK, dV, dQ) are read from the row-major Q, dO, K tiles by transposing LDS
 // reads (ds_read_b64_tr_b16), and P^T / dS^T (dS for dQ) go through LDS
 // between the score products and the gradient products.  LDS tiles are
-// unpadded with XOR-swizzled 16-byte chunks (256-byte rows: chunk c of row
-// r at c ^ (r % 16); 128-byte rows: at c ^ ((r / 2) % 8)), so that 16
-// consecutive rows read at one chunk cover all 16 bank groups: 48 KiB
-// (dK/dV) and 40 KiB (dQ) of LDS, two CTAs per CU (register-bound).
+// unpadded with XOR-swizzled 16-byte chunks (swz below), conflict-free for
+// every read these kernels make: 130 KiB (bwd_kv_pp_kernel, one CTA per
+// CU), 48 KiB (bwd_kv_kernel) and 40 KiB (dQ) of LDS, two CTAs per CU
+// (register-bound).
 #include "attention.hpp"
 #include "wave_common.hpp"
 
@@ -80,8 +84,7 @@ struct BwdParams {
 // l % 32 of B, elements 16 kk + 8 (l / 32) .. +8).  The two accumulation
 // chains alternate (each MFMA's predecessor on its chain is two MFMAs
 // back), and each A fragment is read kPF slices ahead of its MFMA.
-constexpr int kPF = 2;
-template <int DT>
+template <int DT, int kPF = 2>
 __device__ __forceinline__ void mma2_nt_reg(f32x16 &c0, const uint8_t *A0, const u32x4 (&b0)[8],
                                             f32x16 &c1, const uint8_t *A1, const u32x4 (&b1)[8],
                                             uint32_t a0) {
@@ -134,30 +137,32 @@ __device__ __forceinline__ u32x4 tr_frag(uint32_t rbase, int kk, uint32_t c0) {
 // t = 0, 1, acc[2i + t] += A_i . R_i[:, c_t .. c_t + 31], with A_i rows
 // a0 .. a0+31 of a 128-byte-row LDS tile and R_i a row-major [64][128] LDS
 // tile read transposed (tr_frag).  Steps (slice kk, pair i) run in order,
-// two MFMAs each, and the fragments of step n + 1 are read before the MFMAs
-// of step n.
-template <int DT, int NT>
+// two MFMAs each, and the fragments of step n + GPF are read before the
+// MFMAs of step n.
+template <int DT, int NT, int GPF = 1>
 __device__ __forceinline__ void mma_grad(f32x16 (&acc)[2 * NT], const uint8_t *const (&A)[NT],
                                          uint32_t a0, const uint8_t *const (&R)[NT],
                                          uint32_t c0, uint32_t c1) {
   const uint32_t lane = threadIdx.x & 63, ra = a0 + (lane & 31);
   const uint32_t sw = (lane >> 5) ^ swz<128>(ra);
-  constexpr int NS = 4 * NT;
-  u32x4 fa[2], fb[2][2];
+  constexpr int NS = 4 * NT, NB = GPF + 1;
+  u32x4 fa[NB], fb[NB][2];
   auto load = [&](int n, int slot) {
     const int kk = n / NT, i = n % NT;
     fa[slot] = *reinterpret_cast<const u32x4 *>(A[i] + ra * 128 + (((2u * kk) ^ sw) << 4));
     fb[slot][0] = tr_frag(lds_addr(R[i]), kk, c0);
     fb[slot][1] = tr_frag(lds_addr(R[i]), kk, c1);
   };
-  load(0, 0);
+#pragma unroll
+  for (int n = 0; n < GPF && n < NS; ++n)
+    load(n, n % NB);
 #pragma unroll
   for (int n = 0; n < NS; ++n) {
-    if (n + 1 < NS)
-      load(n + 1, (n + 1) & 1);
+    if (n + GPF < NS)
+      load(n + GPF, (n + GPF) % NB);
     const int i = n % NT;
-    acc[2 * i] = mfma32x32x16<DT>(fa[n & 1], fb[n & 1][0], acc[2 * i]);
-    acc[2 * i + 1] = mfma32x32x16<DT>(fa[n & 1], fb[n & 1][1], acc[2 * i + 1]);
+    acc[2 * i] = mfma32x32x16<DT>(fa[n % NB], fb[n % NB][0], acc[2 * i]);
+    acc[2 * i + 1] = mfma32x32x16<DT>(fa[n % NB], fb[n % NB][1], acc[2 * i + 1]);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -356,6 +361,173 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdParams p) {
   }
 }
 
+// dK, dV of a 128-key block of one KV head as two groups of four waves:
+// group g (waves 4g .. 4g+3) owns keys 64 g .. 64 g + 63 of the block and
+// does for them what bwd_kv_kernel does for its 64 keys (same wave roles,
+// same products), on the same work items.  The groups share each item's Q
+// and dO rows and its rows' lse and -delta, which arrive by LDS DMA into a
+// 3-buffer ring (so no global load is waited for inside the loop), and run
+// one segment apart ("ping-pong"), so that on every SIMD one wave's MFMAs
+// run next to the other group's softmax:
+//
+//   segment    2i              2i+1            2i+2
+//   group 0    M2(i-1) M1(i)   SM(i)           M2(i) M1(i+1)
+//   group 1    SM(i-1)         M2(i-1) M1(i)   SM(i)
+//
+// M1(i): S and dP of item i (A fragments from its Q / dO buffer); SM(i): P
+// and dS of item i into the group's P^T / dS^T tiles; M2(i): dV, dK += the
+// products of those tiles with Q / dO of item i (transposing reads).  Every
+// segment ends with a workgroup barrier (2 * items + 2 of them for every
+// wave).  Buffers: item i's Q / dO sit in ring slot i % 3, read from
+// segment 2i (group 0's M1(i)) to 2i+3 (group 1's M2(i)); all waves issue
+// the DMA of item j+1 at the start of segment 2j, after slot (j+1) % 3's
+// previous item (j-2) was last read in segment 2j-1, and wait for it at the
+// end of segment 2j+1.  A group's P^T / dS^T are written in SM(i) and read
+// in M2(i), the next segment of that group.
+#ifndef WAVE_BWD_PF
+#define WAVE_BWD_PF 3  // score products: A fragments read this many slices ahead
+#endif
+#ifndef WAVE_BWD_GPF
+#define WAVE_BWD_GPF 2  // gradient products: fragments read this many steps ahead
+#endif
+template <int DT, bool CAUSAL>
+__global__ __launch_bounds__(512, 1) void bwd_kv_pp_kernel(BwdParams p) {
+  // One ring slot: an item's Q and dO rows (32 KiB), then its 64 rows' lse
+  // and -delta (256 B each).
+  constexpr uint32_t kStats = 2 * kWide, kQD = kStats + 512;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[3 * kQD + 4 * kNarrowS];
+  const int nb = p.seq / kBlk, nkb = nb / 2;
+  const int pid = xcd_pid((int)blockIdx.x, (int)gridDim.x);
+  const int kb2 = pid % nkb, bhk = pid / nkb;
+  const int b = bhk / p.kv_heads, hkv = bhk - b * p.kv_heads;
+  const int group = p.q_heads / p.kv_heads;
+  const uint32_t wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const uint32_t grp = wave >> 2, wg = wave & 3;
+  const int kb = 2 * kb2 + (int)grp;  // this group's 64-key block
+  const size_t kv_off = ((size_t)bhk * p.seq + (size_t)kb * kBlk) * kBD;
+  uint8_t *sPt = smem + 3 * kQD + grp * 2 * kNarrowS, *sdSt = sPt + kNarrowS;
+  const uint32_t lds0 = lds_addr(smem);
+  // Wave roles within the group, as in bwd_kv_kernel.
+  const int qh2 = wg & 1, kh2 = wg >> 1, kh = wg & 1, dq = wg >> 1;
+  u32x4 kf[8], vf[8];
+  load_frags(p.K + kv_off + (size_t)(kh2 * 32 + (lane & 31)) * kBD, kf);
+  load_frags(p.V + kv_off + (size_t)(kh2 * 32 + (lane & 31)) * kBD, vf);
+  f32x16 g[4] = {f32x16{}, f32x16{}, f32x16{}, f32x16{}};
+  const int key = kb * kBlk + kh2 * 32 + (int)(lane & 31);
+  // Work items (q head h, query block qb), h major; causal: the blocks at
+  // or after group 0's key block (group 1's first one is wholly masked).
+  const int qb0 = CAUSAL ? 2 * kb2 : 0, items = group * (nb - qb0);
+  struct Cursor {
+    int h, qb;
+  };
+  auto advance = [&](Cursor &c) {
+    if (++c.qb == nb) {
+      c.qb = qb0;
+      ++c.h;
+    }
+  };
+  auto rows_of = [&](const Cursor &c) {
+    return ((size_t)b * p.q_heads + (size_t)hkv * group + c.h) * p.seq + (size_t)c.qb * kBlk;
+  };
+  // DMA of an item into ring slot `slot`: wave w fills Q and dO rows
+  // 8w .. 8w+7 (two 1 KiB windows each), lane l row 4j + l / 16, slot l % 16,
+  // which holds chunk (l % 16) ^ swz(row); waves 0 and 1 add the rows' lse
+  // and -delta (256 B each, 4 bytes a lane).
+  auto dma_item = [&](const Cursor &c, uint32_t slot) {
+    const size_t rb = rows_of(c);
+    const uint32_t l = lds0 + slot * kQD;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t win = 2 * wave + j, r = 4 * win + (lane >> 4);
+      const uint32_t off = r * 256 + (((lane & 15) ^ swz<256>(r)) << 4);
+      dma16(l + win * 1024, p.Q + rb * kBD, off);
+      dma16(l + kWide + win * 1024, p.dO + rb * kBD, off);
+    }
+    if (wave < 2)
+      dma4(l + kStats + wave * 256, wave == 0 ? (const void *)(p.lse + rb) : (const void *)(p.delta + rb),
+           4 * lane);
+  };
+  f32x16 s, dp;
+  // This wave's score rows' lse and -delta (rows qh2*32 + 8 g + 4 (l / 32)
+  // + e) from the item's ring slot: the accumulators' start values.
+  auto load_stats = [&](const uint8_t *q) {
+    const float *r0 = reinterpret_cast<const float *>(q + kStats) + qh2 * 32 + 4 * (lane >> 5);
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const f32x4 a = *reinterpret_cast<const f32x4 *>(r0 + 8 * g4);
+      const f32x4 d = *reinterpret_cast<const f32x4 *>(r0 + 64 + 8 * g4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s[4 * g4 + e] = a[e];
+        dp[4 * g4 + e] = d[e];
+      }
+    }
+  };
+  Cursor dmac{0, qb0}, cur{0, qb0};
+  dma_item(dmac, 0);
+  advance(dmac);
+  vm_wait_barrier();
+  const int nseg = 2 * items + 2;
+  for (int sg = 0; sg < nseg; ++sg) {
+    if ((sg & 1) == 0 && (sg >> 1) + 1 < items) {
+      dma_item(dmac, (uint32_t)(((sg >> 1) + 1) % 3));
+      advance(dmac);
+    }
+    const int ls = sg - (int)grp;
+    if (ls >= 0 && ls <= 2 * items) {
+      const int i = ls >> 1;
+      if ((ls & 1) == 0) {
+        if (i >= 1) {  // M2(i-1)
+          const uint8_t *q = smem + ((i - 1) % 3) * kQD;
+          const uint8_t *const ga[2] = {sPt, sdSt};
+          const uint8_t *const gr[2] = {q + kWide, q};
+          mma_grad<DT, 2, WAVE_BWD_GPF>(g, ga, kh * 32, gr, (2 * dq) * 32, (2 * dq + 1) * 32);
+        }
+        if (i < items) {  // M1(i): S starts at -lse / scale, dP at -delta
+          const uint8_t *q = smem + (i % 3) * kQD;
+          load_stats(q);
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            s[r] *= -p.inv_scale;
+          mma2_nt_reg<DT, WAVE_BWD_PF>(s, q, kf, dp, q + kWide, vf, qh2 * 32);
+        }
+      } else {  // SM(i)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          float pv[4], dsv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * g4 + e;
+            const int q = cur.qb * kBlk + qh2 * 32 + 8 * g4 + 4 * (int)(lane >> 5) + e;
+            float pr = __builtin_amdgcn_exp2f(s[r] * p.scale_log2);
+            if (CAUSAL && key > q)
+              pr = 0.f;
+            pv[e] = pr;
+            dsv[e] = pr * dp[r];
+          }
+          const uint32_t off =
+              toff<128>(kh2 * 32 + (lane & 31), 2 * (qh2 * 32 + 8 * g4 + 4 * (lane >> 5)));
+          *reinterpret_cast<u32x2 *>(sPt + off) =
+              u32x2{pack2<DT>(pv[0], pv[1]), pack2<DT>(pv[2], pv[3])};
+          *reinterpret_cast<u32x2 *>(sdSt + off) =
+              u32x2{pack2<DT>(dsv[0], dsv[1]), pack2<DT>(dsv[2], dsv[3])};
+        }
+        advance(cur);
+      }
+    }
+    if (sg & 1)
+      vm_wait_barrier();  // the DMA of item (sg >> 1) + 1 has landed
+    else
+      lds_barrier();
+  }
+  uint16_t *dK = p.dK + kv_off, *dV = p.dV + kv_off;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    store_tile32<DT>(dV, kh * 32, (2 * dq + t) * 32, g[t], 1.f);
+    store_tile32<DT>(dK, kh * 32, (2 * dq + t) * 32, g[2 + t], p.scale);
+  }
+}
+
 // dQ of one 64-query block of one q head.
 template <int DT, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdParams p) {
@@ -433,8 +605,12 @@ hipError_t launch_bwd_dt(const BwdParams &p, hipStream_t stream) {
   hipLaunchKernelGGL((bwd_delta_kernel<DT>), dim3((rows + 15) / 16), dim3(256), 0, stream, p,
                      rows);
   const int nb = p.seq / kBlk;
-  hipLaunchKernelGGL((bwd_kv_kernel<DT, CAUSAL>), dim3(nb * p.batch * p.kv_heads), dim3(256), 0,
-                     stream, p);
+  if (nb % 2 == 0)
+    hipLaunchKernelGGL((bwd_kv_pp_kernel<DT, CAUSAL>), dim3(nb / 2 * p.batch * p.kv_heads),
+                       dim3(512), 0, stream, p);
+  else
+    hipLaunchKernelGGL((bwd_kv_kernel<DT, CAUSAL>), dim3(nb * p.batch * p.kv_heads), dim3(256),
+                       0, stream, p);
   hipLaunchKernelGGL((bwd_q_kernel<DT, CAUSAL>), dim3(nb * p.batch * p.q_heads), dim3(256), 0,
                      stream, p);
   return hipGetLastError();

@@ -50,8 +50,10 @@ def check(got, ref, dt):
 
 @pytest.mark.parametrize("dt", [1, 2])
 @pytest.mark.parametrize("causal", [False, True])
+# S % 128 == 0 runs the two-group dK/dV kernel (several 128-key blocks, GQA
+# and causal at 384), the other lengths the 64-key one.
 @pytest.mark.parametrize("B,Hq,Hkv,S", [(1, 2, 2, 64), (1, 2, 2, 256), (2, 4, 2, 192),
-                                         (1, 4, 1, 320)])
+                                         (1, 4, 1, 320), (2, 4, 2, 384)])
 def test_fa_bwd_parity(wave, oracle, dev, dt, causal, B, Hq, Hkv, S):
     got, ref = run_bwd(wave, oracle, dev, dt, B, Hq, Hkv, S, causal)
     check(got, ref, dt)
