@@ -531,14 +531,19 @@ __global__ __launch_bounds__(512, 1) void bwd_kv_pp_kernel(BwdParams p) {
 // dQ of one 64-query block of one q head.
 template <int DT, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kWide + kNarrowS];
-  uint8_t *sK = smem, *sV = sK + kWide, *sdS = sV + kWide;
+  // K and V rows of a key block arrive by LDS DMA into a 2-slot ring: the
+  // DMA of block kb + 1 goes into the slot block kb - 1 used, after the
+  // barrier that starts iteration kb, and is waited for at the barrier that
+  // starts iteration kb + 1.
+  constexpr uint32_t kKV = 2 * kWide;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kKV + kNarrowS];
+  uint8_t *sdS = smem + 2 * kKV;
   const int nb = p.seq / kBlk;
   const int pid = xcd_pid((int)blockIdx.x, (int)gridDim.x);
   const int qb = pid % nb, bh = pid / nb;
   const int b = bh / p.q_heads, hq = bh - b * p.q_heads;
   const int hkv = hq / (p.q_heads / p.kv_heads);
-  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t wave = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const size_t q_off = ((size_t)bh * p.seq + (size_t)qb * kBlk) * kBD;
   // Score tiles: wave w computes S^T[key][q] for key half w&1, q half w>>1;
   // lane l holds query qh2*32 + l%32 and keys kh2*32 + 8g + 4(l/32) + e.
@@ -555,18 +560,30 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdParams p) {
   f32x16 dqa[2] = {f32x16{}, f32x16{}};
   const size_t kv_base = (size_t)(b * p.kv_heads + hkv) * p.seq * kBD;
   const int kb_end = CAUSAL ? qb + 1 : nb;
-  BlockRegs rk, rv;
-  rk.fetch(p.K + kv_base);
-  rv.fetch(p.V + kv_base);
-  for (int kb = 0; kb < kb_end; ++kb) {
-    __syncthreads();
-    rk.put(sK);
-    rv.put(sV);
-    if (kb + 1 < kb_end) {
-      rk.fetch(p.K + kv_base + (size_t)(kb + 1) * kBlk * kBD);
-      rv.fetch(p.V + kv_base + (size_t)(kb + 1) * kBlk * kBD);
+  const uint32_t lds0 = lds_addr(smem);
+  // DMA of key block kb into ring slot kb % 2: wave w fills K and V rows
+  // 16w .. 16w+15 (four 1 KiB windows each), lane l row 4 win + l / 16,
+  // slot l % 16, which holds chunk (l % 16) ^ swz(row).
+  auto dma_block = [&](int kb) {
+    const size_t r0 = kv_base + (size_t)kb * kBlk * kBD;
+    const uint32_t l = lds0 + (kb & 1) * kKV;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t win = 4 * wave + j, r = 4 * win + (lane >> 4);
+      const uint32_t off = r * 256 + (((lane & 15) ^ swz<256>(r)) << 4);
+      dma16(l + win * 1024, p.K + r0, off);
+      dma16(l + kWide + win * 1024, p.V + r0, off);
     }
-    __syncthreads();
+  };
+  dma_block(0);
+  for (int kb = 0; kb < kb_end; ++kb) {
+    // Block kb's DMA has landed everywhere, and every wave is done with
+    // iteration kb - 1's LDS reads (of the slot block kb + 1 takes, and of
+    // dS, which this iteration rewrites).
+    vm_wait_barrier();
+    if (kb + 1 < kb_end)
+      dma_block(kb + 1);
+    const uint8_t *sK = smem + (kb & 1) * kKV, *sV = sK + kWide;
     f32x16 st = {}, dpt = {};
     mma2_nt_reg<DT>(st, sK, qf, dpt, sV, dof, kh2 * 32);
 #pragma unroll
