@@ -529,6 +529,12 @@ __global__ __launch_bounds__(512, 1) void bwd_kv_pp_kernel(BwdParams p) {
 }
 
 // dQ of one 64-query block of one q head.
+#ifndef WAVE_BWDQ_PF
+#define WAVE_BWDQ_PF 2  // score products: A fragments read this many slices ahead
+#endif
+#ifndef WAVE_BWDQ_GPF
+#define WAVE_BWDQ_GPF 1  // dQ product: fragments read this many steps ahead
+#endif
 template <int DT, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdParams p) {
   // K and V rows of a key block arrive by LDS DMA into a 2-slot ring: the
@@ -585,7 +591,7 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdParams p) {
       dma_block(kb + 1);
     const uint8_t *sK = smem + (kb & 1) * kKV, *sV = sK + kWide;
     f32x16 st = {}, dpt = {};
-    mma2_nt_reg<DT>(st, sK, qf, dpt, sV, dof, kh2 * 32);
+    mma2_nt_reg<DT, WAVE_BWDQ_PF>(st, sK, qf, dpt, sV, dof, kh2 * 32);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       float dsv[4];
@@ -607,7 +613,7 @@ __global__ __launch_bounds__(256, 2) void bwd_q_kernel(BwdParams p) {
     __syncthreads();
     const uint8_t *const ga[1] = {sdS};
     const uint8_t *const gr[1] = {sK};
-    mma_grad<DT, 1>(dqa, ga, qh * 32, gr, (2 * dq) * 32, (2 * dq + 1) * 32);
+    mma_grad<DT, 1, WAVE_BWDQ_GPF>(dqa, ga, qh * 32, gr, (2 * dq) * 32, (2 * dq + 1) * 32);
   }
   uint16_t *dQ = p.dQ + q_off;
 #pragma unroll
