@@ -343,6 +343,31 @@ def test_split_short_m_matches_unsplit(wave, oracle, dev, in_dt, out_dt, layout,
         assert torch.equal(got, ref)
 
 
+@pytest.mark.parametrize("shape,workers", [((2048, 2048, 8192), 128),   # 2 contributors
+                                           ((1024, 1024, 8192), 64),    # 4
+                                           ((1000, 1000, 8200), 128)])  # ragged, 8-9
+def test_streamk_alternating_inputs(wave, oracle, dev, shape, workers):
+    """Two different B on one Stream-K workspace, alternated launch after
+    launch: each output equals the tiled kernel's for its own B, so the last
+    arriver of a tile never reads a contributor's partial from an earlier
+    launch (partials are read with device-coherent loads)."""
+    M, N, K = shape
+    a = oracle.gemm_inputs(M, K, 1, 9, 0)
+    b0 = oracle.gemm_inputs(N, K, 1, 9, 1)
+    b1 = oracle.gemm_inputs(N, K, 1, 9, 2)
+    A = to_dev(a, torch.float16, dev)
+    Bs = [to_dev(b0, torch.float16, dev), to_dev(b1, torch.float16, dev)]
+    refs = [wave.gemm(A, B, out_dtype=torch.float32) for B in Bs]
+    assert not torch.equal(refs[0], refs[1])
+    ws = wave.StreamKWorkspace(M, N, workers, dev)
+    out = torch.empty_like(refs[0])
+    for i in range(16):
+        wave.gemm_streamk(A, Bs[i & 1], workers, out_dtype=torch.float32, workspace=ws, out=out)
+        torch.cuda.synchronize()
+        assert torch.equal(out, refs[i & 1]), i
+    assert ws.nonzero_counters() == 0
+
+
 @pytest.mark.parametrize("shape", [(128, 8192, 8192), (128, 4096, 8192), (100, 5000, 12288)])
 def test_split_short_m_alternating_inputs(wave, oracle, dev, shape):
     """Two different B on one workspace, alternated launch after launch: each
