@@ -313,10 +313,26 @@ def fa_bwd_line(wave, torch, dev, steps):
     bw_tf = 10.0 * B * H * S * S * D / (bw_ms * 1e-3) / 1e12
     log(f"fa bwd f16 B4 H32 S4096 D128: {bw_ms * 1e3:.1f} us/launch, {bw_tf:.1f} TFLOP/s "
         f"({100 * bw_tf / MFMA_PEAK_TFLOPS:.1f}%)")
-    return {"workload": "fa_bwd_f16_b4_h32_s4096_d128_noncausal",
+    line = {"workload": "fa_bwd_f16_b4_h32_s4096_d128_noncausal",
             "value": round(bw_tf, 2), "unit": "TFLOP/s", "ms_per_step": round(bw_ms, 4),
             "frac_of_mfma_peak": round(bw_tf / MFMA_PEAK_TFLOPS, 4),
             "flops": "10*B*H*S^2*D"}
+    # PyTorch's flash-attention backward op on the same inputs, for scale
+    # (its forward run once outside the timed region, as here).
+    try:
+        fa = torch.ops.aten._scaled_dot_product_flash_attention(q, k, v, 0.0, False, False)
+        t_out, t_lse, cq, ck, mq, mk, seed, offset = fa[:8]
+        vms = time_launches(
+            lambda: torch.ops.aten._scaled_dot_product_flash_attention_backward(
+                do, q, k, v, t_out, t_lse, cq, ck, mq, mk, 0.0, False, seed, offset),
+            10, 3, torch)
+        line["torch_sdpa_flash_bwd_value"] = round(10.0 * B * H * S * S * D / (vms * 1e-3) / 1e12,
+                                                   2)
+        log(f"vendor: torch flash-attention backward op f16 B4 H32 S4096: "
+            f"{line['torch_sdpa_flash_bwd_value']:.1f} TFLOP/s")
+    except (RuntimeError, TypeError, AttributeError) as e:
+        log(f"vendor: torch flash-attention backward unavailable ({type(e).__name__})")
+    return line
 
 
 def config_lines(wave, torch, dev, steps, warmup):
@@ -386,8 +402,13 @@ def config_lines(wave, torch, dev, steps, warmup):
                          "frac_of_mfma_peak": round(atf / MFMA_PEAK_TFLOPS, 4),
                          "kernel": "wave_gemm_auto_launch (Stream-K, min(2*tiles, CUs) workers)",
                          "tiled_kernel_value": round(tf, 2)})
+        # The vendor library on the same inputs and output, for scale (not
+        # this build's code): hipBLASLt through torch.matmul, C = A . B^T.
+        vms = time_launches(lambda: torch.matmul(a, b.t(), out=c), steps, warmup, torch)
+        line["hipblaslt_value"] = round(fl / (vms * 1e-3) / 1e12, 2)
         log(f"config {name} gemm bf16 {M}x{N}x{K}: {line['ms_per_step'] * 1e3:.1f} us/launch, "
-            f"{line['value']:.1f} TFLOP/s" + (f", {line['gbps']:.0f} GB/s" if "gbps" in line else ""))
+            f"{line['value']:.1f} TFLOP/s" + (f", {line['gbps']:.0f} GB/s" if "gbps" in line else "")
+            + f" (hipBLASLt {line['hipblaslt_value']:.1f})")
         lines.append(line)
         del a, b, c
 
@@ -401,11 +422,29 @@ def config_lines(wave, torch, dev, steps, warmup):
     tf = 2.0 * B * Hq * S * S * D / (ms * 1e-3) / 1e12
     log(f"config 5 fa fwd causal GQA bf16 B1 Hq64 Hkv8 S8192: {ms * 1e3:.1f} us/launch, "
         f"{tf:.1f} TFLOP/s (causal FLOPs)")
-    lines.append({"workload": "fa_fwd_bf16_b1_hq64_hkv8_s8192_d128_causal_config5",
-                  "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
-                  "frac_of_mfma_peak": round(tf / MFMA_PEAK_TFLOPS, 4),
-                  "flops": "2*B*Hq*S^2*D (the keys a causal row attends to; the reference's "
-                           "4*B*H*S^2*D non-causal count would double it)"})
+    line5 = {"workload": "fa_fwd_bf16_b1_hq64_hkv8_s8192_d128_causal_config5",
+             "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+             "frac_of_mfma_peak": round(tf / MFMA_PEAK_TFLOPS, 4),
+             "flops": "2*B*Hq*S^2*D (the keys a causal row attends to; the reference's "
+                      "4*B*H*S^2*D non-causal count would double it)"}
+    # PyTorch's SDPA flash backend on the same inputs, for scale: K and V
+    # expanded to the 64 query heads (the flash backend is forced, so nothing
+    # falls back to batched matmuls).
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        ke = k.repeat_interleave(Hq // Hkv, dim=1).contiguous()
+        ve = v.repeat_interleave(Hq // Hkv, dim=1).contiguous()
+        with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+            vms = time_launches(
+                lambda: torch.nn.functional.scaled_dot_product_attention(q, ke, ve, is_causal=True),
+                10, 3, torch)
+        line5["torch_sdpa_flash_value"] = round(2.0 * B * Hq * S * S * D / (vms * 1e-3) / 1e12, 2)
+        log(f"vendor: torch SDPA flash causal bf16 B1 H64 S8192 (K, V expanded): "
+            f"{line5['torch_sdpa_flash_value']:.1f} TFLOP/s")
+        del ke, ve
+    except (RuntimeError, ImportError) as e:
+        log(f"vendor: torch SDPA flash unavailable for config 5 ({type(e).__name__})")
+    lines.append(line5)
     del q, k, v, o
     return lines
 
