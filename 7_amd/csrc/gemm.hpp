@@ -46,8 +46,10 @@ hipError_t launch_skinny(const GemmArgs &args, hipStream_t stream);
 // Split-K short-M kernel (gemm_skinny.hip): `bn`-column CTAs over
 // `splits` K ranges, fp32 partials in `slots` (skinny_split_slot_bytes)
 // reduced in the launch by each column block's last arriver, through
-// `counters` (skinny_split_counter_count u32s, zero before the launch and
-// left zero).  skinny_split_plan: the plan for the shape on `cus` CUs,
+// `counters` (skinny_split_counter_count 64-bit words, 8-byte aligned, any
+// contents before the launch: a word counts only under the launch's
+// nonzero `epoch`; left zero).  skinny_split_plan: the plan for the shape
+// on `cus` CUs,
 // splits == 0 when the shape takes the unsplit kernel (pointers and C's
 // leading dimension are checked by skinny_supported).
 struct SplitPlan {
@@ -58,7 +60,8 @@ SplitPlan skinny_split_plan(int M, int N, int K, int cus);
 size_t skinny_split_slot_bytes(int N, const SplitPlan &plan);
 size_t skinny_split_counter_count(int N, const SplitPlan &plan);
 hipError_t launch_skinny_split(const GemmArgs &args, const SplitPlan &plan, float *slots,
-                               uint32_t *counters, hipStream_t stream);
+                               unsigned long long *counters, uint32_t epoch,
+                               hipStream_t stream);
 
 } // namespace gemm
 } // namespace wave

@@ -183,10 +183,38 @@ hipError_t launch_out(const SkinnyParams &p, bool cm, hipStream_t s) {
 // release or acquire: the data never sits in a non-coherent cache), sums
 // them in split order (its own from its accumulators),
 // s = ((p_0 + p_1) + p_2) + p_3, so the result does not depend on arrival
-// order, stores C, and resets both counters to zero for the next launch.
+// order, stores C, and resets both counters to zero.
 // Splits of a tile take consecutive CTA numbers after the XCD renumbering
 // (workgroup i runs on XCD i % 8), so they run on one XCD.
+//
+// Counter words are 64-bit: the launch's epoch (nonzero, from the host) in
+// the high half, a count in the low half, and a word that carries any
+// other epoch counts as zero.  So a workspace needs no clearing before a
+// launch -- neither a fresh one nor one another launch left (which leaves
+// zeros) -- and the launch is one kernel, not a fill kernel and this one
+// (the fill and its kernel boundary cost 4-5 us at 128 x 8192 x 8192).
+// The reset to zero keeps replays of a captured launch, whose epoch is
+// fixed, correct.
 constexpr int kXMaxSplits = 4;
+
+typedef unsigned long long u64;
+__device__ __forceinline__ uint32_t epoch_count(u64 w, uint32_t epoch) {
+  return (uint32_t)(w >> 32) == epoch ? (uint32_t)w : 0u;
+}
+// Counts one arrival on *c for this launch and returns the count before it.
+// The first guess is the zero every launch leaves, so the common first
+// arrival takes one atomic round trip; each failed exchange means another
+// contributor's succeeded (at most splits - 1) or the word was stale.
+__device__ __forceinline__ uint32_t epoch_increment(u64 *c, uint32_t epoch) {
+  u64 old = 0;
+  for (;;) {
+    const uint32_t n = epoch_count(old, epoch);
+    if (__hip_atomic_compare_exchange_strong(c, &old, ((u64)epoch << 32) | (n + 1u),
+                                             __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT))
+      return n;
+  }
+}
 
 template <int BN> struct SplitCfg {
   static_assert(BN == 128 || BN == 64, "column block");
@@ -205,8 +233,9 @@ struct SplitParams {
   const uint16_t *A, *B;
   void *C;
   float *slots;         // [tiles * splits][128 * BN]
-  uint32_t *counters;   // [tiles][2] arrived, published; zero between launches
+  unsigned long long *counters;  // [tiles][2] arrived, published (epoch << 32 | count)
   int M, N, K, ldc, splits;
+  uint32_t epoch;       // nonzero; the tag of this launch's counts
 };
 
 template <int IN_DT, int OUT_DT, bool COL_MAJOR, int BN>
@@ -332,8 +361,7 @@ __global__ __launch_bounds__(256, 1) void skinny_split_kernel(SplitParams p) {
     // its K range reduces and never publishes its own partial; the others
     // publish and then count themselves published with a release.
     if (threadIdx.x == 0)
-      arrival = __hip_atomic_fetch_add(&p.counters[2 * tile], 1u, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+      arrival = epoch_increment(&p.counters[2 * tile], p.epoch);
     __syncthreads();
     if (arrival != (uint32_t)p.splits - 1) {
       // Device-scope (sc1) stores: written through to the device's
@@ -349,21 +377,20 @@ __global__ __launch_bounds__(256, 1) void skinny_split_kernel(SplitParams p) {
       // the reader's device-coherent loads below find them there.
       vm_wait_barrier();
       if (threadIdx.x == 0)
-        __hip_atomic_fetch_add(&p.counters[2 * tile + 1], 1u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+        epoch_increment(&p.counters[2 * tile + 1], p.epoch);
       return;
     }
     // Last arriver: every other contributor has taken its ticket, so it is
     // resident and finishes its publish without waiting on anything; the
     // wait below ends once the last of them has.  Both counters then go
-    // back to zero for the next launch (ordered after this one by the
-    // kernel boundary; no contributor touches them again in this one).
+    // back to zero (no contributor touches them again in this launch).
     if (threadIdx.x == 0) {
-      while (__hip_atomic_load(&p.counters[2 * tile + 1], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT) != (uint32_t)p.splits - 1)
+      while (epoch_count(__hip_atomic_load(&p.counters[2 * tile + 1], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT),
+                         p.epoch) != (uint32_t)p.splits - 1)
         __builtin_amdgcn_s_sleep(1);
-      __hip_atomic_store(&p.counters[2 * tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&p.counters[2 * tile + 1], 0u, __ATOMIC_RELAXED,
+      __hip_atomic_store(&p.counters[2 * tile], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&p.counters[2 * tile + 1], 0ull, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
@@ -539,12 +566,13 @@ size_t skinny_split_counter_count(int N, const SplitPlan &plan) {
 }
 
 hipError_t launch_skinny_split(const GemmArgs &g, const SplitPlan &plan, float *slots,
-                               uint32_t *counters, hipStream_t s) {
+                               unsigned long long *counters, uint32_t epoch, hipStream_t s) {
   if (plan.splits < 1 || plan.splits > kXMaxSplits || g.K / kBK < plan.splits ||
-      (plan.bn != 128 && plan.bn != 64))
+      (plan.bn != 128 && plan.bn != 64) || epoch == 0)
     return hipErrorInvalidValue;
   SplitParams p{static_cast<const uint16_t *>(g.A), static_cast<const uint16_t *>(g.B),
-                g.C, slots, counters, g.M, g.N, g.K, g.col_major ? g.M : g.N, plan.splits};
+                g.C, slots, counters, g.M, g.N, g.K, g.col_major ? g.M : g.N, plan.splits,
+                epoch};
   const bool cm = g.col_major;
   const int bn = plan.bn;
   if (g.in_dtype == kF16) {

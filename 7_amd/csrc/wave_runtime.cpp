@@ -9,6 +9,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+#include <chrono>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -420,6 +422,19 @@ int wave_gemm_streamk_noalloc_launch(const void *A, const void *B, void *C, int 
                                   counters, workers, stream);
 }
 
+// Launch epochs for counters that carry their launch's tag (the split-K
+// short-M kernel): process-wide, never 0, and started from the clock, so
+// that a workspace another process left behind is unlikely to hold one.
+static uint32_t next_epoch() {
+  static std::atomic<uint32_t> epoch{
+      (uint32_t)std::chrono::steady_clock::now().time_since_epoch().count()};
+  uint32_t e;
+  do
+    e = epoch.fetch_add(1u, std::memory_order_relaxed) + 1u;
+  while (e == 0u);
+  return e;
+}
+
 int wave_gemm_auto_workspace_bytes(int M, int N, int K, size_t *bytes) {
   if (!bytes)
     return fail(WAVE_ERR_INVALID, "gemm auto: null size output");
@@ -434,7 +449,7 @@ int wave_gemm_auto_workspace_bytes(int M, int N, int K, size_t *bytes) {
   *bytes = 0;
   if (plan.splits > 0)
     *bytes = wave::gemm::skinny_split_slot_bytes(N, plan) +
-             wave::gemm::skinny_split_counter_count(N, plan) * sizeof(uint32_t);
+             wave::gemm::skinny_split_counter_count(N, plan) * sizeof(uint64_t);
   if (workers > 0) {
     size_t scratch = 0, counters = 0;
     st = streamk_sizes(M, N, workers, &scratch, &counters);
@@ -476,17 +491,15 @@ int wave_gemm_auto_launch(const void *A, const void *B, void *C, int M, int N, i
     g.in_dtype = in_dtype;
     g.out_dtype = out_dtype;
     g.col_major = c_layout == WAVE_COL_MAJOR;
-    if (!workspace || workspace_bytes < slot_bytes + count * sizeof(uint32_t) ||
+    if (!workspace || workspace_bytes < slot_bytes + count * sizeof(uint64_t) ||
         !wave::gemm::skinny_supported(g))
       return wave_gemm_launch(A, B, C, M, N, K, in_dtype, out_dtype, c_layout, stream);
     float *slots = static_cast<float *>(workspace);
-    uint32_t *counters = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + slot_bytes);
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    st = hip_status(wave::gemm::zero_counters(counters, count, s),
-                    "wave_gemm_auto_launch: counter reset");
-    if (st != WAVE_OK)
-      return st;
-    return hip_status(wave::gemm::launch_skinny_split(g, plan, slots, counters, s),
+    auto *counters = reinterpret_cast<unsigned long long *>(static_cast<char *>(workspace) +
+                                                            slot_bytes);
+    // No counter fill: the kernel's counts carry this launch's epoch.
+    return hip_status(wave::gemm::launch_skinny_split(g, plan, slots, counters, next_epoch(),
+                                                      static_cast<hipStream_t>(stream)),
                       "wave_gemm_auto_launch (split-K short-M)");
   }
   const int workers = auto_workers(M, N, K, cus);

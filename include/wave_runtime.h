@@ -155,8 +155,10 @@ int wave_gemm_streamk_counters_check(const uint32_t *counters, int M, int N,
  * and the split short-M kernel take their workspace from `workspace`
  * (caller-owned, 16-byte aligned device memory of
  * wave_gemm_auto_workspace_bytes(M, N, K) bytes, 0 when the shape takes an
- * unsplit path; no initialisation needed, each launch zeroes the counters
- * it uses with a fill kernel); with a smaller workspace the unsplit kernel
+ * unsplit path; no initialisation needed: a Stream-K launch zeroes the
+ * counters it uses with a fill kernel, and the split short-M kernel's
+ * counters carry a per-launch tag, so whatever they hold counts as zero,
+ * and it leaves them zero); with a smaller workspace the unsplit kernel
  * runs.  One launch in flight per workspace.  Same C as wave_gemm_launch
  * (c_layout row- or column-major). */
 int wave_gemm_auto_workspace_bytes(int M, int N, int K, size_t *bytes);

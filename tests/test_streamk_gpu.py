@@ -186,9 +186,9 @@ def device_cus(dev):
 
 def expected_workspace(wave, M, N, K, dev):
     bn, s = short_m_plan(M, N, K, device_cus(dev))
-    if s:
+    if s:  # fp32 partial slots, then two 64-bit counters a column block
         tiles = -(-N // bn)
-        return 0, tiles * s * 128 * bn * 4 + tiles * 8
+        return 0, tiles * s * 128 * bn * 4 + tiles * 16
     w = auto_workers(M, N, K, device_cus(dev))
     if w == 0:
         return 0, 0
@@ -390,6 +390,50 @@ def test_split_short_m_alternating_inputs(wave, oracle, dev, shape):
         wave.gemm_auto(A, Bs[i & 1], out_dtype=torch.bfloat16, workspace=ws, out=out)
         torch.cuda.synchronize()
         assert torch.equal(out, refs[i & 1]), i
+
+
+def test_split_short_m_graph_replays(wave, oracle, dev):
+    """A captured split short-M launch replays with one fixed counter epoch:
+    each replay equals wave_gemm_launch's output, with eager launches for
+    another B on the same workspace between the replays (every launch leaves
+    the counters at zero, and a word of another epoch counts as zero).  On
+    256 CUs: 64-column blocks in 3 K splits."""
+    M, N, K = 100, 5000, 12288
+    bn, s = short_m_plan(M, N, K, device_cus(dev))
+    if not s:
+        pytest.skip("this device's CU count takes the unsplit kernel at this shape")
+    need = wave.gemm_auto_workspace_bytes(M, N, K)
+    a = oracle.gemm_inputs(M, K, 2, 11, 0)
+    b0 = oracle.gemm_inputs(N, K, 2, 11, 1)
+    b1 = oracle.gemm_inputs(N, K, 2, 11, 2)
+    A = to_dev(a, torch.bfloat16, dev)
+    B0, B1 = to_dev(b0, torch.bfloat16, dev), to_dev(b1, torch.bfloat16, dev)
+    ref0 = wave.gemm(A, B0, out_dtype=torch.bfloat16)
+    ref1 = wave.gemm(A, B1, out_dtype=torch.bfloat16)
+    assert not torch.equal(ref0, ref1)
+    ws = torch.full((need,), 0xFF, dtype=torch.uint8, device=dev)
+    out = torch.empty_like(ref0)
+    wave.gemm_auto(A, B0, out_dtype=torch.bfloat16, workspace=ws, out=out)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref0)
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        graph.capture_begin()
+        wave.gemm_auto(A, B0, out_dtype=torch.bfloat16, workspace=ws, out=out)
+        graph.capture_end()
+    torch.cuda.current_stream().wait_stream(stream)
+    other = torch.empty_like(ref1)
+    for i in range(4):
+        out.zero_()
+        wave.gemm_auto(A, B1, out_dtype=torch.bfloat16, workspace=ws, out=other)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref0), i
+        assert torch.equal(other, ref1), i
+    tiles = -(-N // bn)
+    assert int(ws[tiles * s * 128 * bn * 4:].count_nonzero()) == 0
 
 
 def test_split_short_m_float_inputs_same_bits(wave, oracle, dev):
