@@ -383,11 +383,18 @@ __global__ __launch_bounds__(256, 1) void skinny_split_kernel(SplitParams p) {
     // Last arriver: every other contributor has taken its ticket, so it is
     // resident and finishes its publish without waiting on anything; the
     // wait below ends once the last of them has.  Both counters then go
-    // back to zero (no contributor touches them again in this launch).
+    // back to zero (no contributor touches them again in this launch).  The
+    // wait is bounded (2^20 polls, about a second): only a counter word that
+    // already held this launch's epoch before it started (a chance of about
+    // 2^-32 a word for arbitrary contents) could keep it from ending, and
+    // then the launch still finishes.
     if (threadIdx.x == 0) {
-      while (epoch_count(__hip_atomic_load(&p.counters[2 * tile + 1], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT),
-                         p.epoch) != (uint32_t)p.splits - 1)
+      for (uint32_t poll = 0;
+           poll < (1u << 20) &&
+           epoch_count(__hip_atomic_load(&p.counters[2 * tile + 1], __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT),
+                       p.epoch) != (uint32_t)p.splits - 1;
+           ++poll)
         __builtin_amdgcn_s_sleep(1);
       __hip_atomic_store(&p.counters[2 * tile], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(&p.counters[2 * tile + 1], 0ull, __ATOMIC_RELAXED,
