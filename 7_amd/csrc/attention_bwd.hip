@@ -167,6 +167,43 @@ __device__ __forceinline__ void mma_grad(f32x16 (&acc)[2 * NT], const uint8_t *c
   }
 }
 
+// One gradient product over K = 64 (4 slices) for 64 rows: acc[2a + t] +=
+// A[32a .. 32a+31] . R[:, c_t .. c_t + 31] (a, t = 0, 1), A a 128-byte-row
+// LDS tile (rows r and r + 32 share swz<128>), R a row-major [64][128] tile
+// read transposed.  Per slice two A and two B fragments feed four MFMAs:
+// 1 KiB of LDS reads an MFMA, against 1.5 KiB for mma_grad's two products
+// of 32 rows each (whose A fragment feeds two MFMAs but each B one).  The
+// fragments of slice kk + GPF are read before the MFMAs of slice kk.
+template <int DT, int GPF = 1>
+__device__ __forceinline__ void mma_grad_rows2(f32x16 (&acc)[4], const uint8_t *A,
+                                               const uint8_t *R, uint32_t c0, uint32_t c1) {
+  const uint32_t lane = threadIdx.x & 63, ra = lane & 31;
+  const uint32_t sw = (lane >> 5) ^ swz<128>(ra);
+  constexpr int NB = GPF + 1;
+  u32x4 fa[NB][2], fb[NB][2];
+  auto load = [&](int kk, int slot) {
+    const uint32_t cb = ((2u * kk) ^ sw) << 4;
+    fa[slot][0] = *reinterpret_cast<const u32x4 *>(A + ra * 128 + cb);
+    fa[slot][1] = *reinterpret_cast<const u32x4 *>(A + (ra + 32) * 128 + cb);
+    fb[slot][0] = tr_frag(lds_addr(R), kk, c0);
+    fb[slot][1] = tr_frag(lds_addr(R), kk, c1);
+  };
+#pragma unroll
+  for (int kk = 0; kk < GPF && kk < 4; ++kk)
+    load(kk, kk % NB);
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    if (kk + GPF < 4)
+      load(kk + GPF, (kk + GPF) % NB);
+    const int sl = kk % NB;
+    acc[0] = mfma32x32x16<DT>(fa[sl][0], fb[sl][0], acc[0]);
+    acc[1] = mfma32x32x16<DT>(fa[sl][0], fb[sl][1], acc[1]);
+    acc[2] = mfma32x32x16<DT>(fa[sl][1], fb[sl][0], acc[2]);
+    acc[3] = mfma32x32x16<DT>(fa[sl][1], fb[sl][1], acc[3]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // MFMA fragments of 32 rows of a [rows][128] global block (row0 = the
 // lane's row): lane l holds elements 16 kk + 8 (l / 32) .. +8 for kk < 8.
 __device__ __forceinline__ void load_frags(const uint16_t *row, u32x4 (&f)[8]) {
@@ -379,11 +416,13 @@ __global__ __launch_bounds__(256, 2) void bwd_kv_kernel(BwdParams p) {
 // products of those tiles with Q / dO of item i (transposing reads).  Every
 // segment ends with a workgroup barrier (2 * items + 2 of them for every
 // wave).  Buffers: item i's Q / dO sit in ring slot i % 3, read from
-// segment 2i (group 0's M1(i)) to 2i+3 (group 1's M2(i)); all waves issue
-// the DMA of item j+1 at the start of segment 2j, after slot (j+1) % 3's
-// previous item (j-2) was last read in segment 2j-1, and wait for it at the
-// end of segment 2j+1.  A group's P^T / dS^T are written in SM(i) and read
-// in M2(i), the next segment of that group.
+// segment 2i (group 0's M1(i)) to 2i+3 (group 1's M2(i)); group 1's waves
+// issue the DMA of item j+1 at the start of segment 2j (their SM(j-1),
+// shorter than group 0's matrix segment beside it, which the DMA issues
+// used to lengthen: 4-5 % of the kernel's time), after slot (j+1) % 3's
+// previous item (j-2) was last read in segment 2j-1, and every wave waits
+// for it at the end of segment 2j+1.  A group's P^T / dS^T are written in
+// SM(i) and read in M2(i), the next segment of that group.
 #ifndef WAVE_BWD_PF
 #define WAVE_BWD_PF 3  // score products: A fragments read this many slices ahead
 #endif
@@ -408,7 +447,10 @@ __global__ __launch_bounds__(512, 1) void bwd_kv_pp_kernel(BwdParams p) {
   uint8_t *sPt = smem + 3 * kQD + grp * 2 * kNarrowS, *sdSt = sPt + kNarrowS;
   const uint32_t lds0 = lds_addr(smem);
   // Wave roles within the group, as in bwd_kv_kernel.
-  const int qh2 = wg & 1, kh2 = wg >> 1, kh = wg & 1, dq = wg >> 1;
+  // Score products: query half qh2, key half kh2.  Gradient products: wave
+  // role 0 accumulates dV, role 1 dK, each for all 64 keys of the group and
+  // d columns 64 dq .. 64 dq + 63.
+  const int qh2 = wg & 1, kh2 = wg >> 1, role = wg & 1, dq = wg >> 1;
   u32x4 kf[8], vf[8];
   load_frags(p.K + kv_off + (size_t)(kh2 * 32 + (lane & 31)) * kBD, kf);
   load_frags(p.V + kv_off + (size_t)(kh2 * 32 + (lane & 31)) * kBD, vf);
@@ -429,22 +471,23 @@ __global__ __launch_bounds__(512, 1) void bwd_kv_pp_kernel(BwdParams p) {
   auto rows_of = [&](const Cursor &c) {
     return ((size_t)b * p.q_heads + (size_t)hkv * group + c.h) * p.seq + (size_t)c.qb * kBlk;
   };
-  // DMA of an item into ring slot `slot`: wave w fills Q and dO rows
-  // 8w .. 8w+7 (two 1 KiB windows each), lane l row 4j + l / 16, slot l % 16,
-  // which holds chunk (l % 16) ^ swz(row); waves 0 and 1 add the rows' lse
-  // and -delta (256 B each, 4 bytes a lane).
+  // DMA of an item into ring slot `slot`, issued by group 1's waves: wave
+  // wg fills Q and dO rows 16 wg .. 16 wg + 15 (four 1 KiB windows each),
+  // lane l row 4 win + l / 16, slot l % 16, which holds chunk (l % 16) ^
+  // swz(row); waves wg = 0 and 1 add the rows' lse and -delta (256 B each,
+  // 4 bytes a lane).
   auto dma_item = [&](const Cursor &c, uint32_t slot) {
     const size_t rb = rows_of(c);
     const uint32_t l = lds0 + slot * kQD;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const uint32_t win = 2 * wave + j, r = 4 * win + (lane >> 4);
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t win = 4 * wg + j, r = 4 * win + (lane >> 4);
       const uint32_t off = r * 256 + (((lane & 15) ^ swz<256>(r)) << 4);
       dma16(l + win * 1024, p.Q + rb * kBD, off);
       dma16(l + kWide + win * 1024, p.dO + rb * kBD, off);
     }
-    if (wave < 2)
-      dma4(l + kStats + wave * 256, wave == 0 ? (const void *)(p.lse + rb) : (const void *)(p.delta + rb),
+    if (wg < 2)
+      dma4(l + kStats + wg * 256, wg == 0 ? (const void *)(p.lse + rb) : (const void *)(p.delta + rb),
            4 * lane);
   };
   f32x16 s, dp;
@@ -464,13 +507,15 @@ __global__ __launch_bounds__(512, 1) void bwd_kv_pp_kernel(BwdParams p) {
     }
   };
   Cursor dmac{0, qb0}, cur{0, qb0};
-  dma_item(dmac, 0);
+  if (grp == 1)
+    dma_item(dmac, 0);
   advance(dmac);
   vm_wait_barrier();
   const int nseg = 2 * items + 2;
   for (int sg = 0; sg < nseg; ++sg) {
     if ((sg & 1) == 0 && (sg >> 1) + 1 < items) {
-      dma_item(dmac, (uint32_t)(((sg >> 1) + 1) % 3));
+      if (grp == 1)
+        dma_item(dmac, (uint32_t)(((sg >> 1) + 1) % 3));
       advance(dmac);
     }
     const int ls = sg - (int)grp;
@@ -479,9 +524,9 @@ __global__ __launch_bounds__(512, 1) void bwd_kv_pp_kernel(BwdParams p) {
       if ((ls & 1) == 0) {
         if (i >= 1) {  // M2(i-1)
           const uint8_t *q = smem + ((i - 1) % 3) * kQD;
-          const uint8_t *const ga[2] = {sPt, sdSt};
-          const uint8_t *const gr[2] = {q + kWide, q};
-          mma_grad<DT, 2, WAVE_BWD_GPF>(g, ga, kh * 32, gr, (2 * dq) * 32, (2 * dq + 1) * 32);
+          // dV += P^T dO, dK += dS^T Q (scaled at the store).
+          mma_grad_rows2<DT, WAVE_BWD_GPF>(g, role ? sdSt : sPt, role ? q : q + kWide,
+                                           (2 * dq) * 32, (2 * dq + 1) * 32);
         }
         if (i < items) {  // M1(i): S starts at -lse / scale, dP at -delta
           const uint8_t *q = smem + (i % 3) * kQD;
@@ -520,12 +565,13 @@ __global__ __launch_bounds__(512, 1) void bwd_kv_pp_kernel(BwdParams p) {
     else
       lds_barrier();
   }
-  uint16_t *dK = p.dK + kv_off, *dV = p.dV + kv_off;
+  uint16_t *dst = (role ? p.dK : p.dV) + kv_off;
+  const float sc = role ? p.scale : 1.f;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    store_tile32<DT>(dV, kh * 32, (2 * dq + t) * 32, g[t], 1.f);
-    store_tile32<DT>(dK, kh * 32, (2 * dq + t) * 32, g[2 + t], p.scale);
-  }
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      store_tile32<DT>(dst, a * 32, (2 * dq + t) * 32, g[2 * a + t], sc);
 }
 
 // dQ of one 64-query block of one q head.
