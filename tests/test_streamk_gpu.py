@@ -436,6 +436,33 @@ def test_split_short_m_graph_replays(wave, oracle, dev):
     assert int(ws[tiles * s * 128 * bn * 4:].count_nonzero()) == 0
 
 
+def test_split_short_m_shared_workspace_two_shapes(wave, oracle, dev):
+    """One workspace alternated between two split shapes whose layouts
+    overlap: on 256 CUs the counters of 100 x 5000 x 12288 (3 splits) sit
+    inside the fp32 partial slots of 128 x 8192 x 8192 (2 splits), so its
+    launches find their counter words holding partial sums the other shape
+    left there.  A word carrying another launch's epoch counts as zero, so
+    every output equals wave_gemm_launch's, bit for bit (bucket inputs)."""
+    cus = device_cus(dev)
+    shapes = [(128, 8192, 8192), (100, 5000, 12288)]
+    plans = [short_m_plan(M, N, K, cus) for M, N, K in shapes]
+    if not all(s for _, s in plans):
+        pytest.skip("this device's CU count takes the unsplit kernel for one of the shapes")
+    need = max(wave.gemm_auto_workspace_bytes(*sh) for sh in shapes)
+    ws = torch.zeros((need,), dtype=torch.uint8, device=dev)
+    cases = []
+    for i, (M, N, K) in enumerate(shapes):
+        a = oracle.gemm_inputs(M, K, 2, 13 + i, 0)
+        b = oracle.gemm_inputs(N, K, 2, 13 + i, 1)
+        A, B = to_dev(a, torch.bfloat16, dev), to_dev(b, torch.bfloat16, dev)
+        cases.append((A, B, wave.gemm(A, B, out_dtype=torch.bfloat16)))
+    for it in range(6):
+        for j, (A, B, ref) in enumerate(cases):
+            got = wave.gemm_auto(A, B, out_dtype=torch.bfloat16, workspace=ws)
+            torch.cuda.synchronize()
+            assert torch.equal(got, ref), (it, j)
+
+
 def test_split_short_m_float_inputs_same_bits(wave, oracle, dev):
     """Inexact inputs, fp32 C: the last arriver sums the partials in split
     order whichever arrives last, so every launch gives the same bits, within
